@@ -1,0 +1,16 @@
+"""Shared pytest setup: the `gpu` marker and import paths.
+
+Tests marked `gpu` need a real MI355X and the built HIP library; everything
+else runs on the CPU (oracle known answers, host logic, C-ABI exports).
+"""
+import os
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+for p in (ROOT, os.path.join(ROOT, "orda-cutile-rs_amd"), os.path.join(ROOT, "oracle")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X GPU and the built HIP library")
