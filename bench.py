@@ -1,0 +1,262 @@
+#!/usr/bin/env python3
+"""Throughput of the fused CE + forward-KL distillation loss (fwd+bwd) on one
+MI355X.
+
+A step is one `distillation_loss` call over device-resident synthetic inputs:
+logits GEMMs, fused row pass, grad_hidden and grad_W GEMMs, deferred mean,
+INT8 round trip of grad_W, loss assembly. Default workload: Tied teacher,
+BT=8192, H=4096, V=131072, bf16 inputs with fp32 accumulation, kd=0.4,
+T=1.5, label smoothing 0.1, INT8 grad_W (16 chunks x 512 rows).
+
+Prints one JSON line (see the repository's benchmark contract) with the
+per-kernel roofline of the dominant kernel measured with HIP events on the
+stream the kernels run on, and the CPU oracle timed on a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "orda-cutile-rs_amd"))
+
+PEAK_HBM_GBS = 8000.0           # MI355X HBM3E, GB/s
+PEAK_MFMA_TFLOPS = {"bf16": 2500.0, "f32": 157.3}   # dense
+
+WORKLOADS = {
+    # name: (teacher, BT, H, Ht, V, dtype, kd, T, alpha, w_t, quant)
+    "tied-8192x4096x131072-bf16-int8": ("tied", 8192, 4096, 4096, 131072, "bf16", 0.4, 1.5, 0.1,
+                                        None, True),
+    "tied-2048x4096x32000-f32": ("tied", 2048, 4096, 4096, 32000, "f32", 0.4, 1.5, 0.0, None,
+                                 False),
+    "separate-4096x2048x4096x32000-f32": ("separate", 4096, 2048, 4096, 32000, "f32", 0.5, 2.0,
+                                          0.1, 1.0, False),
+    "precomputed-4096x4096x65536-f32": ("precomputed", 4096, 4096, 4096, 65536, "f32", 0.7, 1.0,
+                                        0.0, None, False),
+    "tied-256x512x8192-f32": ("tied", 256, 512, 512, 8192, "f32", 0.4, 1.5, 0.0, None, False),
+}
+DEFAULT = "tied-8192x4096x131072-bf16-int8"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def make_inputs(torch, wl, dev, seed=0):
+    teacher, bt, h, ht, v, dt, *_ = wl
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+
+    def normal(shape, std):
+        x = torch.empty(shape, device=dev, dtype=torch.float32)
+        x.normal_(0.0, std, generator=g)
+        return x.to(tdt)
+    s = normal((bt, h), 1.0)
+    w = normal((v, h), 0.02)
+    y = torch.randint(0, v, (bt,), device=dev, generator=g, dtype=torch.int64)
+    if teacher == "tied":
+        t = ("tied", normal((bt, h), 1.0))
+    elif teacher == "separate":
+        t = ("separate", normal((bt, ht), 1.0), normal((v, ht), 0.015))
+    else:
+        lg = torch.empty((bt, v), device=dev, dtype=torch.float32)
+        lg.normal_(0.0, 2.0, generator=g)
+        lg[torch.arange(bt, device=dev), y] += 8.0
+        t = ("precomputed", lg)
+    return s, w, y, t
+
+
+def teacher_obj(H, t):
+    if t[0] == "tied":
+        return H.Teacher.Tied(t[1])
+    if t[0] == "separate":
+        return H.Teacher.Separate(t[1], t[2])
+    return H.Teacher.Precomputed(t[1])
+
+
+def options(H, wl):
+    _, _, _, _, _, _, kd, T, alpha, w_t, quant = wl
+    return H.LossOptions(kd_weight=kd, temperature=T, label_smoothing=alpha,
+                         teacher_ce_weight=w_t,
+                         config=H.KernelConfig(quantize_grad_weight=quant))
+
+
+def work_per_step(wl, plan):
+    """Algorithmic flops (GEMMs) and bytes (row pass, quant) of one step."""
+    teacher, bt, h, ht, v, dt, kd, T, alpha, w_t, quant = wl
+    es = 2 if dt == "bf16" else 4
+    wt = w_t if w_t is not None else (1.0 if teacher == "tied" else 0.0)
+    hs = h
+    if teacher == "tied":
+        fwd = 2 * (2 * bt) * h * v
+        back_rows = 2 * bt if wt > 0 else bt
+        dgrad = 2 * back_rows * v * h
+        wgrad = 2 * back_rows * v * h
+        t_rows_written = bt if wt > 0 else 0
+    elif teacher == "separate":
+        fwd = 2 * bt * v * (hs + ht)
+        dgrad = 2 * bt * v * hs + (2 * bt * v * ht if wt > 0 else 0)
+        wgrad = dgrad
+        t_rows_written = bt if wt > 0 else 0
+    else:
+        fwd = 2 * bt * h * v
+        dgrad = 2 * bt * v * h
+        wgrad = dgrad
+        t_rows_written = 0
+    # row pass: read student + teacher logits once, write the gradient rows
+    rows_read = 2 * bt
+    rowpass = (rows_read + bt + t_rows_written) * v * es
+    quant_b = v * h * 8 if quant else 0
+    return {"gemm_logits": ("mfma", fwd), "gemm_grad_hidden": ("mfma", dgrad),
+            "gemm_grad_weight": ("mfma", wgrad), "row_pass": ("hbm", rowpass),
+            "quant": ("hbm", quant_b)}
+
+
+def cpu_baseline(wl, budget_rows=(2, 6)):
+    """The CPU oracle (single thread) on two small samples of the same
+    workload; per-row and per-call costs are separated from the two timings
+    and extrapolated to the full BT and chunk count."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle as O
+    import orda_hip as H
+    teacher, bt, h, ht, v, dt, kd, T, alpha, w_t, quant = wl
+    rng = np.random.default_rng(0)
+
+    def mk(n):
+        s = rng.standard_normal((n, h), dtype=np.float32)
+        w = (rng.standard_normal((v, h), dtype=np.float32) * 0.02).astype(np.float32)
+        y = rng.integers(0, v, n)
+        if teacher == "tied":
+            t = H.Teacher.Tied(rng.standard_normal((n, h), dtype=np.float32))
+        elif teacher == "separate":
+            t = H.Teacher.Separate(rng.standard_normal((n, ht), dtype=np.float32),
+                                   (rng.standard_normal((v, ht), dtype=np.float32) * 0.015))
+        else:
+            t = H.Teacher.Precomputed(rng.standard_normal((n, v), dtype=np.float32) * 2)
+        return s, w, y, t
+    times = []
+    opts = options(H, wl)
+    for n in budget_rows:
+        s, w, y, t = mk(n)
+        t0 = time.perf_counter()
+        O.distillation_loss(s, w, y, t, opts)
+        times.append(time.perf_counter() - t0)
+        log(f"cpu oracle sample BT={n}: {times[-1]:.2f} s")
+    (n1, n2), (t1, t2) = budget_rows, times
+    per_row = max((t2 - t1) / (n2 - n1), 1e-9)
+    fixed = max(t1 - n1 * per_row, 0.0)
+    plan = H.resolve_chunk_size(bt, H.ChunkSize.Auto, v, None)
+    est = bt * per_row + plan.num_chunks * fixed
+    return {"value": bt / est, "unit": "rows/s", "cores": 1, "kind": "port",
+            "sample": (f"oracle/liborda_oracle.so, one thread, BT={n1} and BT={n2} of this "
+                       f"workload (same H, V, options; f32 arithmetic as the reference); "
+                       f"per-row {per_row:.3f} s and per-chunk {fixed:.3f} s fitted from the two "
+                       f"timings, extrapolated to BT={bt} in {plan.num_chunks} chunks "
+                       f"({est:.0f} s)")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(this build has no multi-GPU path).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import orda_hip as H
+    if not H.is_available():
+        raise SystemExit("liborda_hip.so sees no gfx950 device")
+    wl = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    log(f"workload {args.workload}: generating inputs")
+    s, w, y, t = make_inputs(torch, wl, dev)
+    teacher = teacher_obj(H, t)
+    opts = options(H, wl)
+    ctx = H.Context(0)
+    torch.cuda.synchronize()
+    out = None
+    for i in range(args.warmup):
+        out = H.distillation_loss(s, w, y, teacher, opts, ctx=ctx)
+        log(f"warmup {i + 1}/{args.warmup}: loss {out.loss:.5f}")
+    outputs = {"grad_student_hidden": out.grad_student_hidden, "grad_weight": out.grad_weight}
+    if out.grad_teacher_hidden is not None:
+        outputs["grad_teacher_hidden"] = out.grad_teacher_hidden
+    if out.grad_teacher_weight is not None:
+        outputs["grad_teacher_weight"] = out.grad_teacher_weight
+    plan = out.chunk_plan
+    ctx.reset_timing()
+    ctx.set_timing(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        out = H.distillation_loss(s, w, y, teacher, opts, ctx=ctx, outputs=outputs)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ctx.set_timing(False)
+    log(f"timed {args.steps} steps in {elapsed * 1e3:.1f} ms, loss {out.loss:.5f}")
+    teacher_kind, bt, h, ht, v, dt, *_ = wl
+    work = work_per_step(wl, plan)
+    kernels = {}
+    for kind, (bound, amount) in work.items():
+        ms, n = ctx.kernel_time(kind)
+        if n == 0 or amount == 0:
+            continue
+        per_step = amount
+        if bound == "mfma":
+            achieved = per_step * args.steps / (ms * 1e-3) / 1e12
+            peak = PEAK_MFMA_TFLOPS[dt]
+            unit = "TFLOP/s"
+        else:
+            achieved = per_step * args.steps / (ms * 1e-3) / 1e9
+            peak = PEAK_HBM_GBS
+            unit = "GB/s"
+        kernels[kind] = {"bound": bound, "achieved": round(achieved, 2), "peak": peak,
+                         "unit": unit, "frac": round(achieved / peak, 4),
+                         "ms_per_step": round(ms / args.steps, 4),
+                         "launches_per_step": n // args.steps,
+                         "work_per_step": per_step}
+    ms_other, _ = ctx.kernel_time("other")
+    dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
+    d = kernels[dom]
+    n_launch = max(d["launches_per_step"], 1)
+    roofline = {"bound": d["bound"], "kernel": dom, "achieved": d["achieved"], "peak": d["peak"],
+                "unit": d["unit"], "frac": d["frac"],
+                "work_per_launch": d["work_per_step"] / n_launch,
+                "avg_launch_ms": d["ms_per_step"] / n_launch, "traffic": None}
+    rows_per_s = bt * args.steps / elapsed
+    line = {
+        "metric": "fwd+bwd rows/sec at BT=8192 H=4096 V=131072; MFMA util %; row-pass HBM GB/s",
+        "value": round(rows_per_s, 1), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": dt, "data": "synthetic",
+        "config": {"workload": args.workload, "teacher": teacher_kind, "bt": bt, "h": h,
+                   "v": v, "chunks": f"{plan.num_chunks}x{plan.chunk_size}"},
+        "roofline": roofline,
+        "kernels": kernels,
+        "mfma_util": {k: kernels[k]["frac"] for k in kernels if kernels[k]["bound"] == "mfma"},
+        "row_pass_gbs": kernels.get("row_pass", {}).get("achieved"),
+        "other_ms_per_step": round(ms_other / args.steps, 4),
+    }
+    del s, w, y, t, teacher, out, outputs
+    ctx.close()
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle on a bounded sample")
+        line["cpu_baseline"] = cpu_baseline(wl)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

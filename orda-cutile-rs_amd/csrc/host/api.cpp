@@ -1,0 +1,1174 @@
+// api.cpp — host orchestration of liborda_hip.so: the C ABI of
+// include/orda/orda.h over the gfx950 kernels.
+//
+// distillation_loss follows src/api.rs:188-422 step for step: validate, pick
+// the teacher-CE weight, count non-ignored labels for the deferred mean,
+// resolve the chunk plan, then per chunk build the [student; teacher]
+// logits (one MFMA GEMM with a fused statistics epilogue), run the fused
+// KL + CE row pass that overwrites the logits with their gradient, and
+// finally run the backward GEMMs, the deferred mean (fused as GEMM alpha),
+// the optional INT8 round trip and the f64 loss assembly.
+//
+// Device-first layout: the logits of consecutive chunks are kept side by
+// side in one staging buffer (student block, then teacher block, each
+// [rows, round_up(V, 8)]); each chunk's logits_chunk is a slice of it, and
+// the backward GEMMs run once per group of chunks so grad_W is written once
+// per group instead of read-modified-written per chunk. The group size is
+// bounded by the context's staging budget; an out-of-memory failure first
+// halves the group, then walks the reference's chunk-doubling schedule
+// (resolver.rs:107-126).
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <map>
+#include <memory>
+
+#include "orda_host.h"
+
+using orda::DType;
+using orda::Error;
+
+struct orda_ctx {
+  int device = 0;
+  hipStream_t own = nullptr;
+  hipStream_t stream = nullptr;
+  int64_t mem_limit = 0;
+  int64_t held = 0;
+  int64_t staging_budget = int64_t(8) << 30;
+  struct Buf {
+    void* p = nullptr;
+    int64_t bytes = 0;
+  };
+  std::map<std::string, Buf> bufs;
+  bool timing = false;
+  struct Pending {
+    int kind;
+    hipEvent_t a, b;
+  };
+  std::vector<Pending> pending;
+  std::vector<hipEvent_t> pool;
+  double total_ms[ORDA_KERNEL_KINDS] = {};
+  int64_t launches[ORDA_KERNEL_KINDS] = {};
+};
+
+namespace {
+
+[[noreturn]] void fail(int32_t status, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  throw Error{status, buf};
+}
+
+void hip_check(hipError_t e, const char* what) {
+  if (e == hipSuccess) return;
+  (void)hipGetLastError();
+  if (e == hipErrorOutOfMemory) fail(ORDA_ERR_OOM, "%s: device out of memory", what);
+  fail(ORDA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+void copy_err(const Error& e, char* err, size_t len) {
+  if (!err || !len) return;
+  snprintf(err, len, "%s", e.msg.c_str());
+}
+
+// Rust's `{}` Display of an f32 (shortest round-trip digits, no exponent).
+std::string fmt_f32(float x) {
+  if (isnan(x)) return "NaN";
+  if (isinf(x)) return x > 0 ? "inf" : "-inf";
+  char buf[128];
+  int p = 1;
+  for (; p <= 9; ++p) {
+    snprintf(buf, sizeof buf, "%.*g", p, static_cast<double>(x));
+    if (strtof(buf, nullptr) == x) break;
+  }
+  if (!strchr(buf, 'e')) return buf;
+  // expand exponent notation to a plain decimal
+  double d = strtod(buf, nullptr);
+  int exp10 = static_cast<int>(floor(log10(fabs(d))));
+  int decimals = exp10 < 0 ? (p - 1 - exp10) : std::max(0, p - 1 - exp10);
+  snprintf(buf, sizeof buf, "%.*f", decimals, d);
+  return buf;
+}
+
+int64_t round8(int64_t x) { return (x + 7) / 8 * 8; }
+
+int64_t tensor_ld(const orda_tensor& t) { return t.ld ? t.ld : t.cols; }
+
+DType to_dtype(int32_t d, const char* what) {
+  if (d == ORDA_F32) return DType::F32;
+  if (d == ORDA_BF16) return DType::BF16;
+  fail(ORDA_ERR_INVALID, "%s must be float32 or bfloat16", what);
+}
+
+// ------------------------------------------------------------ workspace
+void* ws(orda_ctx* c, const std::string& name, int64_t bytes) {
+  orda_ctx::Buf& b = c->bufs[name];
+  if (bytes <= 0) return b.p;
+  if (b.p && b.bytes >= bytes) return b.p;
+  if (b.p) {
+    hip_check(hipFree(b.p), "hipFree");
+    c->held -= b.bytes;
+    b = orda_ctx::Buf{};
+  }
+  const int64_t rounded = (bytes + 255) / 256 * 256;
+  if (c->mem_limit > 0 && c->held + rounded > c->mem_limit)
+    fail(ORDA_ERR_OOM, "workspace '%s' (%lld bytes) exceeds the context memory limit",
+         name.c_str(), static_cast<long long>(rounded));
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, rounded);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    if (e == hipErrorOutOfMemory)
+      fail(ORDA_ERR_OOM, "hipMalloc of workspace '%s' (%lld bytes): out of memory", name.c_str(),
+           static_cast<long long>(rounded));
+    hip_check(e, "hipMalloc");
+  }
+  b.p = p;
+  b.bytes = rounded;
+  c->held += rounded;
+  return p;
+}
+
+void ws_release(orda_ctx* c, const std::string& name) {
+  auto it = c->bufs.find(name);
+  if (it == c->bufs.end() || !it->second.p) return;
+  (void)hipFree(it->second.p);
+  c->held -= it->second.bytes;
+  it->second = orda_ctx::Buf{};
+}
+
+void ws_trim(orda_ctx* c) {
+  for (auto& kv : c->bufs)
+    if (kv.second.p) (void)hipFree(kv.second.p);
+  c->bufs.clear();
+  c->held = 0;
+}
+
+// ------------------------------------------------------------ timing
+hipEvent_t get_event(orda_ctx* c) {
+  if (!c->pool.empty()) {
+    hipEvent_t e = c->pool.back();
+    c->pool.pop_back();
+    return e;
+  }
+  hipEvent_t e;
+  hip_check(hipEventCreate(&e), "hipEventCreate");
+  return e;
+}
+
+template <class F>
+void timed(orda_ctx* c, int kind, F&& f) {
+  if (!c->timing) {
+    hip_check(f(), "kernel launch");
+    return;
+  }
+  hipEvent_t a = get_event(c), b = get_event(c);
+  hip_check(hipEventRecord(a, c->stream), "hipEventRecord");
+  hip_check(f(), "kernel launch");
+  hip_check(hipEventRecord(b, c->stream), "hipEventRecord");
+  c->pending.push_back({kind, a, b});
+}
+
+void collect_timing(orda_ctx* c) {
+  for (auto& p : c->pending) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+      c->total_ms[p.kind] += ms;
+      c->launches[p.kind] += 1;
+    }
+    c->pool.push_back(p.a);
+    c->pool.push_back(p.b);
+  }
+  c->pending.clear();
+}
+
+// ------------------------------------------------------------ staging
+struct DMat {
+  const void* p = nullptr;
+  int64_t ld = 0, rows = 0, cols = 0;
+  DType t = DType::F32;
+};
+
+// Device-resident view of an input matrix with a pitch that is a multiple of
+// 8 elements and a 16-byte aligned base; copies only when needed.
+DMat stage(orda_ctx* c, const orda_tensor& t, const std::string& name, const char* what) {
+  DMat d;
+  d.t = to_dtype(t.dtype, what);
+  d.rows = t.rows;
+  d.cols = t.cols;
+  const int64_t ld = tensor_ld(t);
+  const int es = orda::dtype_size(d.t);
+  if (t.rows > 0 && t.cols > 0 && !t.data) fail(ORDA_ERR_INVALID, "%s has a null data pointer", what);
+  if (ld < t.cols) fail(ORDA_ERR_INVALID, "%s has ld < cols", what);
+  // Pass-through needs whole 16-byte chunks inside every row, including the
+  // last one: pitch and width both multiples of 8 elements.
+  if (t.location == ORDA_DEVICE && ld % 8 == 0 && t.cols % 8 == 0 &&
+      (reinterpret_cast<uintptr_t>(t.data) % 16) == 0) {
+    d.p = t.data;
+    d.ld = ld;
+    return d;
+  }
+  d.ld = round8(t.cols > 0 ? t.cols : 1);
+  void* buf = ws(c, name, t.rows * d.ld * es);
+  d.p = buf;
+  if (t.rows == 0) return d;
+  if (t.location == ORDA_DEVICE) {
+    hip_check(orda::launch_convert_rows(d.t, t.data, ld, d.t, buf, d.ld, t.rows, t.cols, c->stream),
+              "stage input");
+  } else {
+    if (d.ld != t.cols)
+      hip_check(hipMemsetAsync(buf, 0, t.rows * d.ld * es, c->stream), "hipMemsetAsync");
+    hip_check(hipMemcpy2DAsync(buf, d.ld * es, t.data, ld * es, t.cols * es, t.rows,
+                               hipMemcpyHostToDevice, c->stream),
+              "upload input");
+  }
+  return d;
+}
+
+// Output matrix: the caller's device buffer, or a device temporary copied
+// back to the caller's host buffer at the end.
+struct OutMat {
+  float* p = nullptr;
+  int64_t ld = 0;
+  const orda_tensor* t = nullptr;
+  bool host = false;
+};
+
+OutMat out_mat(orda_ctx* c, const orda_tensor& t, int64_t rows, int64_t cols,
+               const std::string& name, const char* what) {
+  if (t.dtype != ORDA_F32) fail(ORDA_ERR_INVALID, "%s must be float32", what);
+  if (t.rows != rows || t.cols != cols)
+    fail(ORDA_ERR_INVALID, "%s must be (%lld, %lld), got (%lld, %lld)", what,
+         static_cast<long long>(rows), static_cast<long long>(cols),
+         static_cast<long long>(t.rows), static_cast<long long>(t.cols));
+  if (!t.data && rows * cols > 0) fail(ORDA_ERR_INVALID, "%s has a null data pointer", what);
+  OutMat o;
+  o.t = &t;
+  if (t.location == ORDA_DEVICE) {
+    o.p = static_cast<float*>(t.data);
+    o.ld = tensor_ld(t);
+  } else {
+    o.host = true;
+    o.ld = cols;
+    o.p = static_cast<float*>(ws(c, name, rows * cols * 4));
+  }
+  return o;
+}
+
+void download(orda_ctx* c, const OutMat& o) {
+  if (!o.host) return;
+  const orda_tensor& t = *o.t;
+  if (t.rows == 0 || t.cols == 0) return;
+  hip_check(hipMemcpy2DAsync(t.data, tensor_ld(t) * 4, o.p, o.ld * 4, t.cols * 4, t.rows,
+                             hipMemcpyDeviceToHost, c->stream),
+            "download output");
+}
+
+// Copy a contiguous device array into an optional caller tensor (1-D data
+// viewed as rows x cols with the tensor's pitch).
+void deliver(orda_ctx* c, const orda_tensor& t, const void* src, int64_t rows, int64_t cols,
+             int es, const char* what) {
+  if (!t.data) return;
+  if (t.rows != rows || t.cols != cols)
+    fail(ORDA_ERR_INVALID, "%s must be (%lld, %lld)", what, static_cast<long long>(rows),
+         static_cast<long long>(cols));
+  const hipMemcpyKind k = t.location == ORDA_DEVICE ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost;
+  hip_check(hipMemcpy2DAsync(t.data, tensor_ld(t) * es, src, cols * es, cols * es, rows, k,
+                             c->stream),
+            what);
+}
+
+std::vector<int64_t> host_labels(orda_ctx* c, const int64_t* labels, int64_t n, int32_t loc) {
+  std::vector<int64_t> h(static_cast<size_t>(n));
+  if (n == 0) return h;
+  if (!labels) fail(ORDA_ERR_INVALID, "labels is null");
+  if (loc == ORDA_DEVICE) {
+    hip_check(hipMemcpyAsync(h.data(), labels, n * 8, hipMemcpyDeviceToHost, c->stream),
+              "read labels");
+    hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  } else {
+    memcpy(h.data(), labels, n * 8);
+  }
+  return h;
+}
+
+const int64_t* device_labels(orda_ctx* c, const int64_t* labels, const std::vector<int64_t>& h,
+                             int32_t loc, const std::string& name) {
+  if (loc == ORDA_DEVICE && (reinterpret_cast<uintptr_t>(labels) % 8) == 0) return labels;
+  void* d = ws(c, name, std::max<int64_t>(8, h.size() * 8));
+  if (!h.empty())
+    hip_check(hipMemcpyAsync(d, h.data(), h.size() * 8, hipMemcpyHostToDevice, c->stream),
+              "upload labels");
+  return static_cast<const int64_t*>(d);
+}
+
+void config_validate(const orda_kernel_config& k) {
+  const int64_t mf = k.max_fused_size;
+  if (mf < 1 || (mf & (mf - 1)) != 0)
+    fail(ORDA_ERR_INVALID, "max_fused_size must be a power of two >= 1, got %lld",
+         static_cast<long long>(mf));
+  if (k.has_max_chunks && k.max_chunks < 1)
+    fail(ORDA_ERR_INVALID, "max_chunks must be >= 1, got %lld", static_cast<long long>(k.max_chunks));
+}
+
+const char* dt_name(DType t) { return t == DType::F32 ? "float32" : "bfloat16"; }
+
+// ------------------------------------------------------------ the loss
+struct LossPlan {
+  int mode;
+  float w_s, w_t, kd, T, ls;
+  int64_t ignore;
+  bool need_teacher, has_ght, has_gwt;
+  float mean_scale;
+  int64_t bt, h, v, ht;
+  DType dt;
+  bool quant, stochastic;
+  uint64_t seed;
+};
+
+struct Inputs {
+  DMat hs, W, th, tw, tl;
+  const int64_t* labels = nullptr;
+  OutMat gh, gw, ght, gwt;
+};
+
+struct RunResult {
+  float scal[4];
+};
+
+char* at(const void* base, int64_t elems, DType t) {
+  return static_cast<char*>(const_cast<void*>(base)) + elems * orda::dtype_size(t);
+}
+
+void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan plan, int64_t G,
+              float* row3_out, float* scal_dev) {
+  using namespace orda;
+  const int64_t cs = plan.chunk_size, nc = plan.num_chunks;
+  const int64_t bt = P.bt, v = P.v, h = P.h;
+  const DType dt = P.dt;
+  const int es = dtype_size(dt);
+  const int64_t ldl = round8(v);
+  const int64_t nst = gemm_stat_tiles(v);
+  const int64_t cap = std::min(bt, G * cs);
+  const int blocks = P.need_teacher ? 2 : 1;
+  const bool tied_tce = P.mode == ORDA_TEACHER_TIED && P.w_t > 0.f;
+
+  void* L = ws(c, "logits", blocks * cap * ldl * es);
+  float4* stats = static_cast<float4*>(ws(c, "stats", 2 * cs * nst * 16));
+  float* xy = static_cast<float*>(ws(c, "xy", 2 * cs * 4));
+  hip_check(hipMemsetAsync(xy, 0, 2 * cs * 4, c->stream), "hipMemsetAsync");
+  float* rnll_s = row3_out;
+  float* rnll_t = row3_out + bt;
+  float* rkl = row3_out + 2 * bt;
+  const int64_t ldh_cat = round8(h);
+  void* hcat = tied_tce ? ws(c, "hcat", 2 * cap * ldh_cat * es) : nullptr;
+  const float inv_t = 1.0f / P.T;
+
+  for (int64_t g0 = 0; g0 < nc; g0 += G) {
+    const int64_t g1 = std::min(nc, g0 + G);
+    const int64_t gs = g0 * cs;
+    if (gs >= bt) break;
+    const int64_t ge = std::min(bt, g1 * cs);
+    const int64_t btg = ge - gs;
+    void* Ls = L;
+    void* Lt = at(L, btg * ldl, dt);
+    const bool first = g0 == 0;
+    const bool last = ge >= bt;
+
+    for (int64_t ci = g0; ci < g1; ++ci) {
+      const int64_t start = ci * cs;
+      if (start >= bt) break;
+      const int64_t end = std::min(start + cs, bt);
+      const int64_t n = end - start;
+      const int64_t sc = start - gs;
+
+      // ---- logits_chunk = [h_s; h_t] · Wᵀ (api.rs:272-299) with statistics
+      GemmArgs f{};
+      f.M = n;
+      f.N = v;
+      f.K = h;
+      f.lda = in.hs.ld;
+      f.ldb = in.W.ld;
+      f.ldc = ldl;
+      f.a_kmajor = f.b_kmajor = true;
+      f.in_type = dt;
+      f.logits_type = dt;
+      f.epi = GemmEpilogue::Logits;
+      f.alpha = 1.f;
+      f.lg.stats = stats;
+      f.lg.stats_ld = nst;
+      f.lg.xy = xy;
+      f.lg.labels = in.labels + start;
+      f.lg.ignore_index = P.ignore;
+      f.lg.inv_t = inv_t;
+      f.nprob = 1;
+      f.prob[0] = {at(in.hs.p, start * in.hs.ld, dt), in.W.p, at(Ls, sc * ldl, dt)};
+      const bool fuse_t = P.need_teacher && P.mode == ORDA_TEACHER_TIED && in.th.ld == in.hs.ld;
+      if (fuse_t) {
+        f.nprob = 2;
+        f.prob[1] = {at(in.th.p, start * in.th.ld, dt), in.W.p, at(Lt, sc * ldl, dt)};
+      }
+      f.group_m = static_cast<int>(((n + 255) / 256) * f.nprob);
+      timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_gemm(f, c->stream); });
+      if (P.need_teacher && !fuse_t) {
+        if (P.mode == ORDA_TEACHER_PRECOMPUTED) {
+          RowStatsArgs r{};
+          r.src_type = in.tl.t;
+          r.src = at(in.tl.p, start * in.tl.ld, in.tl.t);
+          r.lds = in.tl.ld;
+          r.dst_type = dt;
+          r.dst = at(Lt, sc * ldl, dt);
+          r.ldd = ldl;
+          r.n_rows = n;
+          r.v = v;
+          r.stats = stats + n * nst;
+          r.stats_ld = nst;
+          r.xy = xy + n;
+          r.labels = in.labels + start;
+          r.ignore_index = P.ignore;
+          r.inv_t = inv_t;
+          timed(c, ORDA_KERNEL_OTHER, [&] { return launch_row_stats(r, c->stream); });
+        } else {
+          GemmArgs t = f;
+          t.nprob = 1;
+          const bool sep = P.mode == ORDA_TEACHER_SEPARATE;
+          t.K = sep ? P.ht : h;
+          t.lda = in.th.ld;
+          t.ldb = sep ? in.tw.ld : in.W.ld;
+          t.prob[0] = {at(in.th.p, start * in.th.ld, dt), sep ? in.tw.p : in.W.p,
+                       at(Lt, sc * ldl, dt)};
+          t.lg.stats = stats + n * nst;
+          t.lg.xy = xy + n;
+          t.group_m = static_cast<int>((n + 255) / 256);
+          timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_gemm(t, c->stream); });
+        }
+      }
+
+      // ---- KL + CE + merge, in place (api.rs:301-344)
+      RowPassArgs r{};
+      r.ltype = dt;
+      r.student = at(Ls, sc * ldl, dt);
+      r.teacher = P.need_teacher ? at(Lt, sc * ldl, dt) : nullptr;
+      r.ld = ldl;
+      r.n_rows = n;
+      r.v = v;
+      r.stats_s = stats;
+      r.stats_t = stats + n * nst;
+      r.stats_ld = nst;
+      r.stats_tiles = nst;
+      r.stats_tiles_t = P.mode == ORDA_TEACHER_PRECOMPUTED ? 1 : nst;
+      r.xy_s = xy;
+      r.xy_t = xy + n;
+      r.labels = in.labels + start;
+      r.ignore_index = P.ignore;
+      r.w_s = P.w_s;
+      r.w_t = P.w_t;
+      r.kd = P.kd;
+      r.temperature = P.T;
+      r.label_smoothing = P.ls;
+      r.teacher_ce = P.w_t > 0.f;
+      r.teacher_grad = P.w_t > 0.f && P.mode != ORDA_TEACHER_PRECOMPUTED;
+      r.kl = P.kd > 0.f;
+      r.row_nll_s = rnll_s + start;
+      r.row_nll_t = rnll_t + start;
+      r.row_kl = rkl + start;
+      r.split = false;
+      timed(c, ORDA_KERNEL_ROW_PASS, [&] { return launch_row_pass(r, c->stream); });
+    }
+
+    // ---- grad_hidden = dlogits · W, scaled by the deferred mean (api.rs:347-366, 381-388)
+    {
+      GemmArgs d{};
+      d.M = btg;
+      d.N = h;
+      d.K = v;
+      d.lda = ldl;
+      d.ldb = in.W.ld;
+      d.ldc = in.gh.ld;
+      d.a_kmajor = true;
+      d.b_kmajor = false;
+      d.in_type = dt;
+      d.epi = GemmEpilogue::StoreF32;
+      d.alpha = P.mean_scale;
+      d.group_m = 4;
+      d.nprob = 1;
+      d.prob[0] = {Ls, in.W.p, in.gh.p + gs * in.gh.ld};
+      const bool fuse = P.has_ght && P.mode == ORDA_TEACHER_TIED && in.ght.ld == in.gh.ld;
+      if (fuse) {
+        d.nprob = 2;
+        d.prob[1] = {Lt, in.W.p, in.ght.p + gs * in.ght.ld};
+      }
+      timed(c, ORDA_KERNEL_GEMM_GRAD_HIDDEN, [&] { return launch_gemm(d, c->stream); });
+      if (P.has_ght && !fuse) {
+        GemmArgs t = d;
+        t.nprob = 1;
+        const bool sep = P.mode == ORDA_TEACHER_SEPARATE;
+        t.N = sep ? P.ht : h;
+        t.ldb = sep ? in.tw.ld : in.W.ld;
+        t.ldc = in.ght.ld;
+        t.prob[0] = {Lt, sep ? in.tw.p : in.W.p, in.ght.p + gs * in.ght.ld};
+        timed(c, ORDA_KERNEL_GEMM_GRAD_HIDDEN, [&] { return launch_gemm(t, c->stream); });
+      }
+    }
+
+    // ---- grad_W (+)= dlogitsᵀ · hidden (api.rs:350, 360, 367-370)
+    {
+      GemmArgs w{};
+      w.M = v;
+      w.N = h;
+      w.lda = ldl;
+      w.ldc = in.gw.ld;
+      w.a_kmajor = false;
+      w.b_kmajor = false;
+      w.in_type = dt;
+      w.epi = first ? GemmEpilogue::StoreF32 : GemmEpilogue::AccumF32;
+      w.alpha = last ? P.mean_scale : 1.f;
+      w.group_m = 4;
+      w.nprob = 1;
+      if (tied_tce) {
+        // [dS; dT]ᵀ · [h_s; h_t]: one GEMM over K = 2·rows.
+        hip_check(hipMemcpy2DAsync(hcat, ldh_cat * es, at(in.hs.p, gs * in.hs.ld, dt),
+                                   in.hs.ld * es, h * es, btg, hipMemcpyDeviceToDevice, c->stream),
+                  "stage hidden");
+        hip_check(hipMemcpy2DAsync(at(hcat, btg * ldh_cat, dt), ldh_cat * es,
+                                   at(in.th.p, gs * in.th.ld, dt), in.th.ld * es, h * es, btg,
+                                   hipMemcpyDeviceToDevice, c->stream),
+                  "stage hidden");
+        w.K = 2 * btg;
+        w.ldb = ldh_cat;
+        w.prob[0] = {Ls, hcat, in.gw.p};
+      } else {
+        w.K = btg;
+        w.ldb = in.hs.ld;
+        w.prob[0] = {Ls, at(in.hs.p, gs * in.hs.ld, dt), in.gw.p};
+      }
+      timed(c, ORDA_KERNEL_GEMM_GRAD_WEIGHT, [&] { return launch_gemm(w, c->stream); });
+      if (P.has_gwt) {
+        GemmArgs t = w;
+        t.K = btg;
+        t.N = P.ht;
+        t.ldb = in.th.ld;
+        t.ldc = in.gwt.ld;
+        t.prob[0] = {Lt, at(in.th.p, gs * in.th.ld, dt), in.gwt.p};
+        timed(c, ORDA_KERNEL_GEMM_GRAD_WEIGHT, [&] { return launch_gemm(t, c->stream); });
+      }
+    }
+  }
+
+  // ---- loss assembly (api.rs:401-405)
+  FinalizeArgs fa{};
+  fa.row_nll_s = rnll_s;
+  fa.row_nll_t = rnll_t;
+  fa.row_kl = rkl;
+  fa.bt = bt;
+  fa.chunk_size = cs;
+  fa.w_s = P.w_s;
+  fa.w_t = P.w_t;
+  fa.kd = P.kd;
+  fa.mean_scale = P.mean_scale;
+  fa.out = scal_dev;
+  timed(c, ORDA_KERNEL_OTHER, [&] { return launch_finalize(fa, c->stream); });
+}
+
+void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const int64_t* labels,
+               int64_t n_labels, int32_t lab_loc, const orda_teacher* teacher,
+               const orda_loss_options* o, orda_loss_output* out) {
+  using namespace orda;
+  if (!sh || !w || !teacher || !o || !out) fail(ORDA_ERR_INVALID, "null argument");
+  // ---- validate (api.rs:104-181)
+  config_validate(o->config);
+  const int64_t bt = sh->rows, h = sh->cols;
+  if (bt == 0) fail(ORDA_ERR_INVALID, "student_hidden has 0 rows (BT must be > 0)");
+  if (bt < 0 || h < 0 || w->rows < 0 || w->cols < 0) fail(ORDA_ERR_INVALID, "negative shape");
+  if (w->cols != h)
+    fail(ORDA_ERR_INVALID, "weight must have shape (V, %lld), got (%lld, %lld)",
+         static_cast<long long>(h), static_cast<long long>(w->rows), static_cast<long long>(w->cols));
+  const int64_t v = w->rows;
+  if (n_labels != bt)
+    fail(ORDA_ERR_INVALID, "labels must have length BT=%lld, got %lld", static_cast<long long>(bt),
+         static_cast<long long>(n_labels));
+  const std::vector<int64_t> hl = host_labels(c, labels, n_labels, lab_loc);
+  for (int64_t t : hl)
+    if (t != o->ignore_index && (t < 0 || t >= v))
+      fail(ORDA_ERR_INVALID, "label %lld out of range [0, %lld) and != ignore_index %lld",
+           static_cast<long long>(t), static_cast<long long>(v),
+           static_cast<long long>(o->ignore_index));
+  if (!(o->label_smoothing >= 0.f && o->label_smoothing <= 1.f))
+    fail(ORDA_ERR_INVALID, "label_smoothing must be in [0,1], got %s",
+         fmt_f32(o->label_smoothing).c_str());
+  if (o->kd_weight < 0.f)
+    fail(ORDA_ERR_INVALID, "kd_weight must be >= 0, got %s", fmt_f32(o->kd_weight).c_str());
+  if (o->temperature <= 0.f)
+    fail(ORDA_ERR_INVALID, "temperature must be > 0, got %s", fmt_f32(o->temperature).c_str());
+  const int mode = teacher->mode;
+  int64_t ht = h;
+  switch (mode) {
+    case ORDA_TEACHER_TIED:
+      if (teacher->hidden.rows != bt || teacher->hidden.cols != h)
+        fail(ORDA_ERR_INVALID, "Tied teacher hidden must be (%lld, %lld), got (%lld, %lld)",
+             static_cast<long long>(bt), static_cast<long long>(h),
+             static_cast<long long>(teacher->hidden.rows),
+             static_cast<long long>(teacher->hidden.cols));
+      break;
+    case ORDA_TEACHER_SEPARATE:
+      if (teacher->hidden.rows != bt)
+        fail(ORDA_ERR_INVALID, "Separate teacher hidden must have BT=%lld rows",
+             static_cast<long long>(bt));
+      ht = teacher->hidden.cols;
+      if (teacher->weight.rows != v || teacher->weight.cols != ht)
+        fail(ORDA_ERR_INVALID, "Separate teacher weight must be (%lld, %lld), got (%lld, %lld)",
+             static_cast<long long>(v), static_cast<long long>(ht),
+             static_cast<long long>(teacher->weight.rows),
+             static_cast<long long>(teacher->weight.cols));
+      break;
+    case ORDA_TEACHER_PRECOMPUTED:
+      if (teacher->logits.rows != bt || teacher->logits.cols != v)
+        fail(ORDA_ERR_INVALID, "Precomputed teacher logits must be (%lld, %lld), got (%lld, %lld)",
+             static_cast<long long>(bt), static_cast<long long>(v),
+             static_cast<long long>(teacher->logits.rows),
+             static_cast<long long>(teacher->logits.cols));
+      break;
+    default:
+      fail(ORDA_ERR_INVALID, "unknown teacher mode %d", mode);
+  }
+  // ---- backend (api.rs:197-207)
+  if (o->backend == ORDA_BACKEND_CPU)
+    fail(ORDA_ERR_INVALID,
+         "Backend::Cpu is the reference crate's CPU path; liborda_hip serves Backend::Auto and "
+         "Backend::Hip");
+  if (o->backend != ORDA_BACKEND_AUTO && o->backend != ORDA_BACKEND_HIP)
+    fail(ORDA_ERR_INVALID, "unknown backend %d", o->backend);
+
+  LossPlan P{};
+  P.mode = mode;
+  P.w_s = o->student_ce_weight;
+  P.w_t = o->has_teacher_ce_weight ? o->teacher_ce_weight : (mode == ORDA_TEACHER_TIED ? 1.f : 0.f);
+  if (P.w_t < 0.f)
+    fail(ORDA_ERR_INVALID, "teacher_ce_weight must be >= 0, got %s", fmt_f32(P.w_t).c_str());
+  P.kd = o->kd_weight;
+  P.T = o->temperature;
+  P.ls = o->label_smoothing;
+  P.ignore = o->ignore_index;
+  P.need_teacher = P.kd > 0.f || P.w_t > 0.f;
+  P.has_ght = P.w_t > 0.f && (mode == ORDA_TEACHER_TIED || mode == ORDA_TEACHER_SEPARATE);
+  P.has_gwt = P.w_t > 0.f && mode == ORDA_TEACHER_SEPARATE;
+  int64_t n_valid = 0;
+  for (int64_t t : hl) n_valid += t != P.ignore;
+  const int64_t denom = o->reduction == ORDA_REDUCTION_MEAN ? std::max<int64_t>(n_valid, 1) : 1;
+  P.mean_scale = 1.0f / static_cast<float>(denom);
+  P.bt = bt;
+  P.h = h;
+  P.v = v;
+  P.ht = ht;
+  P.quant = o->config.quantize_grad_weight != 0;
+  P.stochastic = o->config.stochastic_rounding != 0;
+  P.seed = o->config.has_stochastic_seed ? o->config.stochastic_seed : 0;
+
+  // ---- dtypes: every float input shares the student's dtype
+  P.dt = to_dtype(sh->dtype, "student_hidden");
+  if (to_dtype(w->dtype, "weight") != P.dt)
+    fail(ORDA_ERR_INVALID, "weight must be %s like student_hidden", dt_name(P.dt));
+  if (P.need_teacher && (mode == ORDA_TEACHER_TIED || mode == ORDA_TEACHER_SEPARATE) &&
+      to_dtype(teacher->hidden.dtype, "teacher hidden") != P.dt)
+    fail(ORDA_ERR_INVALID, "teacher hidden must be %s like student_hidden", dt_name(P.dt));
+  if (P.need_teacher && mode == ORDA_TEACHER_SEPARATE &&
+      to_dtype(teacher->weight.dtype, "teacher weight") != P.dt)
+    fail(ORDA_ERR_INVALID, "teacher weight must be %s like student_hidden", dt_name(P.dt));
+
+  const orda::ChunkPlan plan0 = resolve_chunk_size(bt, o->chunk_fixed != 0, o->chunk_rows, true, v,
+                                                   o->config.has_max_chunks != 0,
+                                                   o->config.max_chunks);
+
+  hip_check(hipSetDevice(c->device), "hipSetDevice");
+  // ---- device inputs and outputs
+  Inputs in;
+  in.hs = stage(c, *sh, "in.student", "student_hidden");
+  in.W = stage(c, *w, "in.weight", "weight");
+  if (P.need_teacher && (mode == ORDA_TEACHER_TIED || mode == ORDA_TEACHER_SEPARATE))
+    in.th = stage(c, teacher->hidden, "in.t_hidden", "teacher hidden");
+  if (P.need_teacher && mode == ORDA_TEACHER_SEPARATE)
+    in.tw = stage(c, teacher->weight, "in.t_weight", "teacher weight");
+  if (P.need_teacher && mode == ORDA_TEACHER_PRECOMPUTED) {
+    const orda_tensor& tl = teacher->logits;
+    if (tl.location == ORDA_DEVICE) {
+      in.tl.p = tl.data;
+      in.tl.ld = tensor_ld(tl);
+      in.tl.t = to_dtype(tl.dtype, "teacher logits");
+      in.tl.rows = tl.rows;
+      in.tl.cols = tl.cols;
+    } else {
+      in.tl = stage(c, tl, "in.t_logits", "teacher logits");
+    }
+  }
+  in.labels = device_labels(c, labels, hl, lab_loc, "in.labels");
+  in.gh = out_mat(c, out->grad_student_hidden, bt, h, "out.gh", "grad_student_hidden");
+  in.gw = out_mat(c, out->grad_weight, v, h, "out.gw", "grad_weight");
+  if (P.has_ght) in.ght = out_mat(c, out->grad_teacher_hidden, bt, ht, "out.ght", "grad_teacher_hidden");
+  if (P.has_gwt) in.gwt = out_mat(c, out->grad_teacher_weight, v, ht, "out.gwt", "grad_teacher_weight");
+  float* row3 = static_cast<float*>(ws(c, "rows", 3 * bt * 4));
+  float* scal = static_cast<float*>(ws(c, "scalars", 64));
+
+  // ---- chunk plan, staging group, OOM retry (resolver.rs:103-126)
+  orda::ChunkPlan plan = plan0;
+  const int64_t limit = o->config.has_max_chunks ? o->config.max_chunks : default_max_chunks_limit(bt);
+  const int64_t chunk_bytes = (P.need_teacher ? 2 : 1) * plan.chunk_size * round8(v) * dtype_size(P.dt);
+  int64_t G = std::max<int64_t>(1, std::min<int64_t>(plan.num_chunks, c->staging_budget / std::max<int64_t>(chunk_bytes, 1)));
+  for (;;) {
+    try {
+      run_loss(c, P, in, plan, G, row3, scal);
+      break;
+    } catch (const Error& e) {
+      if (e.status != ORDA_ERR_OOM) throw;
+      (void)hipStreamSynchronize(c->stream);
+      (void)hipGetLastError();
+      ws_release(c, "logits");
+      ws_release(c, "hcat");
+      if (G > 1) {
+        G /= 2;
+        continue;
+      }
+      const std::vector<int64_t> sched = chunk_doubling_schedule(bt, plan.num_chunks, limit);
+      int64_t next = -1;
+      for (int64_t s : sched)
+        if (s > plan.num_chunks) {
+          next = s;
+          break;
+        }
+      if (next < 0)
+        fail(ORDA_ERR_OOM, "out of device memory at num_chunks=%lld (limit %lld): %s",
+             static_cast<long long>(plan.num_chunks), static_cast<long long>(limit), e.msg.c_str());
+      plan = orda::ChunkPlan{ceil_div(bt, next), next};
+      G = 1;
+    }
+  }
+
+  // ---- optional INT8 round trip of grad_W (api.rs:390-399)
+  if (P.quant) {
+    uint8_t* keep = static_cast<uint8_t*>(ws(c, "keep", v));
+    hip_check(hipMemsetAsync(keep, 0, v, c->stream), "hipMemsetAsync");
+    hip_check(launch_mark_targets(in.labels, bt, P.ignore, keep, v, c->stream), "mark targets");
+    const bool want_codes = out->quant_codes.data != nullptr;
+    const bool want_scales = out->quant_scales.data != nullptr;
+    int8_t* codes = nullptr;
+    float* scales = nullptr;
+    int64_t ldq = h;
+    if (want_codes) {
+      if (out->quant_codes.dtype != ORDA_I8 || out->quant_codes.rows != v || out->quant_codes.cols != h)
+        fail(ORDA_ERR_INVALID, "quant_codes must be int8 (%lld, %lld)", static_cast<long long>(v),
+             static_cast<long long>(h));
+      if (out->quant_codes.location == ORDA_DEVICE) {
+        codes = static_cast<int8_t*>(out->quant_codes.data);
+        ldq = tensor_ld(out->quant_codes);
+      } else {
+        codes = static_cast<int8_t*>(ws(c, "out.codes", v * h));
+      }
+    }
+    if (want_scales) {
+      if (out->quant_scales.dtype != ORDA_F32 || out->quant_scales.rows * std::max<int64_t>(out->quant_scales.cols, 1) != v)
+        fail(ORDA_ERR_INVALID, "quant_scales must be float32 with V=%lld entries", static_cast<long long>(v));
+      scales = out->quant_scales.location == ORDA_DEVICE
+                   ? static_cast<float*>(out->quant_scales.data)
+                   : static_cast<float*>(ws(c, "out.scales", v * 4));
+    }
+    QuantArgs q{};
+    q.src = in.gw.p;
+    q.lds = in.gw.ld;
+    q.dst = in.gw.p;
+    q.ldd = in.gw.ld;
+    q.codes = codes;
+    q.ldq = ldq;
+    q.scales = scales;
+    q.keep_exact = keep;
+    q.rows = v;
+    q.cols = h;
+    q.stochastic = P.stochastic;
+    q.seed = P.seed;
+    q.grad_output = 1.0f;
+    timed(c, ORDA_KERNEL_QUANT, [&] { return launch_quant(q, c->stream); });
+    if (want_codes && out->quant_codes.location != ORDA_DEVICE)
+      hip_check(hipMemcpy2DAsync(out->quant_codes.data, tensor_ld(out->quant_codes), codes, h, h, v,
+                                 hipMemcpyDeviceToHost, c->stream),
+                "download codes");
+    if (want_scales && out->quant_scales.location != ORDA_DEVICE)
+      hip_check(hipMemcpyAsync(out->quant_scales.data, scales, v * 4, hipMemcpyDeviceToHost,
+                               c->stream),
+                "download scales");
+  }
+
+  // ---- outputs
+  download(c, in.gh);
+  download(c, in.gw);
+  if (P.has_ght) download(c, in.ght);
+  if (P.has_gwt) download(c, in.gwt);
+  deliver(c, out->row_nll_student, row3, bt, 1, 4, "row_nll_student");
+  deliver(c, out->row_nll_teacher, row3 + bt, bt, 1, 4, "row_nll_teacher");
+  deliver(c, out->row_kl, row3 + 2 * bt, bt, 1, 4, "row_kl");
+  float hs[4];
+  hip_check(hipMemcpyAsync(hs, scal, 16, hipMemcpyDeviceToHost, c->stream), "read loss");
+  hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  collect_timing(c);
+  out->loss = hs[0];
+  out->student_ce = hs[1];
+  out->teacher_ce = hs[2];
+  out->kl = hs[3];
+  out->has_grad_teacher_hidden = P.has_ght;
+  out->has_grad_teacher_weight = P.has_gwt;
+  out->chunk_size = plan.chunk_size;
+  out->num_chunks = plan.num_chunks;
+}
+
+struct TempCtx {
+  orda_ctx* c = nullptr;
+  bool owned = false;
+  ~TempCtx() {
+    if (owned) orda_ctx_destroy(c);
+  }
+};
+
+orda_ctx* ensure_ctx(orda_ctx* ctx, TempCtx& tmp) {
+  if (ctx) return ctx;
+  char err[256];
+  if (orda_ctx_create(0, &tmp.c, err, sizeof err) != ORDA_OK) fail(ORDA_ERR_UNAVAILABLE, "%s", err);
+  tmp.owned = true;
+  return tmp.c;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t orda_abi_version(void) { return ORDA_ABI_VERSION; }
+
+int32_t orda_is_available(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, 0) != hipSuccess) return 0;
+  return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+void orda_kernel_config_from_profile(int32_t profile, orda_kernel_config* cfg) {
+  if (!cfg) return;
+  memset(cfg, 0, sizeof *cfg);
+  cfg->fast_math = profile == ORDA_PROFILE_FAST;
+  cfg->max_fused_size = 65536 / 2;
+}
+
+void orda_loss_options_default(orda_loss_options* o) {
+  if (!o) return;
+  memset(o, 0, sizeof *o);
+  o->student_ce_weight = 1.0f;
+  o->kd_weight = 0.0f;
+  o->temperature = 1.0f;
+  o->ignore_index = -100;
+  o->label_smoothing = 0.0f;
+  o->reduction = ORDA_REDUCTION_MEAN;
+  o->chunk_fixed = 0;
+  orda_kernel_config_from_profile(ORDA_PROFILE_BALANCED, &o->config);
+  o->backend = ORDA_BACKEND_AUTO;
+}
+
+int32_t orda_kernel_config_validate(const orda_kernel_config* cfg, char* err, size_t err_len) {
+  try {
+    if (!cfg) fail(ORDA_ERR_INVALID, "null config");
+    config_validate(*cfg);
+    return ORDA_OK;
+  } catch (const Error& e) {
+    copy_err(e, err, err_len);
+    return e.status;
+  }
+}
+
+int32_t orda_ctx_create(int32_t device, orda_ctx** out, char* err, size_t err_len) {
+  try {
+    if (!out) fail(ORDA_ERR_INVALID, "null output pointer");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
+      (void)hipGetLastError();
+      fail(ORDA_ERR_UNAVAILABLE, "no HIP device is visible");
+    }
+    if (device < 0 || device >= n) fail(ORDA_ERR_INVALID, "device %d out of range [0, %d)", device, n);
+    std::unique_ptr<orda_ctx> c(new orda_ctx());
+    c->device = device;
+    hip_check(hipSetDevice(device), "hipSetDevice");
+    hip_check(hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking), "hipStreamCreate");
+    c->stream = c->own;
+    *out = c.release();
+    return ORDA_OK;
+  } catch (const Error& e) {
+    copy_err(e, err, err_len);
+    return e.status;
+  }
+}
+
+void orda_ctx_destroy(orda_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  for (auto& p : c->pending) {
+    c->pool.push_back(p.a);
+    c->pool.push_back(p.b);
+  }
+  for (hipEvent_t e : c->pool) (void)hipEventDestroy(e);
+  ws_trim(c);
+  if (c->own) (void)hipStreamDestroy(c->own);
+  delete c;
+}
+
+int32_t orda_ctx_set_stream(orda_ctx* c, void* s) {
+  if (!c) return ORDA_ERR_INVALID;
+  c->stream = s ? static_cast<hipStream_t>(s) : c->own;
+  return ORDA_OK;
+}
+
+int32_t orda_ctx_set_memory_limit(orda_ctx* c, int64_t bytes) {
+  if (!c || bytes < 0) return ORDA_ERR_INVALID;
+  c->mem_limit = bytes;
+  return ORDA_OK;
+}
+
+int32_t orda_ctx_trim(orda_ctx* c) {
+  if (!c) return ORDA_ERR_INVALID;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  ws_trim(c);
+  return ORDA_OK;
+}
+
+int32_t orda_ctx_set_timing(orda_ctx* c, int32_t enable) {
+  if (!c) return ORDA_ERR_INVALID;
+  c->timing = enable != 0;
+  return ORDA_OK;
+}
+
+int32_t orda_ctx_get_kernel_time(orda_ctx* c, int32_t kind, double* total_ms, int64_t* launches) {
+  if (!c || kind < 0 || kind >= ORDA_KERNEL_KINDS) return ORDA_ERR_INVALID;
+  if (total_ms) *total_ms = c->total_ms[kind];
+  if (launches) *launches = c->launches[kind];
+  return ORDA_OK;
+}
+
+int32_t orda_ctx_reset_kernel_time(orda_ctx* c) {
+  if (!c) return ORDA_ERR_INVALID;
+  for (int k = 0; k < ORDA_KERNEL_KINDS; ++k) {
+    c->total_ms[k] = 0;
+    c->launches[k] = 0;
+  }
+  return ORDA_OK;
+}
+
+int32_t orda_distillation_loss(orda_ctx* ctx, const orda_tensor* student_hidden,
+                               const orda_tensor* weight, const int64_t* labels, int64_t n_labels,
+                               int32_t labels_location, const orda_teacher* teacher,
+                               const orda_loss_options* opts, orda_loss_output* out, char* err,
+                               size_t err_len) {
+  TempCtx tmp;
+  try {
+    orda_ctx* c = ensure_ctx(ctx, tmp);
+    loss_impl(c, student_hidden, weight, labels, n_labels, labels_location, teacher, opts, out);
+    return ORDA_OK;
+  } catch (const Error& e) {
+    copy_err(e, err, err_len);
+    return e.status;
+  } catch (const std::exception& e) {
+    copy_err(Error{ORDA_ERR_INTERNAL, e.what()}, err, err_len);
+    return ORDA_ERR_INTERNAL;
+  }
+}
+
+int32_t orda_kl_ce_on_logits_chunk(orda_ctx* ctx, const orda_tensor* logits_chunk,
+                                   const int32_t* targets, int32_t targets_location, int64_t n_rows,
+                                   float inv_t, float kl_grad_scale, float t_sq,
+                                   float student_ce_weight, float teacher_ce_weight,
+                                   float label_smoothing, int32_t ignore_index,
+                                   int32_t student_only, int32_t compute_kl,
+                                   orda_tensor* grad_kl_student, orda_tensor* kl_per_row,
+                                   orda_tensor* grad_ce, orda_tensor* ce_loss, char* err,
+                                   size_t err_len) {
+  using namespace orda;
+  TempCtx tmp;
+  try {
+    orda_ctx* c = ensure_ctx(ctx, tmp);
+    if (!logits_chunk || !grad_kl_student || !kl_per_row || !grad_ce || !ce_loss)
+      fail(ORDA_ERR_INVALID, "null argument");
+    // launch.rs:67-73
+    const int64_t v = logits_chunk->cols;
+    if (logits_chunk->rows != 2 * n_rows) fail(ORDA_ERR_INVALID, "logits_chunk must be [2*n_rows, V]");
+    if (n_rows < 0 || v < 1) fail(ORDA_ERR_INVALID, "empty logits_chunk");
+    hip_check(hipSetDevice(c->device), "hipSetDevice");
+    const DMat L = stage(c, *logits_chunk, "slot.logits", "logits_chunk");
+    std::vector<int64_t> hl(static_cast<size_t>(n_rows));
+    {
+      std::vector<int32_t> t32(static_cast<size_t>(n_rows));
+      if (n_rows > 0) {
+        if (!targets) fail(ORDA_ERR_INVALID, "targets is null");
+        if (targets_location == ORDA_DEVICE) {
+          hip_check(hipMemcpy(t32.data(), targets, n_rows * 4, hipMemcpyDeviceToHost), "read targets");
+        } else {
+          memcpy(t32.data(), targets, n_rows * 4);
+        }
+      }
+      for (int64_t i = 0; i < n_rows; ++i) hl[i] = t32[i];
+    }
+    const int64_t* lab = device_labels(c, nullptr, hl, ORDA_HOST, "slot.labels");
+    const int64_t grid_rows = student_only ? n_rows : 2 * n_rows;
+    OutMat gk = out_mat(c, *grad_kl_student, n_rows, v, "slot.gkl", "grad_kl_student");
+    OutMat gc = out_mat(c, *grad_ce, grid_rows, v, "slot.gce", "grad_ce");
+    OutMat kr = out_mat(c, *kl_per_row, n_rows, 1, "slot.klr", "kl_per_row");
+    OutMat cl = out_mat(c, *ce_loss, grid_rows, 1, "slot.cel", "ce_loss");
+    if (gk.ld != v || gc.ld != v) fail(ORDA_ERR_INVALID, "gradient outputs must be dense");
+    float4* stats = static_cast<float4*>(ws(c, "slot.stats", std::max<int64_t>(1, 2 * n_rows) * 16));
+    float* xy = static_cast<float*>(ws(c, "slot.xy", std::max<int64_t>(1, 2 * n_rows) * 4));
+    hip_check(hipMemsetAsync(xy, 0, std::max<int64_t>(1, 2 * n_rows) * 4, c->stream), "hipMemsetAsync");
+    for (int half = 0; half < 2; ++half) {
+      RowStatsArgs r{};
+      r.src_type = L.t;
+      r.src = at(L.p, half * n_rows * L.ld, L.t);
+      r.lds = L.ld;
+      r.dst = nullptr;
+      r.n_rows = n_rows;
+      r.v = v;
+      r.stats = stats + half * n_rows;
+      r.stats_ld = 1;
+      r.xy = xy + half * n_rows;
+      r.labels = lab;
+      r.ignore_index = ignore_index;
+      r.inv_t = inv_t;
+      timed(c, ORDA_KERNEL_OTHER, [&] { return launch_row_stats(r, c->stream); });
+    }
+    float* nll_t_unused = static_cast<float*>(ws(c, "slot.unused", std::max<int64_t>(1, n_rows) * 8));
+    RowPassArgs a{};
+    a.ltype = L.t;
+    a.student = const_cast<void*>(L.p);
+    a.teacher = at(L.p, n_rows * L.ld, L.t);
+    a.ld = L.ld;
+    a.n_rows = n_rows;
+    a.v = v;
+    a.stats_s = stats;
+    a.stats_t = stats + n_rows;
+    a.stats_ld = 1;
+    a.stats_tiles = 1;
+    a.stats_tiles_t = 1;
+    a.xy_s = xy;
+    a.xy_t = xy + n_rows;
+    a.labels = lab;
+    a.ignore_index = ignore_index;
+    a.w_s = student_ce_weight;
+    a.w_t = teacher_ce_weight;
+    a.kd = 0.f;
+    a.temperature = 1.f / inv_t;
+    a.label_smoothing = label_smoothing;
+    a.kl = compute_kl != 0;
+    a.row_nll_s = nll_t_unused;
+    a.row_nll_t = nll_t_unused + n_rows;
+    a.row_kl = kr.p;
+    a.split = true;
+    a.grad_kl = gk.p;
+    a.grad_ce = gc.p;
+    a.ce_loss = cl.p;
+    a.kl_grad_scale = kl_grad_scale;
+    a.t_sq = t_sq;
+    a.inv_t = inv_t;
+    a.student_only = student_only != 0;
+    timed(c, ORDA_KERNEL_ROW_PASS, [&] { return launch_row_pass(a, c->stream); });
+    download(c, gk);
+    download(c, gc);
+    download(c, kr);
+    download(c, cl);
+    hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    collect_timing(c);
+    return ORDA_OK;
+  } catch (const Error& e) {
+    copy_err(e, err, err_len);
+    return e.status;
+  } catch (const std::exception& e) {
+    copy_err(Error{ORDA_ERR_INTERNAL, e.what()}, err, err_len);
+    return ORDA_ERR_INTERNAL;
+  }
+}
+
+int32_t orda_quant_rows_int8(orda_ctx* ctx, const orda_tensor* m, const int64_t* targets,
+                             int64_t n_targets, int32_t targets_location, int64_t ignore_index,
+                             int32_t stochastic, uint64_t seed, float grad_output,
+                             orda_tensor* outp, orda_tensor* codes, orda_tensor* scales, char* err,
+                             size_t err_len) {
+  using namespace orda;
+  TempCtx tmp;
+  try {
+    orda_ctx* c = ensure_ctx(ctx, tmp);
+    if (!m || !outp) fail(ORDA_ERR_INVALID, "null argument");
+    if (m->dtype != ORDA_F32) fail(ORDA_ERR_INVALID, "m must be float32");
+    hip_check(hipSetDevice(c->device), "hipSetDevice");
+    const int64_t rows = m->rows, cols = m->cols;
+    const DMat src = stage(c, *m, "q.src", "m");
+    OutMat o = out_mat(c, *outp, rows, cols, "q.out", "out");
+    const std::vector<int64_t> hl = host_labels(c, targets, n_targets, targets_location);
+    const int64_t* lab = device_labels(c, targets, hl, targets_location, "q.labels");
+    uint8_t* keep = static_cast<uint8_t*>(ws(c, "q.keep", std::max<int64_t>(rows, 1)));
+    hip_check(hipMemsetAsync(keep, 0, std::max<int64_t>(rows, 1), c->stream), "hipMemsetAsync");
+    hip_check(launch_mark_targets(lab, n_targets, ignore_index, keep, rows, c->stream), "mark targets");
+    int8_t* q = nullptr;
+    int64_t ldq = cols;
+    if (codes && codes->data) {
+      if (codes->dtype != ORDA_I8 || codes->rows != rows || codes->cols != cols)
+        fail(ORDA_ERR_INVALID, "codes must be int8 [rows, cols]");
+      if (codes->location == ORDA_DEVICE) {
+        q = static_cast<int8_t*>(codes->data);
+        ldq = tensor_ld(*codes);
+      } else {
+        q = static_cast<int8_t*>(ws(c, "q.codes", std::max<int64_t>(1, rows * cols)));
+      }
+    }
+    float* s = nullptr;
+    if (scales && scales->data) {
+      if (scales->dtype != ORDA_F32 || scales->rows * std::max<int64_t>(scales->cols, 1) != rows)
+        fail(ORDA_ERR_INVALID, "scales must be float32 with one entry per row");
+      s = scales->location == ORDA_DEVICE ? static_cast<float*>(scales->data)
+                                          : static_cast<float*>(ws(c, "q.scales", std::max<int64_t>(1, rows) * 4));
+    }
+    QuantArgs a{};
+    a.src = static_cast<const float*>(src.p);
+    a.lds = src.ld;
+    a.dst = o.p;
+    a.ldd = o.ld;
+    a.codes = q;
+    a.ldq = ldq;
+    a.scales = s;
+    a.keep_exact = keep;
+    a.rows = rows;
+    a.cols = cols;
+    a.stochastic = stochastic != 0;
+    a.seed = seed;
+    a.grad_output = grad_output;
+    timed(c, ORDA_KERNEL_QUANT, [&] { return launch_quant(a, c->stream); });
+    download(c, o);
+    if (q && codes->location != ORDA_DEVICE && rows * cols > 0)
+      hip_check(hipMemcpy2DAsync(codes->data, tensor_ld(*codes), q, cols, cols, rows,
+                                 hipMemcpyDeviceToHost, c->stream),
+                "download codes");
+    if (s && scales->location != ORDA_DEVICE && rows > 0)
+      hip_check(hipMemcpyAsync(scales->data, s, rows * 4, hipMemcpyDeviceToHost, c->stream),
+                "download scales");
+    hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    collect_timing(c);
+    return ORDA_OK;
+  } catch (const Error& e) {
+    copy_err(e, err, err_len);
+    return e.status;
+  } catch (const std::exception& e) {
+    copy_err(Error{ORDA_ERR_INTERNAL, e.what()}, err, err_len);
+    return ORDA_ERR_INTERNAL;
+  }
+}
+
+}  // extern "C"

@@ -1,0 +1,171 @@
+// orda_kernels.h — launchers for the gfx950 kernels of the fused
+// cross-entropy + forward-KL distillation loss. Internal to liborda_hip.so;
+// the public surface is include/orda/orda.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace orda {
+
+enum class DType : int { F32 = 0, BF16 = 1 };
+
+inline int dtype_size(DType t) { return t == DType::F32 ? 4 : 2; }
+
+// ---------------------------------------------------------------- GEMM
+// One launch computes up to two problems that share M, N, K and pitches:
+//   C_p[M,N] (op)= alpha * A_p · B_p
+// A is K-major ([M][lda], element (m,k) at m*lda+k) or M-major ([K][lda],
+// (m,k) at k*lda+m); likewise B is K-major ([N][ldb]) or N-major ([K][ldb]).
+// Pitches are in elements and must be multiples of 8; base pointers 16-byte
+// aligned. Out-of-range rows/columns/K are zero-filled on load and masked on
+// store.
+enum class GemmEpilogue : int {
+  StoreF32 = 0,    // C = alpha*acc                       (C is float)
+  AccumF32 = 1,    // C = alpha*(C + acc)                 (C is float)
+  Logits = 2,      // C = acc stored in the logits dtype, plus per-row
+                   // partial softmax statistics for every 256-column tile
+};
+
+struct GemmProblem {
+  const void* a;
+  const void* b;
+  void* c;
+};
+
+struct LogitStatsArgs {
+  // stats[(p*M + m) * stats_ld + n_tile] = {max, Σe^(x-max), Σe^((x-max)/T), Σx}
+  float4* stats;
+  int64_t stats_ld;       // in float4 units, >= ceil(N/256)
+  float* xy;              // xy[p*M + m] = fp32 logit at the row's label column
+  const int64_t* labels;  // label of row m of either problem = labels[m]
+  int64_t ignore_index;
+  float inv_t;            // 1/T
+};
+
+struct GemmArgs {
+  int nprob;              // 1 or 2
+  GemmProblem prob[2];
+  int64_t M, N, K;
+  int64_t lda, ldb, ldc;
+  bool a_kmajor, b_kmajor;
+  DType in_type;          // dtype of A and B
+  DType logits_type;      // dtype of C for the Logits epilogue
+  GemmEpilogue epi;
+  float alpha;
+  int group_m;            // M-tiles per raster group (L2 reuse of B)
+  LogitStatsArgs lg;
+};
+
+hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);
+int64_t gemm_stat_tiles(int64_t n);   // ceil(n/256)
+
+// ---------------------------------------------------------------- row pass
+// Fused KL + CE + merge over row pairs of a logits chunk, gradient written
+// in place (or to split outputs for the chunk-launcher entry point).
+struct RowPassArgs {
+  DType ltype;             // logits storage dtype
+  void* student;           // row r of the student block at student + r*ld
+  void* teacher;           // row r of the teacher block (may be null)
+  int64_t ld;              // pitch (elements) of both blocks, multiple of 8
+  int64_t n_rows;          // row pairs
+  int64_t v;               // vocabulary
+  const float4* stats_s;   // per-row partial stats of student rows
+  const float4* stats_t;   // ... of teacher rows (may be null)
+  int64_t stats_ld;        // float4 entries per row
+  int64_t stats_tiles;     // entries filled per student row
+  int64_t stats_tiles_t;   // entries filled per teacher row
+  const float* xy_s;       // fp32 target logit of each student row
+  const float* xy_t;
+  const int64_t* labels;   // [n_rows]
+  int64_t ignore_index;
+  float w_s, w_t, kd, temperature, label_smoothing;
+  bool teacher_ce;         // w_t > 0: compute teacher CE loss
+  bool teacher_grad;       // write the teacher CE gradient into teacher rows
+  bool kl;                 // kd > 0: KL loss and student KL gradient
+  float* row_nll_s;        // [n_rows] outputs (never null)
+  float* row_nll_t;
+  float* row_kl;           // KL_row * T^2 (T^2 in f32), 0 when ignored
+  // Split mode (chunk-launcher entry point): gradients go to separate
+  // buffers instead of overwriting the logits, and are not merged.
+  bool split;
+  float* grad_kl;          // [n_rows][v] (split mode)
+  float* grad_ce;          // [n_rows or 2*n_rows][v] (split mode)
+  float* ce_loss;          // [n_rows or 2*n_rows] (split mode)
+  float kl_grad_scale;     // split mode: KL gradient scale as given
+  float t_sq;              // split mode: T^2 as given
+  float inv_t;             // split mode: 1/T as given
+  bool student_only;       // split mode: CE over student rows only
+};
+
+hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t stream);
+
+// Per-row statistics of rows that were not produced by the GEMM (Precomputed
+// teacher logits, the chunk-launcher entry point). Reads src (fp32 or bf16,
+// any pitch), writes one stats entry per row and the fp32 target logit, and
+// optionally copies the row into dst (logits dtype, pitch ldd, zero padding
+// up to the next multiple of 8).
+struct RowStatsArgs {
+  DType src_type;
+  const void* src;
+  int64_t lds;
+  DType dst_type;
+  void* dst;               // may be null
+  int64_t ldd;
+  int64_t n_rows, v;
+  float4* stats;           // stats[r * stats_ld]
+  int64_t stats_ld;
+  float* xy;
+  const int64_t* labels;   // may be null (then xy is not written)
+  int64_t ignore_index;
+  float inv_t;
+};
+hipError_t launch_row_stats(const RowStatsArgs& a, hipStream_t stream);
+
+// Zero columns [v, ld) of rows [0, n_rows) (keeps pitch padding zero).
+hipError_t launch_zero_pad_cols(DType t, void* base, int64_t ld, int64_t n_rows, int64_t v,
+                                hipStream_t stream);
+
+// ---------------------------------------------------------------- reductions
+// Sums per-row losses into the reference's scalars (api.rs:401-405):
+// out[0..3] = loss, student_ce, teacher_ce, kl (as float).
+struct FinalizeArgs {
+  const float* row_nll_s;
+  const float* row_nll_t;
+  const float* row_kl;
+  int64_t bt;
+  int64_t chunk_size;      // KL is summed per chunk then rounded to f32
+  float w_s, w_t, kd;
+  float mean_scale;
+  float* out;              // 4 floats
+};
+hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t stream);
+
+// ---------------------------------------------------------------- INT8 quant
+struct QuantArgs {
+  const float* src;        // [rows][cols]
+  int64_t lds;
+  float* dst;              // dequantized output (may equal src)
+  int64_t ldd;
+  int8_t* codes;           // may be null
+  int64_t ldq;
+  float* scales;           // may be null
+  const uint8_t* keep_exact;  // per-row flag: copy the source row exactly
+  int64_t rows, cols;
+  bool stochastic;
+  uint64_t seed;
+  float grad_output;
+};
+hipError_t launch_quant(const QuantArgs& a, hipStream_t stream);
+
+// keep[labels[i]] = 1 for every in-range, non-ignored label.
+hipError_t launch_mark_targets(const int64_t* labels, int64_t n, int64_t ignore_index,
+                               uint8_t* keep, int64_t rows, hipStream_t stream);
+
+// Strided 2-D copy with dtype conversion (f32<->bf16) and zero padding of
+// columns [cols, ldd).
+hipError_t launch_convert_rows(DType src_t, const void* src, int64_t lds, DType dst_t,
+                               void* dst, int64_t ldd, int64_t rows, int64_t cols,
+                               hipStream_t stream);
+
+}  // namespace orda

@@ -1,0 +1,139 @@
+// quant.hip — INT8 row-wise quantize/dequantize of grad_W on gfx950, and the
+// small element-wise helpers of the host orchestration.
+//
+// One workgroup per row (src/quant.rs:96-144, 157-202):
+//   s    = max(amax, 1e-12) / 127                (f32, IEEE division)
+//   code = clamp(RNE(x / s), -127, 127)           deterministic
+//   code = clamp(floor(x/s) + (frac > u), ...)    stochastic, u from SplitMix64
+//   out  = (target row ? x : code * s) * grad_output
+// The reference draws one SplitMix64 uniform per element in row-major order
+// over the whole matrix. SplitMix64 advances its state by a constant, so the
+// draw for flat element e is mix(seed + (e + 2)·γ) — computed here per
+// element, which reproduces the sequential stream bit for bit.
+#include <math.h>
+
+#include "orda_kernels.h"
+
+namespace orda {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr uint64_t kGamma = 0x9E3779B97F4A7C15ull;
+
+__device__ __forceinline__ uint64_t splitmix_mix(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// quant.rs:39-43 for the draw with index e of Rng::new(seed).
+__device__ __forceinline__ float uniform_at(uint64_t seed, uint64_t e) {
+  const uint64_t z = splitmix_mix(seed + (e + 2) * kGamma);
+  return static_cast<float>(z >> 40) * (1.0f / 16777216.0f);
+}
+
+__device__ __forceinline__ int8_t to_code(float v) {
+  if (isnan(v)) return 0;
+  v = fminf(fmaxf(v, -127.0f), 127.0f);
+  return static_cast<int8_t>(v);
+}
+
+__global__ __launch_bounds__(kThreads) void quant_kernel(QuantArgs a) {
+  __shared__ float red[kThreads / 64];
+  const int64_t r = blockIdx.x;
+  const float* src = a.src + r * a.lds;
+  float amax = 0.f;
+  for (int64_t c = threadIdx.x; c < a.cols; c += kThreads) amax = fmaxf(amax, fabsf(src[c]));
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = red[0];
+#pragma unroll
+  for (int w = 1; w < kThreads / 64; ++w) amax = fmaxf(amax, red[w]);
+  const float s = fmaxf(amax, 1e-12f) / 127.0f;
+  const bool keep = a.keep_exact && a.keep_exact[r];
+  float* dst = a.dst + r * a.ldd;
+  int8_t* q = a.codes ? a.codes + r * a.ldq : nullptr;
+  const uint64_t ebase = static_cast<uint64_t>(r) * static_cast<uint64_t>(a.cols);
+  for (int64_t c = threadIdx.x; c < a.cols; c += kThreads) {
+    const float x = src[c];
+    const float scaled = x / s;
+    int8_t code;
+    if (a.stochastic) {
+      const float fl = floorf(scaled);
+      const float u = uniform_at(a.seed, ebase + static_cast<uint64_t>(c));
+      code = to_code(fl + ((scaled - fl) > u ? 1.0f : 0.0f));
+    } else {
+      code = to_code(rintf(scaled));
+    }
+    if (q) q[c] = code;
+    const float deq = keep ? x : static_cast<float>(code) * s;
+    dst[c] = deq * a.grad_output;
+  }
+  if (a.scales && threadIdx.x == 0) a.scales[r] = s;
+}
+
+__global__ void mark_targets_kernel(const int64_t* labels, int64_t n, int64_t ignore,
+                                    uint8_t* keep, int64_t rows) {
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t t = labels[i];
+    if (t != ignore && t >= 0 && t < rows) keep[t] = 1;
+  }
+}
+
+template <typename S, typename D>
+__global__ void convert_rows_kernel(const S* src, int64_t lds, D* dst, int64_t ldd, int64_t rows,
+                                    int64_t cols) {
+  const int64_t total = rows * ldd;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t rr = i / ldd, cc = i % ldd;
+    dst[i] = cc < cols ? static_cast<D>(static_cast<float>(src[rr * lds + cc])) : static_cast<D>(0.f);
+  }
+}
+
+unsigned grid_for(int64_t total) {
+  int64_t b = (total + 255) / 256;
+  if (b > 65536) b = 65536;
+  if (b < 1) b = 1;
+  return static_cast<unsigned>(b);
+}
+
+}  // namespace
+
+hipError_t launch_quant(const QuantArgs& a, hipStream_t s) {
+  if (a.rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(quant_kernel, dim3(static_cast<unsigned>(a.rows)), dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_mark_targets(const int64_t* labels, int64_t n, int64_t ignore_index,
+                               uint8_t* keep, int64_t rows, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(mark_targets_kernel, dim3(grid_for(n)), dim3(256), 0, s, labels, n,
+                     ignore_index, keep, rows);
+  return hipGetLastError();
+}
+
+hipError_t launch_convert_rows(DType st, const void* src, int64_t lds, DType dt, void* dst,
+                               int64_t ldd, int64_t rows, int64_t cols, hipStream_t s) {
+  if (rows <= 0 || ldd <= 0) return hipSuccess;
+  const dim3 g(grid_for(rows * ldd)), b(256);
+  if (st == DType::F32 && dt == DType::F32)
+    hipLaunchKernelGGL((convert_rows_kernel<float, float>), g, b, 0, s,
+                       static_cast<const float*>(src), lds, static_cast<float*>(dst), ldd, rows, cols);
+  else if (st == DType::F32)
+    hipLaunchKernelGGL((convert_rows_kernel<float, __bf16>), g, b, 0, s,
+                       static_cast<const float*>(src), lds, static_cast<__bf16*>(dst), ldd, rows, cols);
+  else if (dt == DType::F32)
+    hipLaunchKernelGGL((convert_rows_kernel<__bf16, float>), g, b, 0, s,
+                       static_cast<const __bf16*>(src), lds, static_cast<float*>(dst), ldd, rows, cols);
+  else
+    hipLaunchKernelGGL((convert_rows_kernel<__bf16, __bf16>), g, b, 0, s,
+                       static_cast<const __bf16*>(src), lds, static_cast<__bf16*>(dst), ldd, rows, cols);
+  return hipGetLastError();
+}
+
+}  // namespace orda

@@ -1,0 +1,385 @@
+// rowpass.hip — the fused row pass of the distillation loss on gfx950.
+//
+// One workgroup owns one (student row, teacher row) pair of a logits chunk
+// (layout of src/api.rs:276-299: student rows, then teacher rows). From the
+// per-tile softmax statistics written by the logits GEMM it forms, per row,
+// lse at T=1 and at temperature T, then streams the two rows once:
+//   student grad = w_s·((p_s − α/V) − [j=y](1−α)) + kd·T·(p_s^T − p_t^T)
+//                                          (cross_entropy.rs:58-71, kl.rs:83-124,
+//                                           merge api.rs:335-344)
+//   teacher grad = w_t·((p_t − α/V) − [j=y](1−α))   (api.rs:325-333)
+// overwriting both rows in place, and accumulates Σ p_t^T·(x_t − x_s) so that
+//   KL_row = Σ p_t^T (x_t − x_s)/T + (lse_s^T − lse_t^T)·Σ p_t^T
+// comes out of the same pass. The per-row NLL uses the fp32 label logit and
+// Σx from the GEMM epilogue and is formed in f64 like the reference.
+// Exponentials are exp2 with log2(e) folded into one FMA per element.
+#include <math.h>
+
+#include "orda_kernels.h"
+
+namespace orda {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+struct Stat {
+  float m, d1, dT, sx;
+};
+
+__device__ __forceinline__ Stat merge(Stat a, Stat b, float it2) {
+  Stat r;
+  r.m = fmaxf(a.m, b.m);
+  r.sx = a.sx + b.sx;
+  if (r.m == -INFINITY) {
+    r.d1 = 0.f;
+    r.dT = 0.f;
+  } else {
+    r.d1 = a.d1 * __builtin_amdgcn_exp2f((a.m - r.m) * kLog2e) +
+           b.d1 * __builtin_amdgcn_exp2f((b.m - r.m) * kLog2e);
+    r.dT = a.dT * __builtin_amdgcn_exp2f((a.m - r.m) * it2) +
+           b.dT * __builtin_amdgcn_exp2f((b.m - r.m) * it2);
+  }
+  return r;
+}
+
+__device__ __forceinline__ Stat shfl_xor_stat(Stat s, int o) {
+  Stat r;
+  r.m = __shfl_xor(s.m, o);
+  r.d1 = __shfl_xor(s.d1, o);
+  r.dT = __shfl_xor(s.dT, o);
+  r.sx = __shfl_xor(s.sx, o);
+  return r;
+}
+
+// Block-wide merge of per-thread partial stats; every thread gets the result.
+__device__ Stat block_merge(Stat s, float it2, Stat* scratch) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) s = merge(s, shfl_xor_stat(s, o), it2);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[wave] = s;
+  __syncthreads();
+  Stat r = scratch[0];
+#pragma unroll
+  for (int w = 1; w < kThreads / 64; ++w) r = merge(r, scratch[w], it2);
+  return r;
+}
+
+__device__ float block_sum(float v, float* scratch) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[wave] = v;
+  __syncthreads();
+  float r = 0.f;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) r += scratch[w];
+  return r;
+}
+
+__device__ Stat load_row_stats(const float4* st, int64_t tiles, float it2, Stat* scratch) {
+  Stat s{-INFINITY, 0.f, 0.f, 0.f};
+  for (int64_t t = threadIdx.x; t < tiles; t += kThreads) {
+    const float4 v = st[t];
+    s = merge(s, Stat{v.x, v.y, v.z, v.w}, it2);
+  }
+  return block_merge(s, it2, scratch);
+}
+
+// Vector of logits in storage type LT <-> fp32.
+template <typename LT>
+struct Vec;
+template <>
+struct Vec<float> {
+  static constexpr int N = 4;
+  typedef u32x4 raw;
+  static __device__ __forceinline__ void unpack(raw r, float (&x)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] = __uint_as_float(r[i]);
+  }
+  static __device__ __forceinline__ raw pack(const float (&x)[N]) {
+    raw r;
+#pragma unroll
+    for (int i = 0; i < N; ++i) r[i] = __float_as_uint(x[i]);
+    return r;
+  }
+};
+template <>
+struct Vec<__bf16> {
+  static constexpr int N = 8;
+  typedef u32x4 raw;
+  static __device__ __forceinline__ void unpack(raw r, float (&x)[N]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = __uint_as_float(r[i] << 16);
+      x[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
+    }
+  }
+  static __device__ __forceinline__ raw pack(const float (&x)[N]) {
+    raw r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const __bf16 lo = static_cast<__bf16>(x[2 * i]);
+      const __bf16 hi = static_cast<__bf16>(x[2 * i + 1]);
+      r[i] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
+             (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
+    }
+    return r;
+  }
+};
+
+// nll of cross_entropy.rs:46-56 from merged stats, in f64.
+__device__ __forceinline__ double row_nll(const Stat& s, float xy, double alpha, int64_t v) {
+  const double lse = static_cast<double>(s.m) + log(static_cast<double>(s.d1));
+  if (alpha > 0.0)
+    return lse - (1.0 - alpha) * static_cast<double>(xy) -
+           (alpha / static_cast<double>(v)) * static_cast<double>(s.sx);
+  return lse - static_cast<double>(xy);
+}
+
+template <typename LT, bool SPLIT>
+__global__ __launch_bounds__(kThreads) void row_pass_kernel(RowPassArgs a) {
+  __shared__ Stat sstat[kThreads / 64];
+  __shared__ float ssum[kThreads / 64];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t y = a.labels[r];
+  const bool ignored = (y == a.ignore_index);
+  const bool has_t = a.teacher != nullptr;
+  const float T = a.temperature;
+  const float inv_t = SPLIT ? a.inv_t : 1.0f / T;
+  const float it2 = inv_t * kLog2e;
+
+  const Stat ss = load_row_stats(a.stats_s + r * a.stats_ld, a.stats_tiles, it2, sstat);
+  Stat st{-INFINITY, 0.f, 0.f, 0.f};
+  if (has_t) st = load_row_stats(a.stats_t + r * a.stats_ld, a.stats_tiles_t, it2, sstat);
+
+  const double alpha = static_cast<double>(a.label_smoothing);
+  // Per-row constants: p = exp2(x*log2e - off).
+  const float lse1_s = ss.m + logf(ss.d1);
+  const float lseT_s = ss.m * inv_t + logf(ss.dT);
+  const float lse1_t = st.m + logf(st.d1);
+  const float lseT_t = st.m * inv_t + logf(st.dT);
+  const float o1s = lse1_s * kLog2e, oTs = lseT_s * kLog2e;
+  const float o1t = lse1_t * kLog2e, oTt = lseT_t * kLog2e;
+
+  const float eps = static_cast<float>(alpha / static_cast<double>(a.v));
+  const float one_m_a = 1.0f - a.label_smoothing;
+  // CE scales (ignored rows -> 0, cross_entropy.rs:59).
+  const float ws = ignored ? 0.f : a.w_s;
+  const float wt = ignored ? 0.f : a.w_t;
+  const bool do_kl = a.kl && has_t;
+  const float gsc = ignored ? 0.f : (SPLIT ? a.kl_grad_scale : a.kd * T);  // kl.rs:85
+  const bool do_tgrad = SPLIT ? (!a.student_only && has_t) : (a.teacher_grad && has_t);
+
+  LT* srow = static_cast<LT*>(a.student) + r * a.ld;
+  LT* trow = has_t ? static_cast<LT*>(a.teacher) + r * a.ld : nullptr;
+  float* gkl = SPLIT ? a.grad_kl + r * a.v : nullptr;
+  float* gce_s = SPLIT ? a.grad_ce + r * a.v : nullptr;
+  float* gce_t = (SPLIT && do_tgrad) ? a.grad_ce + (a.n_rows + r) * a.v : nullptr;
+
+  using VT = Vec<LT>;
+  constexpr int NV = VT::N;
+  float cross = 0.f, sum_pt = 0.f;
+  const int64_t vpad = (a.v + NV - 1) / NV * NV;
+  for (int64_t j0 = static_cast<int64_t>(tid) * NV; j0 < vpad; j0 += kThreads * NV) {
+    float xs[NV], xt[NV], gs[NV], gt[NV];
+    VT::unpack(*reinterpret_cast<const typename VT::raw*>(srow + j0), xs);
+    if (has_t) VT::unpack(*reinterpret_cast<const typename VT::raw*>(trow + j0), xt);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t j = j0 + i;
+      const bool valid = j < a.v;
+      float g = 0.f, gkv = 0.f, gtv = 0.f;
+      if (valid) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(xs[i], kLog2e, -o1s));
+        float prob = p - eps;
+        if (j == y) prob -= one_m_a;
+        g = prob * ws;
+        if (do_kl) {
+          const float ps = __builtin_amdgcn_exp2f(fmaf(xs[i], it2, -oTs));
+          const float pt = __builtin_amdgcn_exp2f(fmaf(xt[i], it2, -oTt));
+          gkv = gsc * (ps - pt);
+          cross = fmaf(pt, xt[i] - xs[i], cross);
+          sum_pt += pt;
+        }
+        if (do_tgrad) {
+          const float q = __builtin_amdgcn_exp2f(fmaf(xt[i], kLog2e, -o1t));
+          float pr = q - eps;
+          if (j == y) pr -= one_m_a;
+          gtv = pr * wt;
+        }
+      }
+      if (SPLIT) {
+        if (valid) {
+          gce_s[j] = g;
+          if (do_kl) gkl[j] = gkv;
+          if (do_tgrad) gce_t[j] = gtv;
+        }
+      } else {
+        gs[i] = ignored ? 0.f : g + gkv;
+        gt[i] = gtv;
+      }
+    }
+    if (!SPLIT) {
+      *reinterpret_cast<typename VT::raw*>(srow + j0) = VT::pack(gs);
+      if (do_tgrad) *reinterpret_cast<typename VT::raw*>(trow + j0) = VT::pack(gt);
+    }
+  }
+  if (SPLIT && !do_kl && a.grad_kl) {
+    for (int64_t j = tid; j < a.v; j += kThreads) gkl[j] = 0.f;
+  }
+
+  if (do_kl) {
+    cross = block_sum(cross, ssum);
+    sum_pt = block_sum(sum_pt, ssum);
+  }
+  if (tid == 0) {
+    const float xy_s = ignored ? 0.f : a.xy_s[r];
+    const double nll_s = ignored ? 0.0 : row_nll(ss, xy_s, alpha, a.v);
+    float kl_row = 0.f;
+    if (do_kl && !ignored) {
+      const float t_sq = SPLIT ? a.t_sq : T * T;   // kl.rs:86
+      kl_row = (cross * inv_t + (lseT_s - lseT_t) * sum_pt) * t_sq;
+    }
+    double nll_t = 0.0;
+    const bool tce = SPLIT ? (!a.student_only && has_t) : (a.teacher_ce && has_t);
+    if (tce && !ignored) nll_t = row_nll(st, a.xy_t[r], alpha, a.v);
+    if (SPLIT) {
+      a.ce_loss[r] = static_cast<float>(nll_s);
+      if (tce) a.ce_loss[a.n_rows + r] = static_cast<float>(nll_t);
+      if (a.row_kl) a.row_kl[r] = kl_row;
+    } else {
+      a.row_nll_s[r] = static_cast<float>(nll_s);
+      a.row_nll_t[r] = static_cast<float>(nll_t);
+      a.row_kl[r] = kl_row;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ row stats
+template <typename ST, typename DT>
+__global__ __launch_bounds__(kThreads) void row_stats_kernel(RowStatsArgs a) {
+  __shared__ Stat sstat[kThreads / 64];
+  const int64_t r = blockIdx.x;
+  const ST* src = static_cast<const ST*>(a.src) + r * a.lds;
+  DT* dst = a.dst ? static_cast<DT*>(a.dst) + r * a.ldd : nullptr;
+  const float it2 = a.inv_t * kLog2e;
+  Stat s{-INFINITY, 0.f, 0.f, 0.f};
+  for (int64_t j = threadIdx.x; j < a.v; j += kThreads) {
+    const float x = static_cast<float>(src[j]);
+    if (dst) dst[j] = static_cast<DT>(x);
+    s = merge(s, Stat{x, 1.f, 1.f, x}, it2);
+  }
+  if (dst)
+    for (int64_t j = a.v + threadIdx.x; j < a.ldd; j += kThreads) dst[j] = static_cast<DT>(0.f);
+  s = block_merge(s, it2, sstat);
+  if (threadIdx.x == 0) {
+    a.stats[r * a.stats_ld] = make_float4(s.m, s.d1, s.dT, s.sx);
+    if (a.labels) {
+      const int64_t y = a.labels[r];
+      if (y != a.ignore_index && y >= 0 && y < a.v) a.xy[r] = static_cast<float>(src[y]);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ finalize
+__global__ __launch_bounds__(kThreads) void finalize_kernel(FinalizeArgs a) {
+  __shared__ double red[3][kThreads];
+  double s_nll = 0.0, t_nll = 0.0, kl = 0.0;
+  for (int64_t i = threadIdx.x; i < a.bt; i += kThreads) {
+    s_nll += static_cast<double>(a.row_nll_s[i]);
+    t_nll += static_cast<double>(a.row_nll_t[i]);
+  }
+  // KL is accumulated per chunk and rounded to f32 (api.rs:304-314 with
+  // kl.rs:126).
+  const int64_t nc = (a.bt + a.chunk_size - 1) / a.chunk_size;
+  for (int64_t c = threadIdx.x; c < nc; c += kThreads) {
+    const int64_t e = (c + 1) * a.chunk_size < a.bt ? (c + 1) * a.chunk_size : a.bt;
+    double k = 0.0;
+    for (int64_t i = c * a.chunk_size; i < e; ++i) k += static_cast<double>(a.row_kl[i]);
+    kl += static_cast<double>(static_cast<float>(k));
+  }
+  red[0][threadIdx.x] = s_nll;
+  red[1][threadIdx.x] = t_nll;
+  red[2][threadIdx.x] = kl;
+  __syncthreads();
+  for (int w = kThreads / 2; w > 0; w >>= 1) {
+    if (threadIdx.x < w)
+      for (int q = 0; q < 3; ++q) red[q][threadIdx.x] += red[q][threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const double ms = static_cast<double>(a.mean_scale);
+    const double S = red[0][0], Tt = red[1][0], K = red[2][0];
+    a.out[0] = static_cast<float>((static_cast<double>(a.w_s) * S +
+                                   static_cast<double>(a.w_t) * Tt +
+                                   static_cast<double>(a.kd) * K) * ms);
+    a.out[1] = static_cast<float>(S * ms);
+    a.out[2] = static_cast<float>(Tt * ms);
+    a.out[3] = static_cast<float>(K * ms);
+  }
+}
+
+template <typename T>
+__global__ void zero_pad_kernel(T* base, int64_t ld, int64_t n_rows, int64_t v) {
+  const int64_t w = ld - v;
+  const int64_t total = n_rows * w;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    base[(i / w) * ld + v + i % w] = static_cast<T>(0.f);
+}
+
+}  // namespace
+
+hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
+  if (a.n_rows <= 0) return hipSuccess;
+  if (a.ld % 8) return hipErrorInvalidValue;
+  dim3 grid(static_cast<unsigned>(a.n_rows));
+  if (a.ltype == DType::BF16) {
+    if (a.split) hipLaunchKernelGGL((row_pass_kernel<__bf16, true>), grid, dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL((row_pass_kernel<__bf16, false>), grid, dim3(kThreads), 0, s, a);
+  } else {
+    if (a.split) hipLaunchKernelGGL((row_pass_kernel<float, true>), grid, dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL((row_pass_kernel<float, false>), grid, dim3(kThreads), 0, s, a);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_row_stats(const RowStatsArgs& a, hipStream_t s) {
+  if (a.n_rows <= 0) return hipSuccess;
+  dim3 grid(static_cast<unsigned>(a.n_rows));
+  const bool sf = a.src_type == DType::F32;
+  const bool df = a.dst_type == DType::F32;
+  if (sf && df) hipLaunchKernelGGL((row_stats_kernel<float, float>), grid, dim3(kThreads), 0, s, a);
+  else if (sf) hipLaunchKernelGGL((row_stats_kernel<float, __bf16>), grid, dim3(kThreads), 0, s, a);
+  else if (df) hipLaunchKernelGGL((row_stats_kernel<__bf16, float>), grid, dim3(kThreads), 0, s, a);
+  else hipLaunchKernelGGL((row_stats_kernel<__bf16, __bf16>), grid, dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_zero_pad_cols(DType t, void* base, int64_t ld, int64_t n_rows, int64_t v,
+                                hipStream_t s) {
+  if (ld <= v || n_rows <= 0) return hipSuccess;
+  const int64_t total = n_rows * (ld - v);
+  const unsigned blocks = static_cast<unsigned>(total / 256 + 1 < 4096 ? total / 256 + 1 : 4096);
+  if (t == DType::BF16)
+    hipLaunchKernelGGL(zero_pad_kernel<__bf16>, dim3(blocks), dim3(256), 0, s,
+                       static_cast<__bf16*>(base), ld, n_rows, v);
+  else
+    hipLaunchKernelGGL(zero_pad_kernel<float>, dim3(blocks), dim3(256), 0, s,
+                       static_cast<float*>(base), ld, n_rows, v);
+  return hipGetLastError();
+}
+
+}  // namespace orda

@@ -1,0 +1,111 @@
+"""CPU-side checks of the C ABI library (no GPU needed): it loads, exports
+every entry point include/orda/orda.h declares, and its host logic (chunk
+resolver, doubling schedule, option defaults, config validation) agrees with
+the oracle and the reference's known answers."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle as O
+import orda_hip as H
+from orda_hip import _lib as L
+from orda_hip.types import ChunkSize
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "orda", "orda.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(orda_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.load()
+    names = declared_functions()
+    assert len(names) >= 20
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in orda.h but not exported"
+    # and the ctypes signature table covers the same set
+    assert sorted(n for n, _, _ in L.SIGNATURES) == names
+
+
+def test_abi_version_and_availability_without_gpu():
+    lib = L.load()
+    assert lib.orda_abi_version() == 1
+    avail = H.is_available()
+    assert avail in (True, False)
+
+
+def test_struct_layouts_match_header_sizes():
+    # orda_tensor: ptr + 3*i64 + 2*i32 = 40 bytes
+    assert C.sizeof(L.Tensor) == 40
+    assert C.sizeof(L.TeacherC) == 8 + 3 * 40
+
+
+@pytest.mark.parametrize("bt", [1, 2, 7, 100, 511, 512, 513, 1000, 2048, 4096, 8192, 10000])
+@pytest.mark.parametrize("v", [None, 1, 7, 8192, 32000, 65536, 131072, 262144])
+@pytest.mark.parametrize("mc", [None, 1, 3, 16])
+def test_resolver_matches_oracle(bt, v, mc):
+    for cs in (ChunkSize.Auto, ChunkSize.Fixed(1), ChunkSize.Fixed(256), ChunkSize.Fixed(bt + 5)):
+        a = H.resolve_chunk_size(bt, cs, v, mc)
+        b = O.resolve_chunk_size(bt, cs, v, mc)
+        assert (a.chunk_size, a.num_chunks) == (b.chunk_size, b.num_chunks)
+
+
+def test_resolver_known_answers_via_abi():
+    assert H.resolve_chunk_size(8192, ChunkSize.Auto, 131072, None) == H.ChunkPlan(512, 16)
+    assert H.resolve_chunk_size(1000, ChunkSize.Fixed(256), None, None) == H.ChunkPlan(256, 4)
+    assert H.resolve_chunk_size(100, ChunkSize.Fixed(4096), None, None) == H.ChunkPlan(100, 1)
+    assert H.resolve_chunk_size(8192, ChunkSize.Auto, None, None) == H.ChunkPlan(8192, 1)
+    for raw, n in [(0.0, 1), (1.49, 1), (1.5, 2), (3.0, 4), (6.0, 8), (1e300, 1 << 60)]:
+        assert H.chunks_from_raw(raw) == n == O.chunks_from_raw(raw)
+    assert H.chunk_doubling_schedule(10_000, 4, 32) == [4, 8, 16, 32]
+    assert H.chunk_doubling_schedule(20, 4, 1000) == [4, 8, 16, 20]
+    for bt, st, lim in [(1, 1, 1), (9, 0, 3), (100, 7, 0), (4096, 3, 4096), (37, 40, 64)]:
+        assert H.chunk_doubling_schedule(bt, st, lim) == O.chunk_doubling_schedule(bt, st, lim)
+        assert H.default_max_chunks_limit(bt) == O.default_max_chunks_limit(bt)
+
+
+def test_option_defaults_match_reference():
+    """LossOptions::default (api.rs:49-64) and KernelConfig (config.rs:68-90)."""
+    c = L.LossOptionsC()
+    L.load().orda_loss_options_default(C.byref(c))
+    assert c.student_ce_weight == 1.0 and c.has_teacher_ce_weight == 0
+    assert c.kd_weight == 0.0 and c.temperature == 1.0 and c.ignore_index == -100
+    assert c.label_smoothing == 0.0 and c.reduction == 0 and c.chunk_fixed == 0
+    assert c.backend == 0 and c.config.max_fused_size == 32768
+    assert not c.config.fast_math and not c.config.quantize_grad_weight
+    k = L.KernelConfigC()
+    L.load().orda_kernel_config_from_profile(1, C.byref(k))
+    assert k.fast_math == 1
+    L.load().orda_kernel_config_from_profile(2, C.byref(k))
+    assert k.fast_math == 0
+
+
+def test_config_validate_messages():
+    k = L.KernelConfigC()
+    L.load().orda_kernel_config_from_profile(0, C.byref(k))
+    err = C.create_string_buffer(256)
+    assert L.load().orda_kernel_config_validate(C.byref(k), err, 256) == 0
+    k.max_fused_size = 100
+    assert L.load().orda_kernel_config_validate(C.byref(k), err, 256) == 1
+    assert err.value.decode() == "max_fused_size must be a power of two >= 1, got 100"
+    k.max_fused_size = 1024
+    k.has_max_chunks, k.max_chunks = 1, 0
+    assert L.load().orda_kernel_config_validate(C.byref(k), err, 256) == 1
+    assert err.value.decode() == "max_chunks must be >= 1, got 0"
+
+
+def test_no_gpu_fails_loudly_not_silently():
+    """Without a device the loss must raise, never fall back to a CPU path."""
+    if H.is_available():
+        pytest.skip("a GPU is visible")
+    s = np.zeros((4, 8), np.float32)
+    w = np.zeros((16, 8), np.float32)
+    with pytest.raises(H.OrdaError):
+        H.distillation_loss(s, w, np.zeros(4, np.int64), H.Teacher.Tied(s), H.LossOptions())

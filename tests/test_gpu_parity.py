@@ -1,0 +1,350 @@
+"""GPU parity: liborda_hip.so (through the C ABI) against the CPU oracle on
+identical seeded inputs. Tolerances are stated in tests/parity.py.
+
+Cases: the reference's own end-to-end cases (tests/end_to_end.rs, tiny odd
+shapes that exercise every tail and padding path), the Tied
+256/512/8192 fp32 shape in full, and reduced versions of the four larger
+shapes (same mode, dtype and options; sizes the oracle finishes in seconds).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import bf16_round, labels, mat, normal, uniform_labels
+from parity import check_grad, check_output, check_scalar, to_np
+
+import orda_hip as H
+from orda_hip import (ChunkSize, KernelConfig, LossOptions, OrdaError, Reduction, Teacher)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a visible GPU"
+    assert H.is_available(), "liborda_hip.so does not see a gfx950 device"
+    return torch, torch.device("cuda:0")
+
+
+def gpu(torch_dev, a, dtype=None):
+    torch, dev = torch_dev
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    if dtype == "bf16":
+        t = t.to(torch.bfloat16)
+    return t
+
+
+def gpu_teacher(torch_dev, teacher, dtype=None):
+    m = teacher.mode()
+    if m == H.TeacherMode.Tied:
+        return Teacher.Tied(gpu(torch_dev, teacher.hidden, dtype))
+    if m == H.TeacherMode.Separate:
+        return Teacher.Separate(gpu(torch_dev, teacher.hidden, dtype),
+                                gpu(torch_dev, teacher.weight, dtype))
+    return Teacher.Precomputed(gpu(torch_dev, teacher.logits))
+
+
+def run_pair(torch_dev, s, w, y, teacher, opts, dtype=None):
+    """(gpu output, oracle output); bf16 runs feed the oracle the rounded values."""
+    if dtype == "bf16":
+        s, w = bf16_round(s), bf16_round(w)
+        if teacher.hidden is not None:
+            teacher = Teacher(teacher.mode(), hidden=bf16_round(teacher.hidden),
+                              weight=None if teacher.weight is None else bf16_round(teacher.weight),
+                              logits=teacher.logits)
+    got = H.distillation_loss(gpu(torch_dev, s, dtype), gpu(torch_dev, w, dtype),
+                              gpu(torch_dev, y), gpu_teacher(torch_dev, teacher, dtype), opts,
+                              rows=True, quant_codes=True)
+    ref = O.distillation_loss(s, w, y, teacher, opts)
+    return got, ref
+
+
+def base_opts(**kw):
+    d = dict(student_ce_weight=1.0, kd_weight=0.5, temperature=1.5)
+    d.update(kw)
+    return LossOptions(**d)
+
+
+# ------------------------------------------------ reference end-to-end cases
+def test_tied_small(torch_dev):
+    bt, h, v = 6, 5, 7
+    got, ref = run_pair(torch_dev, mat(bt, h, 1, 0.3), mat(v, h, 2, 0.2), labels(bt, v, 4),
+                        Teacher.Tied(mat(bt, h, 3, 0.3)),
+                        base_opts(teacher_ce_weight=1.0, label_smoothing=0.1))
+    check_output(got, ref)
+
+
+def test_separate_small(torch_dev):
+    bt, h, ht, v = 6, 5, 4, 7
+    got, ref = run_pair(torch_dev, mat(bt, h, 11, 0.3), mat(v, h, 12, 0.2), labels(bt, v, None),
+                        Teacher.Separate(mat(bt, ht, 13, 0.3), mat(v, ht, 14, 0.2)),
+                        base_opts(teacher_ce_weight=0.7))
+    check_output(got, ref)
+
+
+def test_precomputed_small(torch_dev):
+    bt, h, v = 6, 5, 7
+    got, ref = run_pair(torch_dev, mat(bt, h, 21, 0.3), mat(v, h, 22, 0.2), labels(bt, v, 5),
+                        Teacher.Precomputed(mat(bt, v, 23, 0.5)), base_opts())
+    assert got.grad_teacher_hidden is None and got.grad_teacher_weight is None
+    check_output(got, ref)
+
+
+def test_pure_student_small(torch_dev):
+    bt, h, v = 8, 4, 6
+    got, ref = run_pair(torch_dev, mat(bt, h, 31, 0.3), mat(v, h, 32, 0.2), labels(bt, v, None),
+                        Teacher.Tied(np.zeros((bt, h), np.float32)),
+                        LossOptions(kd_weight=0.0, teacher_ce_weight=0.0))
+    assert got.teacher_ce == 0.0 and got.kl == 0.0
+    check_output(got, ref)
+
+
+@pytest.mark.parametrize("cs", [ChunkSize.Fixed(16), ChunkSize.Fixed(1), ChunkSize.Fixed(3),
+                                ChunkSize.Auto])
+def test_chunking_small(torch_dev, cs):
+    bt, h, v = 16, 5, 9
+    got, ref = run_pair(torch_dev, mat(bt, h, 41, 0.3), mat(v, h, 42, 0.2), labels(bt, v, 3),
+                        Teacher.Tied(mat(bt, h, 43, 0.3)),
+                        base_opts(chunk_size=cs, teacher_ce_weight=1.0))
+    check_output(got, ref)
+
+
+def test_sum_reduction_small(torch_dev):
+    bt, h, v = 8, 4, 6
+    got, ref = run_pair(torch_dev, mat(bt, h, 61, 0.3), mat(v, h, 62, 0.2), labels(bt, v, 4),
+                        Teacher.Tied(mat(bt, h, 63, 0.3)),
+                        base_opts(reduction=Reduction.Sum, teacher_ce_weight=1.0))
+    check_output(got, ref)
+
+
+def test_int8_small(torch_dev):
+    bt, h, v = 8, 4, 20
+    got, ref = run_pair(torch_dev, mat(bt, h, 71, 0.3), mat(v, h, 72, 0.2), labels(bt, v, None),
+                        Teacher.Tied(mat(bt, h, 73, 0.3)),
+                        base_opts(teacher_ce_weight=1.0,
+                                  config=KernelConfig(quantize_grad_weight=True)))
+    check_output(got, ref, skip_grad_weight=True)
+    check_quantized_grad_weight(got, ref, labels(bt, v, None))
+
+
+def check_quantized_grad_weight(got, ref, y, ignore=-100):
+    """Dequantized grad_W: target rows carry the exact gradient (fp32 path
+    tolerance); other rows are code*scale with codes within ±1 of the
+    oracle's (grad_W itself differs in its last bits, so a code may flip at a
+    rounding boundary) and scales within 1e-3 relative."""
+    gw, rw = to_np(got.grad_weight), ref.grad_weight
+    gq, rq = to_np(got.quant_codes).astype(np.int32), ref.quant_codes.astype(np.int32)
+    gs, rs = to_np(got.quant_scales).reshape(-1), ref.quant_scales
+    tgt = sorted({int(t) for t in y if t != ignore})
+    assert np.all(np.abs(gq - rq) <= 1)
+    assert np.mean(gq != rq) < 0.01
+    np.testing.assert_allclose(gs, rs, rtol=1e-3, atol=1e-30)
+    mask = np.zeros(rw.shape[0], bool)
+    mask[tgt] = True
+    if tgt:
+        check_grad("grad_weight[target rows]", gw[mask], rw[mask])
+    # non-target rows are exactly code * scale
+    np.testing.assert_array_equal(gw[~mask], (gq[~mask] * gs[~mask, None]).astype(np.float32))
+
+
+# ------------------------------------------------ benchmark-shape cases
+def test_tied_256_512_8192_fp32(torch_dev):
+    """Tied 256/512/8192 fp32, kd 0.4, T 1.5, no smoothing, mean, Auto chunks."""
+    bt, h, v = 256, 512, 8192
+    s, th = normal((bt, h), 1), normal((bt, h), 2)
+    w = normal((v, h), 3, 0.02)
+    y = uniform_labels(bt, v, 5)
+    got, ref = run_pair(torch_dev, s, w, y, Teacher.Tied(th),
+                        LossOptions(kd_weight=0.4, temperature=1.5))
+    check_output(got, ref)
+    assert (got.chunk_plan.chunk_size, got.chunk_plan.num_chunks) == (256, 1)
+    np.testing.assert_allclose(to_np(got.row_nll_student), ref.row_nll_student, rtol=1e-4)
+    np.testing.assert_allclose(to_np(got.row_kl), ref.row_kl, rtol=1e-3, atol=1e-5)
+
+
+def test_tied_reduced_fp32_multichunk(torch_dev):
+    """Tied fp32 at a reduced shape with a non-power-of-two vocabulary and
+    four chunks (one backward group)."""
+    bt, h, v = 512, 256, 3200
+    s, th = normal((bt, h), 11), normal((bt, h), 12)
+    w = normal((v, h), 13, 0.02)
+    y = uniform_labels(bt, v, 15)
+    got, ref = run_pair(torch_dev, s, w, y, Teacher.Tied(th),
+                        LossOptions(kd_weight=0.4, temperature=1.5,
+                                    chunk_size=ChunkSize.Fixed(128)))
+    check_output(got, ref)
+
+
+def test_separate_reduced_fp32(torch_dev):
+    """Separate teacher: Hs != Ht, kd 0.5, T 2, smoothing 0.1, teacher CE weight 1."""
+    bt, hs, ht, v = 256, 128, 256, 3000
+    s = normal((bt, hs), 21)
+    ws = normal((v, hs), 22, 0.02)
+    th = normal((bt, ht), 23)
+    wt = normal((v, ht), 24, 0.015)
+    y = uniform_labels(bt, v, 25)
+    got, ref = run_pair(torch_dev, s, ws, y, Teacher.Separate(th, wt),
+                        LossOptions(kd_weight=0.5, temperature=2.0, label_smoothing=0.1,
+                                    teacher_ce_weight=1.0, chunk_size=ChunkSize.Fixed(64)))
+    check_output(got, ref)
+
+
+def test_separate_default_teacher_weight(torch_dev):
+    """Separate with the default teacher-CE weight 0: no teacher gradients."""
+    bt, hs, ht, v = 128, 64, 96, 1000
+    got, ref = run_pair(torch_dev, normal((bt, hs), 1), normal((v, hs), 2, 0.05),
+                        uniform_labels(bt, v, 3),
+                        Teacher.Separate(normal((bt, ht), 4), normal((v, ht), 5, 0.05)),
+                        LossOptions(kd_weight=0.5, temperature=2.0))
+    assert got.grad_teacher_hidden is None and got.grad_teacher_weight is None
+    check_output(got, ref)
+
+
+def test_precomputed_reduced_fp32(torch_dev):
+    """Precomputed peaked teacher: N(0, 2²) + 8 at the label, kd 0.7, T 1."""
+    bt, h, v = 256, 256, 4096
+    s = normal((bt, h), 31)
+    w = normal((v, h), 32, 0.02)
+    y = uniform_labels(bt, v, 35)
+    tl = normal((bt, v), 36, 2.0)
+    tl[np.arange(bt), y] += 8.0
+    got, ref = run_pair(torch_dev, s, w, y, Teacher.Precomputed(tl),
+                        LossOptions(kd_weight=0.7, temperature=1.0,
+                                    chunk_size=ChunkSize.Fixed(64)))
+    check_output(got, ref)
+
+
+def test_tied_reduced_bf16_int8(torch_dev):
+    """bf16 inputs (fp32 accumulation), kd 0.4, T 1.5, smoothing 0.1, INT8 grad_W."""
+    bt, h, v = 512, 256, 4096
+    s, th = normal((bt, h), 41), normal((bt, h), 42)
+    w = normal((v, h), 43, 0.02)
+    y = uniform_labels(bt, v, 45)
+    opts = LossOptions(kd_weight=0.4, temperature=1.5, label_smoothing=0.1,
+                       chunk_size=ChunkSize.Fixed(128),
+                       config=KernelConfig(quantize_grad_weight=True))
+    got, ref = run_pair(torch_dev, s, w, y, Teacher.Tied(th), opts, dtype="bf16")
+    check_output(got, ref, kind="bf16", skip_grad_weight=True)
+    gw, rw = to_np(got.grad_weight), ref.grad_weight
+    check_grad("grad_weight (dequantized)", gw, rw, "bf16")
+
+
+def test_ignored_labels_and_reductions(torch_dev):
+    bt, h, v = 200, 64, 777
+    s, th = normal((bt, h), 51), normal((bt, h), 52)
+    w = normal((v, h), 53, 0.1)
+    y = uniform_labels(bt, v, 54)
+    y[::3] = -7
+    for red in (Reduction.Mean, Reduction.Sum):
+        got, ref = run_pair(torch_dev, s, w, y, Teacher.Tied(th),
+                            LossOptions(kd_weight=0.3, temperature=0.7, label_smoothing=0.2,
+                                        ignore_index=-7, reduction=red,
+                                        chunk_size=ChunkSize.Fixed(48)))
+        check_output(got, ref)
+        assert np.all(to_np(got.row_nll_student)[::3] == 0.0)
+
+
+def test_all_labels_ignored(torch_dev):
+    bt, h, v = 32, 16, 50
+    y = np.full(bt, -100)
+    got, ref = run_pair(torch_dev, normal((bt, h), 1), normal((v, h), 2, 0.1), y,
+                        Teacher.Tied(normal((bt, h), 3)), LossOptions(kd_weight=0.5))
+    check_output(got, ref)
+    assert got.loss == 0.0 and np.all(to_np(got.grad_weight) == 0.0)
+
+
+# ------------------------------------------------ entry points and host logic
+@pytest.mark.parametrize("stochastic", [False, True])
+def test_quant_entry_point_bit_exact(torch_dev, stochastic):
+    """orda_quant_rows_int8 on the same fp32 matrix as the oracle: codes,
+    scales and the dequantized matrix are identical (quant.rs:96-202)."""
+    rng = np.random.default_rng(9)
+    m = (rng.standard_normal((300, 257)) * rng.uniform(0.001, 3, (300, 1))).astype(np.float32)
+    m[5] = 0.0
+    m[7, :10] = [0.5, 1.5, 2.5, -0.5, -1.5, 127, -127, 63.5, -63.5, 0.0]
+    targets = np.array([3, 3, 17, -100, 299, 0])
+    out, q, s = H.quant_rows_int8(gpu(torch_dev, m), gpu(torch_dev, targets), -100, stochastic,
+                                  seed=12345)
+    rout, rq, rs = O.quant_dequant_grad_w(m, targets, -100, stochastic, 12345)
+    np.testing.assert_array_equal(to_np(q), rq)
+    np.testing.assert_array_equal(to_np(s), rs)
+    np.testing.assert_array_equal(to_np(out), rout)
+
+
+def test_kl_ce_chunk_entry_point(torch_dev):
+    """The chunk launcher slot (src/cuda/launch.rs:51-158) against kl_chunk
+    and ce_fwdbwd_row."""
+    n, v = 24, 1003
+    rng = np.random.default_rng(4)
+    lc = (rng.standard_normal((2 * n, v)) * 2).astype(np.float32)
+    y = rng.integers(0, v, n).astype(np.int32)
+    y[::5] = -100
+    T, kd, ws_, wt_, ls = 1.5, 0.4, 1.0, 0.8, 0.1
+    for student_only in (False, True):
+        got = H.kl_ce_on_logits_chunk(gpu(torch_dev, lc), gpu(torch_dev, y), n, 1.0 / T,
+                                      kd * T, T * T, ws_, wt_, ls, -100, student_only, True)
+        kl, gkl = O.kl_chunk(lc, y.astype(np.int64), n, kd, T, -100, 1.0, True)
+        check_grad("grad_kl_student", got["grad_kl_student"], gkl)
+        rows = n if student_only else 2 * n
+        for r in range(rows):
+            scale = ws_ if r < n else wt_
+            nll, g = O.ce_fwdbwd_row(lc[r], int(y[r % n]), -100, ls, scale)
+            check_scalar(f"ce_loss[{r}]", float(to_np(got["ce_loss"])[r]), nll)
+            check_grad(f"grad_ce[{r}]", to_np(got["grad_ce"])[r], g)
+        check_scalar("sum kl_per_row", float(np.sum(to_np(got["kl_per_row"]), dtype=np.float64)), kl)
+
+
+def test_validation_errors_match_reference(torch_dev):
+    s = gpu(torch_dev, mat(4, 3, 1, 0.3))
+    w = gpu(torch_dev, mat(5, 3, 2, 0.2))
+    t = Teacher.Tied(gpu(torch_dev, mat(4, 3, 3, 0.3)))
+    cases = [
+        (np.array([0, 1, 5, 2]), LossOptions(), "label 5 out of range [0, 5) and != ignore_index -100"),
+        (np.array([0, 1, 2]), LossOptions(), "labels must have length BT=4, got 3"),
+        (np.array([0, 1, 2, 3]), LossOptions(label_smoothing=1.5), "label_smoothing must be in [0,1], got 1.5"),
+        (np.array([0, 1, 2, 3]), LossOptions(temperature=0.0), "temperature must be > 0, got 0"),
+        (np.array([0, 1, 2, 3]), LossOptions(kd_weight=-1.0), "kd_weight must be >= 0, got -1"),
+        (np.array([0, 1, 2, 3]), LossOptions(teacher_ce_weight=-0.5), "teacher_ce_weight must be >= 0, got -0.5"),
+    ]
+    for y, o, msg in cases:
+        with pytest.raises(OrdaError) as e:
+            H.distillation_loss(s, w, y, t, o)
+        assert str(e.value) == msg
+        with pytest.raises(O.OracleError) as e2:
+            O.distillation_loss(to_np(s), to_np(w), y, Teacher.Tied(to_np(t.hidden)), o)
+        assert str(e2.value) == msg
+
+
+def test_oom_retry_doubles_chunks(torch_dev):
+    """A context memory limit below the single-chunk footprint forces the
+    doubling schedule (resolver.rs:114-126); results are unchanged."""
+    bt, h, v = 1024, 64, 20000
+    s, th = normal((bt, h), 61), normal((bt, h), 62)
+    w = normal((v, h), 63, 0.05)
+    y = uniform_labels(bt, v, 64)
+    opts = LossOptions(kd_weight=0.4, temperature=1.5)
+    args = (gpu(torch_dev, s), gpu(torch_dev, w), gpu(torch_dev, y), Teacher.Tied(gpu(torch_dev, th)))
+    free = H.Context(0)
+    a = H.distillation_loss(*args, opts, ctx=free)
+    tight = H.Context(0)
+    tight.set_memory_limit(48 << 20)
+    b = H.distillation_loss(*args, opts, ctx=tight)
+    assert b.chunk_plan.num_chunks > a.chunk_plan.num_chunks
+    check_scalar("loss", b.loss, a.loss, 1e-5)
+    check_grad("grad_weight", b.grad_weight, a.grad_weight)
+    check_grad("grad_student_hidden", b.grad_student_hidden, a.grad_student_hidden)
+    free.close()
+    tight.close()
+
+
+def test_host_buffers_round_trip(torch_dev):
+    """numpy (host) inputs and outputs go through the same device path."""
+    bt, h, v = 40, 24, 130
+    s, th, w = normal((bt, h), 1), normal((bt, h), 2), normal((v, h), 3, 0.1)
+    y = uniform_labels(bt, v, 4)
+    opts = LossOptions(kd_weight=0.2, label_smoothing=0.05)
+    got = H.distillation_loss(s, w, y, Teacher.Tied(th), opts)
+    ref = O.distillation_loss(s, w, y, Teacher.Tied(th), opts)
+    assert isinstance(got.grad_weight, np.ndarray)
+    check_output(got, ref)
