@@ -2,22 +2,34 @@
 //
 // The three products of the reference's chunk loop (src/api.rs:273-292 and
 // :346-377, via src/mat.rs:63-130) all run through one kernel template:
-//   logits      C[2n,V]  = [h_s;h_t] · Wᵀ      A K-major, B K-major
-//   grad_hidden C[rows,H] = dlogits · W         A K-major, B N-major
-//   grad_W      C[V,H]   = dlogitsᵀ · hidden    A M-major, B N-major
+//   logits      C[2n,V]   = [h_s;h_t] · Wᵀ     A K-major, B K-major
+//   grad_hidden C[rows,H] = dlogits · W        A K-major, B N-major
+//   grad_W      C[V,H]    = dlogitsᵀ · hidden  A M-major, B N-major
 //
-// Workgroup tile 256x256, 4 waves each owning 128x128, K staged 128 bytes at a
-// time (64 bf16 or 32 fp32) through a double-buffered, XOR-swizzled LDS tile
-// laid out [row][k]. MN-major operands are transposed in registers
-// (v_perm_b32 for bf16) on their way into LDS so every MFMA operand read is
-// one conflict-free ds_read_b128. bf16 uses v_mfma_f32_16x16x32_bf16, fp32
-// uses v_mfma_f32_16x16x4_f32 (four per 16-byte k-group); accumulation is
-// fp32 in both.
+// Workgroup tile 256x256, 4 waves each owning 128x128 as 8x8 fragments of
+// 16x16. K advances 128 bytes per stage (64 bf16 / 32 fp32) through two LDS
+// stages of 64 KB. Operands travel global -> LDS by DMA
+// (global_load_lds_dwordx4, 16 bytes per lane, written lane-linearly), so no
+// VGPRs hold prefetched data and one barrier per stage suffices:
+//   * K-major tiles are stored [row][128 B] with the 16-byte chunks XOR-
+//     swizzled by row; the swizzle is applied by choosing which global chunk
+//     each lane fetches. Fragment reads are conflict-free ds_read_b128.
+//   * MN-major tiles are stored [k][256 elements] (bf16: 512 B rows) with an
+//     8-byte-pair swizzle and read with ds_read_b64_tr_b16, the gfx950 LDS
+//     transpose read: lanes 4j..4j+3 of each 16-lane group name row j and
+//     lane i receives column i of those 4 rows, i.e. four consecutive k of
+//     one column — exactly an MFMA operand. fp32 MN-major tiles use
+//     ds_read_b32.
+// bf16 uses v_mfma_f32_16x16x32_bf16, fp32 v_mfma_f32_16x16x4_f32 (four per
+// 16-byte k-group); accumulation is fp32 in both. Workgroups are rastered in
+// groups of M-tiles and each XCD receives a contiguous range, so tiles that
+// share an operand strip share that XCD's L2.
 //
 // The Logits epilogue fuses the statistics the row pass needs: for every row
 // and every 256-column tile it writes {max, Σe^(x-max), Σe^((x-max)/T), Σx}
-// computed from the fp32 accumulators, and the fp32 logit at the row's label,
-// so the row pass reads each logit exactly once.
+// from the fp32 accumulators, plus the fp32 logit at the row's label, so the
+// row pass reads each logit exactly once. bf16 logits are staged through LDS
+// and leave as 16-byte row-contiguous stores.
 #include <float.h>
 #include <math.h>
 
@@ -27,33 +39,22 @@ namespace orda {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-constexpr int kTile = 256;           // BM = BN
-constexpr int kSlab = 128;           // bytes of K per LDS stage
+constexpr int kTile = 256;                     // BM = BN
+constexpr int kSlab = 128;                     // bytes of K per stage (K-major rows)
 constexpr int kThreads = 256;
-constexpr int kFrag = 8;             // 8x8 MFMA 16x16 fragments per wave
-constexpr int kStageBytes = kTile * kSlab;   // 32 KB per operand per stage
+constexpr int kFrag = 8;                       // 8x8 fragments of 16x16 per wave
+constexpr int kOpBytes = 32768;                // one operand, one stage
+constexpr int kStageBytes = 2 * kOpBytes;      // A then B
+constexpr int kMainLds = 2 * kStageBytes;      // two stages
+constexpr int kEpiLds = 16384;                 // epilogue scratch after the stages
 constexpr float kLog2e = 1.4426950408889634f;
-
-// Physical 16-byte chunk of (row, chunk) in a [256][128 B] LDS tile. Rows
-// r..r+7 (aligned) reading one chunk, and rows r, r+8, ..., r+56 writing one
-// chunk, both land on 8 distinct chunks (all 32 banks).
-__device__ __forceinline__ int lds_off(int row, int chunk) {
-  return row * kSlab + ((chunk ^ ((row ^ (row >> 3)) & 7)) << 4);
-}
-
-__device__ __forceinline__ u32x4 lds_read16(const unsigned char* base, int off) {
-  return *reinterpret_cast<const u32x4*>(base + off);
-}
-__device__ __forceinline__ void lds_write16(unsigned char* base, int off, u32x4 v) {
-  *reinterpret_cast<u32x4*>(base + off) = v;
-}
-
-__device__ __forceinline__ u32x4 gload16(const unsigned char* p) {
-  return *reinterpret_cast<const u32x4*>(p);
-}
 
 template <typename T>
 struct Elem;
@@ -66,6 +67,23 @@ struct Elem<__bf16> {
   static constexpr int kSize = 2;
 };
 
+// ---------------------------------------------------------------- swizzles
+// K-major tile [256 rows][8 chunks of 16 B]. Rows r..r+7 (aligned) reading one
+// logical chunk land on 8 distinct physical chunks.
+__device__ __forceinline__ int kmaj_swz(int r) { return (r ^ (r >> 3)) & 7; }
+__device__ __forceinline__ int kmaj_off(int r, int c) { return r * kSlab + ((c ^ kmaj_swz(r)) << 4); }
+
+// MN-major bf16 tile [64 k-rows][32 chunks of 16 B]. The four rows a 16-lane
+// transpose read touches (k0..k0+3) and the groups 8 rows apart use distinct
+// 32-byte windows.
+__device__ __forceinline__ int mnb_swz(int r) { return 2 * (r & 3) + 8 * ((r >> 3) & 1); }
+// MN-major fp32 tile [32 k-rows][64 chunks of 16 B].
+__device__ __forceinline__ int mnf_swz(int r) { return 4 * ((r >> 2) & 7); }
+
+__device__ __forceinline__ void dma16(const void* g, lds_void* l) {
+  __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+}
+
 __device__ __forceinline__ float wave16_max(float v) {
 #pragma unroll
   for (int o = 8; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 16));
@@ -77,115 +95,120 @@ __device__ __forceinline__ float wave16_sum(float v) {
   return v;
 }
 
-// Operand loader: global -> registers -> (transpose) -> swizzled LDS tile.
-// KMAJOR: the operand is stored [rows=M or N][ld], one stage is rows
-// [r0, r0+256) x bytes [k0*ES, k0*ES+128).
-// !KMAJOR: the operand is stored [K][ld]; one stage is K rows [k0, k0+SK) x
-// columns [c0, c0+256).
+// ---------------------------------------------------------------- loaders
+// Per-thread description of one operand's 8 DMA transfers per stage.
+// KMAJOR: operand stored [rows of M or N][ld], a stage covers rows
+//         [origin, origin+256) x elements [k0, k0+SK).
+// !KMAJOR: operand stored [K][ld], a stage covers K rows [k0, k0+SK) x
+//         columns [origin, origin+256).
+// Rows/columns past the operand's edge are clamped to the last one that
+// exists: they only feed output rows/columns that are never stored.
 template <typename T, bool KMAJOR>
 struct Loader {
   static constexpr int ES = Elem<T>::kSize;
-  static constexpr int EPC = 16 / ES;     // elements per 16-byte chunk
-  static constexpr int SK = kSlab / ES;   // K elements per stage
+  static constexpr int EPC = 16 / ES;       // elements per 16-byte chunk
+  static constexpr int SK = kSlab / ES;     // K per stage
+  static constexpr int CPR = KMAJOR ? 8 : (kTile * ES / 16);   // chunks per LDS row
 
-  const unsigned char* base;   // operand base (uniform)
+  const unsigned char* base;   // operand origin: KMAJOR row origin, else column origin
   int64_t ld_bytes;
-  int64_t extent;              // rows (KMAJOR) or columns (!KMAJOR) that exist
   int64_t K;
-  int r0;                      // tile origin along M/N
-  uint32_t voff[8];            // per-thread byte offsets within a stage
-  uint32_t valid;              // per-load bit: row/column in range
+  uint32_t goff[8];            // byte offset of each transfer within a stage
+  int kidx[8];                 // K coordinate of each transfer within the stage
 
   __device__ __forceinline__ void init(const void* p, int64_t ld, int64_t ext, int64_t k,
-                                       int origin, int tid) {
-    base = static_cast<const unsigned char*>(p);
+                                       int origin, int wave, int lane) {
     ld_bytes = ld * ES;
-    extent = ext;
     K = k;
-    r0 = origin;
-    valid = 0;
     if (KMAJOR) {
+      base = static_cast<const unsigned char*>(p) + static_cast<int64_t>(origin) * ld_bytes;
+      const int rmax = static_cast<int>(ext - 1 - origin);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        int row = (tid >> 3) + 32 * i;
-        voff[i] = static_cast<uint32_t>(row * ld_bytes + (tid & 7) * 16);
-        if (origin + row < ext) valid |= 1u << i;
+        const int P = (i * 4 + wave) * 64 + lane;
+        const int r = P >> 3;
+        const int c = (P & 7) ^ kmaj_swz(r);
+        const int rr = r < rmax ? r : rmax;
+        goff[i] = static_cast<uint32_t>(rr * ld_bytes + c * 16);
+        kidx[i] = c * EPC;
       }
-    } else if (ES == 2) {
-      int kb = tid >> 5, mb = tid & 31;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) voff[i] = static_cast<uint32_t>((kb * 8 + i) * ld_bytes + mb * 16);
-      if (origin + mb * 8 < ext) valid = 0xffu;
     } else {
-      int mb = tid & 63;
+      base = static_cast<const unsigned char*>(p) + static_cast<int64_t>(origin) * ES;
+      const int cmax = static_cast<int>((ext - 1 - origin) / EPC);
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        int kb = (tid >> 6) + 4 * b;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          voff[b * 4 + i] = static_cast<uint32_t>((kb * 4 + i) * ld_bytes + mb * 16);
+      for (int i = 0; i < 8; ++i) {
+        const int P = (i * 4 + wave) * 64 + lane;
+        const int r = P / CPR;
+        const int pc = P % CPR;
+        const int c = pc ^ (ES == 2 ? mnb_swz(r) : mnf_swz(r));
+        const int cc = c < cmax ? c : cmax;
+        goff[i] = static_cast<uint32_t>(r * ld_bytes + cc * 16);
+        kidx[i] = r;
       }
-      if (origin + mb * 4 < ext) valid = 0xffu;
     }
   }
 
-  // Issue the global loads of stage kt.
-  __device__ __forceinline__ void load(u32x4 (&r)[8], int kt, int tid) const {
+  // Issue the DMA of stage kt into the LDS operand tile `tile`. Transfers past
+  // K write zeros instead, so the tail stage contributes nothing.
+  __device__ __forceinline__ void issue(unsigned char* tile, int kt, int wave, int lane) const {
     const int64_t k0 = static_cast<int64_t>(kt) * SK;
+    const unsigned char* s = KMAJOR ? base + k0 * ES : base + k0 * ld_bytes;
     const int64_t krem = K - k0;
-    if (KMAJOR) {
-      const unsigned char* s = base + r0 * ld_bytes + k0 * ES;
-      const bool kok = (tid & 7) * EPC < krem;
+    if (krem >= SK) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        dma16(s + goff[i], (lds_void*)(tile + (i * 4 + wave) * 1024));
+    } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        r[i] = u32x4{0, 0, 0, 0};
-        if (kok && ((valid >> i) & 1)) r[i] = gload16(s + voff[i]);
-      }
-    } else {
-      const unsigned char* s = base + k0 * ld_bytes + static_cast<int64_t>(r0) * ES;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        int krow;
-        if (ES == 2) krow = (tid >> 5) * 8 + i;
-        else krow = ((tid >> 6) + 4 * (i >> 2)) * 4 + (i & 3);
-        r[i] = u32x4{0, 0, 0, 0};
-        if (krow < krem && ((valid >> i) & 1)) r[i] = gload16(s + voff[i]);
-      }
-    }
-  }
-
-  // Write stage registers to an LDS tile (transposing MN-major data).
-  __device__ __forceinline__ void store(unsigned char* tile, const u32x4 (&r)[8], int tid) const {
-    if (KMAJOR) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) lds_write16(tile, lds_off((tid >> 3) + 32 * i, tid & 7), r[i]);
-    } else if (ES == 2) {
-      // r[i] holds 8 bf16 of K-row kb*8+i at columns mb*8..mb*8+7; chunk j of
-      // the output holds K-rows kb*8..kb*8+7 of column mb*8+j.
-      const int kb = tid >> 5, mb = tid & 31;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-        u32x4 o;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          o[q] = __builtin_amdgcn_perm(r[2 * q + 1][j >> 1], r[2 * q][j >> 1], sel);
-        lds_write16(tile, lds_off(mb * 8 + j, kb), o);
-      }
-    } else {
-      const int mb = tid & 63;
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const int kb = (tid >> 6) + 4 * b;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          u32x4 o = {r[b * 4 + 0][j], r[b * 4 + 1][j], r[b * 4 + 2][j], r[b * 4 + 3][j]};
-          lds_write16(tile, lds_off(mb * 4 + j, kb), o);
+        unsigned char* l = tile + (i * 4 + wave) * 1024;
+        if (kidx[i] < krem) {
+          dma16(s + goff[i], (lds_void*)l);
+        } else {
+          *reinterpret_cast<u32x4*>(l + lane * 16) = u32x4{0, 0, 0, 0};
         }
       }
     }
   }
 };
+
+// ---------------------------------------------------------------- fragments
+// Operand fragment of k-group kg (64 bytes of K) for 16 rows (or columns)
+// starting at r0 of the tile: lane (m = lane%16, g = lane/16) holds the K
+// elements [kg*KG + g*KG/4, +KG/4) of row r0+m, KG = 32 (bf16) or 16 (fp32).
+template <typename T, bool KMAJOR>
+__device__ __forceinline__ u32x4 read_frag(const unsigned char* tile, int r0, int kg, int lane) {
+  const int m = lane & 15, g = lane >> 4;
+  if constexpr (KMAJOR) {
+    return *reinterpret_cast<const u32x4*>(tile + kmaj_off(r0 + m, kg * 4 + g));
+  } else if constexpr (Elem<T>::kSize == 2) {
+    // two transpose reads: K rows kg*32 + 8g + {0..3} and {4..7}
+    u32x4 out;
+    const int col = r0 + 4 * (m & 3);
+    const int c = col >> 3;
+    const int byte = (m & 1) * 8;   // (col % 8) * 2, col % 4 == 0
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int kr = kg * 32 + 8 * g + 4 * h + (m >> 2);
+      const int off = kr * 512 + ((c ^ mnb_swz(kr)) << 4) + byte;
+      const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(tile + off));
+      const u32x2 w = __builtin_bit_cast(u32x2, v);
+      out[2 * h] = w[0];
+      out[2 * h + 1] = w[1];
+    }
+    return out;
+  } else {
+    u32x4 out;
+    const int col = r0 + m;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int kr = kg * 16 + 4 * g + q;
+      const int off = kr * 1024 + (((col >> 2) ^ mnf_swz(kr)) << 4) + (col & 3) * 4;
+      out[q] = *reinterpret_cast<const uint32_t*>(tile + off);
+    }
+    return out;
+  }
+}
 
 template <typename T>
 __device__ __forceinline__ void mfma_step(f32x4 (&acc)[kFrag][kFrag], const u32x4 (&a)[kFrag],
@@ -238,20 +261,27 @@ __device__ __forceinline__ TileCoord map_tile(const GemmArgs& g) {
   return c;
 }
 
+// Byte offset of the 16-byte chunk (row, c) of the staged bf16 logits tile
+// [256 rows][32 chunks]; rows 4 apart (the four lane groups) use distinct
+// 32-byte windows.
+__device__ __forceinline__ int stage_off(int row, int c) {
+  return row * 512 + ((c ^ (2 * ((row >> 2) & 3))) << 4);
+}
+
 template <typename T, bool AK, bool BK, GemmEpilogue EPI, typename LT>
 __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[4 * kStageBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[kMainLds + kEpiLds];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: M0 of the DMA
   const int wm = wave >> 1, wn = wave & 1;
   const TileCoord tc = map_tile(g);
   const GemmProblem& pr = g.prob[tc.p];
 
   Loader<T, AK> la;
   Loader<T, BK> lb;
-  la.init(pr.a, g.lda, g.M, g.K, tc.m0, tid);
-  lb.init(pr.b, g.ldb, g.N, g.K, tc.n0, tid);
+  la.init(pr.a, g.lda, g.M, g.K, tc.m0, wave, lane);
+  lb.init(pr.b, g.ldb, g.N, g.K, tc.n0, wave, lane);
 
   f32x4 acc[kFrag][kFrag];
 #pragma unroll
@@ -262,47 +292,47 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
   constexpr int SK = kSlab / Elem<T>::kSize;
   const int nk = static_cast<int>((g.K + SK - 1) / SK);
 
-  // Stage s of operand A lives at smem + s*2*kStageBytes, of B one stage later.
-
-  u32x4 ra[8], rb[8];
   if (nk > 0) {
-    la.load(ra, 0, tid);
-    lb.load(rb, 0, tid);
-    la.store(smem, ra, tid);
-    lb.store(smem + kStageBytes, rb, tid);
+    la.issue(smem, 0, wave, lane);
+    lb.issue(smem + kOpBytes, 0, wave, lane);
   }
+  for (int kt = 0; kt < nk; ++kt) {
+    // Stage kt has landed (own DMA + zero fills), and every wave is done
+    // reading the buffer the next DMA overwrites.
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __syncthreads();
+    const unsigned char* ta = smem + (kt & 1) * kStageBytes;
+    const unsigned char* tb = ta + kOpBytes;
+    // All operand fragments of the stage first (both k-groups), then the DMA
+    // of the next stage, then the MFMAs: the fragment reads never wait on the
+    // DMA, and the DMA latency hides under 128 MFMAs.
+    u32x4 af0[kFrag], bf0[kFrag], af1[kFrag], bf1[kFrag];
+#pragma unroll
+    for (int i = 0; i < kFrag; ++i) af0[i] = read_frag<T, AK>(ta, wm * 128 + i * 16, 0, lane);
+#pragma unroll
+    for (int j = 0; j < kFrag; ++j) bf0[j] = read_frag<T, BK>(tb, wn * 128 + j * 16, 0, lane);
+#pragma unroll
+    for (int i = 0; i < kFrag; ++i) af1[i] = read_frag<T, AK>(ta, wm * 128 + i * 16, 1, lane);
+#pragma unroll
+    for (int j = 0; j < kFrag; ++j) bf1[j] = read_frag<T, BK>(tb, wn * 128 + j * 16, 1, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt + 1 < nk) {
+      unsigned char* nxt = smem + ((kt + 1) & 1) * kStageBytes;
+      la.issue(nxt, kt + 1, wave, lane);
+      lb.issue(nxt + kOpBytes, kt + 1, wave, lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_step<T>(acc, af0, bf0);
+    mfma_step<T>(acc, af1, bf1);
+  }
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
   __syncthreads();
 
+  // ------------------------------------------------------------ epilogue
   const int lrow = lane & 15;
   const int lgrp = lane >> 4;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) {
-      la.load(ra, kt + 1, tid);
-      lb.load(rb, kt + 1, tid);
-    }
-    const unsigned char* ta = smem + cur * 2 * kStageBytes;
-    const unsigned char* tb = ta + kStageBytes;
-#pragma unroll
-    for (int kg = 0; kg < 2; ++kg) {
-      u32x4 af[kFrag], bfr[kFrag];
-#pragma unroll
-      for (int i = 0; i < kFrag; ++i) af[i] = lds_read16(ta, lds_off(wm * 128 + i * 16 + lrow, kg * 4 + lgrp));
-#pragma unroll
-      for (int j = 0; j < kFrag; ++j) bfr[j] = lds_read16(tb, lds_off(wn * 128 + j * 16 + lrow, kg * 4 + lgrp));
-      mfma_step<T>(acc, af, bfr);
-    }
-    if (kt + 1 < nk) {
-      unsigned char* na = smem + (cur ^ 1) * 2 * kStageBytes;
-      la.store(na, ra, tid);
-      lb.store(na + kStageBytes, rb, tid);
-    }
-    __syncthreads();
-  }
-
-  // ------------------------------------------------------------ epilogue
   const int row_w = tc.m0 + wm * 128;          // first row of this wave
-  const int col_l = tc.n0 + wn * 128 + lrow;   // this lane's column for fragment j=0
+  const int col_l = tc.n0 + wn * 128 + lrow;   // this lane's column of fragment j=0
   if constexpr (EPI == GemmEpilogue::StoreF32 || EPI == GemmEpilogue::AccumF32) {
     float* C = static_cast<float*>(pr.c);
 #pragma unroll
@@ -325,15 +355,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
       }
     }
   } else {
-    // Logits: store, then per-row partial softmax statistics of this tile.
+    // Logits: per-row partial softmax statistics of this 256-column tile, the
+    // label logit, and the logits themselves.
     LT* C = static_cast<LT*>(pr.c);
-    int64_t* lab = reinterpret_cast<int64_t*>(smem);              // [256] labels
-    float4* part = reinterpret_cast<float4*>(smem + 4096);        // [2][256]
+    int64_t* lab = reinterpret_cast<int64_t*>(smem + kMainLds);           // [256]
+    float4* part = reinterpret_cast<float4*>(smem + kMainLds + 2048);     // [2][256]
     {
       const int64_t row = tc.m0 + tid;
       lab[tid] = row < g.M ? g.lg.labels[row] : g.lg.ignore_index;
     }
     __syncthreads();
+    constexpr bool kStage = Elem<LT>::kSize == 2;   // bf16 logits go through LDS
     const float it2 = g.lg.inv_t * kLog2e;
     bool cv[kFrag];
 #pragma unroll
@@ -344,7 +376,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
       for (int e = 0; e < 4; ++e) {
         const int rl = wm * 128 + i * 16 + lgrp * 4 + e;   // row within tile
         const int64_t row = tc.m0 + rl;
-        const bool rv = row < g.M;
         const int64_t y = lab[rl];
         float mx = -INFINITY;
 #pragma unroll
@@ -368,15 +399,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
         dT = wave16_sum(dT);
         sx = wave16_sum(sx);
         if (lrow == 0) part[wn * 256 + rl] = make_float4(mx, d1, dT, sx);
-        if (rv) {
-          LT* crow = C + row * g.ldc;
 #pragma unroll
-          for (int j = 0; j < kFrag; ++j) {
-            const int64_t col = col_l + j * 16;
-            if (cv[j]) {
-              crow[col] = static_cast<LT>(acc[i][j][e]);
-              if (col == y) g.lg.xy[tc.p * g.M + row] = acc[i][j][e];
-            }
+        for (int j = 0; j < kFrag; ++j) {
+          const int64_t col = col_l + j * 16;
+          if (col == y && row < g.M) g.lg.xy[tc.p * g.M + row] = acc[i][j][e];
+          if constexpr (kStage) {
+            const int cl = wn * 128 + j * 16 + lrow;    // column within tile
+            const __bf16 b = static_cast<__bf16>(acc[i][j][e]);
+            *reinterpret_cast<__bf16*>(smem + stage_off(rl, cl >> 3) + (cl & 7) * 2) = b;
+          } else {
+            if (cv[j] && row < g.M) C[row * g.ldc + col] = static_cast<LT>(acc[i][j][e]);
           }
         }
       }
@@ -402,6 +434,26 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
           s.z = a.z * fa + b.z * fb;
         }
         g.lg.stats[(static_cast<int64_t>(tc.p) * g.M + row) * g.lg.stats_ld + tc.ntile] = s;
+      }
+    }
+    if constexpr (kStage) {
+      // 256 rows x 32 chunks of 16 B; a wave covers two rows per instruction.
+      const int ncols = static_cast<int>(g.N - tc.n0 < 256 ? g.N - tc.n0 : 256);
+#pragma unroll 4
+      for (int it = 0; it < 32; ++it) {
+        const int idx = it * kThreads + tid;
+        const int rl = idx >> 5, c = idx & 31;
+        const int64_t row = tc.m0 + rl;
+        if (row < g.M && c * 8 < ncols) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(smem + stage_off(rl, c));
+          LT* dst = C + row * g.ldc + tc.n0 + c * 8;
+          if (c * 8 + 8 <= ncols) {
+            *reinterpret_cast<u32x4*>(dst) = v;
+          } else {
+            const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
+            for (int q = 0; c * 8 + q < ncols; ++q) reinterpret_cast<uint16_t*>(dst)[q] = h[q];
+          }
+        }
       }
     }
   }
@@ -449,6 +501,7 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
   if (g.nprob < 1 || g.nprob > 2) return hipErrorInvalidValue;
   if ((g.lda % 8) || (g.ldb % 8) || (g.ldc % 8 && g.epi == GemmEpilogue::Logits))
     return hipErrorInvalidValue;
+  if (g.M <= 0 || g.N <= 0) return hipSuccess;
   if (g.in_type == DType::BF16) return dispatch_layout<__bf16>(g, stream);
   return dispatch_layout<float>(g, stream);
 }
