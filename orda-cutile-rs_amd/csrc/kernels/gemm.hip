@@ -7,11 +7,13 @@
 //   grad_W      C[V,H]    = dlogitsᵀ · hidden  A M-major, B N-major
 //
 // Workgroup tile 256x256, 4 waves each owning 128x128 as 8x8 fragments of
-// 16x16. K advances 128 bytes per stage (64 bf16 / 32 fp32) through two LDS
-// stages of 64 KB. Operands travel global -> LDS by DMA
-// (global_load_lds_dwordx4, 16 bytes per lane, written lane-linearly), so no
-// VGPRs hold prefetched data and one barrier per stage suffices:
-//   * K-major tiles are stored [row][128 B] with the 16-byte chunks XOR-
+// 16x16. K advances 64 bytes per stage (32 bf16 / 16 fp32) through a ring of
+// four 32 KB LDS stages. Operands travel global -> LDS by DMA
+// (global_load_lds_dwordx4, 16 bytes per lane, written lane-linearly) issued
+// four stages ahead; the fragments of stage s+1 are read into a second
+// register set while the 64 MFMAs of stage s run, so after each barrier the
+// MFMAs start at once and one barrier per stage suffices:
+//   * K-major tiles are stored [row][64 B] with the 16-byte chunks XOR-
 //     swizzled by row; the swizzle is applied by choosing which global chunk
 //     each lane fetches. Fragment reads are conflict-free ds_read_b128.
 //   * MN-major tiles are stored [k][256 elements] (bf16: 512 B rows) with an
@@ -47,13 +49,15 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int kTile = 256;                     // BM = BN
-constexpr int kSlab = 128;                     // bytes of K per stage (K-major rows)
+constexpr int kSlab = 64;                      // bytes of K per stage (K-major rows)
 constexpr int kThreads = 256;
 constexpr int kFrag = 8;                       // 8x8 fragments of 16x16 per wave
-constexpr int kOpBytes = 32768;                // one operand, one stage
+constexpr int kOpBytes = 16384;                // one operand, one stage
 constexpr int kStageBytes = 2 * kOpBytes;      // A then B
-constexpr int kMainLds = 2 * kStageBytes;      // two stages
-constexpr int kEpiLds = 16384;                 // epilogue scratch after the stages
+constexpr int kRing = 4;                       // stages in flight
+constexpr int kXfers = kOpBytes / (kThreads * 16);   // DMA transfers per thread per operand
+constexpr int kMainLds = kRing * kStageBytes;  // 128 KB
+constexpr int kEpiLds = 16384;                 // epilogue scratch after the ring
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <typename T>
@@ -68,17 +72,25 @@ struct Elem<__bf16> {
 };
 
 // ---------------------------------------------------------------- swizzles
-// K-major tile [256 rows][8 chunks of 16 B]. Rows r..r+7 (aligned) reading one
-// logical chunk land on 8 distinct physical chunks.
-__device__ __forceinline__ int kmaj_swz(int r) { return (r ^ (r >> 3)) & 7; }
+// K-major tile [256 rows][4 chunks of 16 B]: two rows share a 128-byte bank
+// line, and rows r..r+7 (aligned) reading one logical chunk land on 8
+// distinct 16-byte bank windows.
+__device__ __forceinline__ int kmaj_swz(int r) { return (r >> 1) & 3; }
 __device__ __forceinline__ int kmaj_off(int r, int c) { return r * kSlab + ((c ^ kmaj_swz(r)) << 4); }
 
-// MN-major bf16 tile [64 k-rows][32 chunks of 16 B]. The four rows a 16-lane
+// MN-major bf16 tile [32 k-rows][32 chunks of 16 B]. The four rows a 16-lane
 // transpose read touches (k0..k0+3) and the groups 8 rows apart use distinct
 // 32-byte windows.
 __device__ __forceinline__ int mnb_swz(int r) { return 2 * (r & 3) + 8 * ((r >> 3) & 1); }
-// MN-major fp32 tile [32 k-rows][64 chunks of 16 B].
-__device__ __forceinline__ int mnf_swz(int r) { return 4 * ((r >> 2) & 7); }
+// MN-major fp32 tile [16 k-rows][64 chunks of 16 B].
+__device__ __forceinline__ int mnf_swz(int r) { return 4 * ((r >> 2) & 3); }
+
+// s_waitcnt encodings (gfx9): vmcnt in bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8. Both wait for every LDS operation.
+constexpr int kWaitAll = 0x0070;                              // vmcnt(0) lgkmcnt(0)
+constexpr int vm_wait(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
+constexpr int kWaitTwoStages = vm_wait(2 * 2 * kXfers);     // stage s+1 landed
+constexpr int kWaitThreeStages = vm_wait(3 * 2 * kXfers);   // stage 0 landed
 
 __device__ __forceinline__ void dma16(const void* g, lds_void* l) {
   __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
@@ -108,13 +120,13 @@ struct Loader {
   static constexpr int ES = Elem<T>::kSize;
   static constexpr int EPC = 16 / ES;       // elements per 16-byte chunk
   static constexpr int SK = kSlab / ES;     // K per stage
-  static constexpr int CPR = KMAJOR ? 8 : (kTile * ES / 16);   // chunks per LDS row
+  static constexpr int CPR = KMAJOR ? kSlab / 16 : (kTile * ES / 16);   // chunks per LDS row
 
   const unsigned char* base;   // operand origin: KMAJOR row origin, else column origin
   int64_t ld_bytes;
   int64_t K;
-  uint32_t goff[8];            // byte offset of each transfer within a stage
-  int kidx[8];                 // K coordinate of each transfer within the stage
+  uint32_t goff[kXfers];       // byte offset of each transfer within a stage
+  int kidx[kXfers];            // K coordinate of each transfer within the stage
 
   __device__ __forceinline__ void init(const void* p, int64_t ld, int64_t ext, int64_t k,
                                        int origin, int wave, int lane) {
@@ -124,10 +136,10 @@ struct Loader {
       base = static_cast<const unsigned char*>(p) + static_cast<int64_t>(origin) * ld_bytes;
       const int rmax = static_cast<int>(ext - 1 - origin);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < kXfers; ++i) {
         const int P = (i * 4 + wave) * 64 + lane;
-        const int r = P >> 3;
-        const int c = (P & 7) ^ kmaj_swz(r);
+        const int r = P / CPR;
+        const int c = (P % CPR) ^ kmaj_swz(r);
         const int rr = r < rmax ? r : rmax;
         goff[i] = static_cast<uint32_t>(rr * ld_bytes + c * 16);
         kidx[i] = c * EPC;
@@ -136,7 +148,7 @@ struct Loader {
       base = static_cast<const unsigned char*>(p) + static_cast<int64_t>(origin) * ES;
       const int cmax = static_cast<int>((ext - 1 - origin) / EPC);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < kXfers; ++i) {
         const int P = (i * 4 + wave) * 64 + lane;
         const int r = P / CPR;
         const int pc = P % CPR;
@@ -156,11 +168,11 @@ struct Loader {
     const int64_t krem = K - k0;
     if (krem >= SK) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < kXfers; ++i)
         dma16(s + goff[i], (lds_void*)(tile + (i * 4 + wave) * 1024));
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < kXfers; ++i) {
         unsigned char* l = tile + (i * 4 + wave) * 1024;
         if (kidx[i] < krem) {
           dma16(s + goff[i], (lds_void*)l);
@@ -173,16 +185,17 @@ struct Loader {
 };
 
 // ---------------------------------------------------------------- fragments
-// Operand fragment of k-group kg (64 bytes of K) for 16 rows (or columns)
+// Operand fragment of a stage (64 bytes of K) for 16 rows (or columns)
 // starting at r0 of the tile: lane (m = lane%16, g = lane/16) holds the K
-// elements [kg*KG + g*KG/4, +KG/4) of row r0+m, KG = 32 (bf16) or 16 (fp32).
+// elements [g*KG/4, +KG/4) of row r0+m, KG = 32 (bf16) or 16 (fp32).
 template <typename T, bool KMAJOR>
-__device__ __forceinline__ u32x4 read_frag(const unsigned char* tile, int r0, int kg, int lane) {
+__device__ __forceinline__ u32x4 read_frag(const unsigned char* tile, int r0, int lane) {
   const int m = lane & 15, g = lane >> 4;
+  constexpr int kg = 0;
   if constexpr (KMAJOR) {
     return *reinterpret_cast<const u32x4*>(tile + kmaj_off(r0 + m, kg * 4 + g));
   } else if constexpr (Elem<T>::kSize == 2) {
-    // two transpose reads: K rows kg*32 + 8g + {0..3} and {4..7}
+    // two transpose reads: K rows 8g + {0..3} and 8g + {4..7}
     u32x4 out;
     const int col = r0 + 4 * (m & 3);
     const int c = col >> 3;
@@ -191,8 +204,12 @@ __device__ __forceinline__ u32x4 read_frag(const unsigned char* tile, int r0, in
     for (int h = 0; h < 2; ++h) {
       const int kr = kg * 32 + 8 * g + 4 * h + (m >> 2);
       const int off = kr * 512 + ((c ^ mnb_swz(kr)) << 4) + byte;
-      const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(tile + off));
-      const u32x2 w = __builtin_bit_cast(u32x2, v);
+      // Issued as inline asm: the compiler would otherwise wait for every
+      // in-flight DMA before it. The result is consumed only after the next
+      // stage's explicit s_waitcnt lgkmcnt(0).
+      u32x2 w;
+      const uint32_t addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(tile + off));
+      asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(w) : "v"(addr));
       out[2 * h] = w[0];
       out[2 * h + 1] = w[1];
     }
@@ -290,43 +307,96 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
     for (int j = 0; j < kFrag; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   constexpr int SK = kSlab / Elem<T>::kSize;
-  const int nk = static_cast<int>((g.K + SK - 1) / SK);
 
-  if (nk > 0) {
-    la.issue(smem, 0, wave, lane);
-    lb.issue(smem + kOpBytes, 0, wave, lane);
-  }
-  for (int kt = 0; kt < nk; ++kt) {
-    // Stage kt has landed (own DMA + zero fills), and every wave is done
-    // reading the buffer the next DMA overwrites.
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    __syncthreads();
-    const unsigned char* ta = smem + (kt & 1) * kStageBytes;
-    const unsigned char* tb = ta + kOpBytes;
-    // All operand fragments of the stage first (both k-groups), then the DMA
-    // of the next stage, then the MFMAs: the fragment reads never wait on the
-    // DMA, and the DMA latency hides under 128 MFMAs.
-    u32x4 af0[kFrag], bf0[kFrag], af1[kFrag], bf1[kFrag];
+  // Full stages (nkf of them) run through the ring; a partial last stage
+  // (K % SK != 0) is handled after the loop. Every half-iteration issues the
+  // same number of DMA transfers (past the last full stage, an in-bounds
+  // dummy copy of stage 0 into a slot nobody reads again), so one constant
+  // vmcnt wait always means "stage s+1 has landed".
+  const int nkf = static_cast<int>(g.K / SK);
+  u32x4 ra[2][kFrag], rb[2][kFrag];
+  auto issue_stage = [&](int slot_idx, int st) {
+    unsigned char* slot = smem + slot_idx * kStageBytes;
+    const int src = st < nkf ? st : 0;
+    la.issue(slot, src, wave, lane);
+    lb.issue(slot + kOpBytes, src, wave, lane);
+  };
+  auto read_stage = [&](int slot_idx, u32x4 (&rA)[kFrag], u32x4 (&rB)[kFrag]) {
+    const unsigned char* nb = smem + slot_idx * kStageBytes;
 #pragma unroll
-    for (int i = 0; i < kFrag; ++i) af0[i] = read_frag<T, AK>(ta, wm * 128 + i * 16, 0, lane);
+    for (int i = 0; i < kFrag; ++i) rA[i] = read_frag<T, AK>(nb, wm * 128 + i * 16, lane);
 #pragma unroll
-    for (int j = 0; j < kFrag; ++j) bf0[j] = read_frag<T, BK>(tb, wn * 128 + j * 16, 0, lane);
-#pragma unroll
-    for (int i = 0; i < kFrag; ++i) af1[i] = read_frag<T, AK>(ta, wm * 128 + i * 16, 1, lane);
-#pragma unroll
-    for (int j = 0; j < kFrag; ++j) bf1[j] = read_frag<T, BK>(tb, wn * 128 + j * 16, 1, lane);
-    __builtin_amdgcn_sched_barrier(0);
-    if (kt + 1 < nk) {
-      unsigned char* nxt = smem + ((kt + 1) & 1) * kStageBytes;
-      la.issue(nxt, kt + 1, wave, lane);
-      lb.issue(nxt + kOpBytes, kt + 1, wave, lane);
+    for (int j = 0; j < kFrag; ++j) rB[j] = read_frag<T, BK>(nb + kOpBytes, wn * 128 + j * 16, lane);
+  };
+  if constexpr (Elem<T>::kSize == 2) {
+    if (nkf > 0) {
+      for (int t = 0; t < kRing; ++t) issue_stage(t, t);
+      __builtin_amdgcn_s_waitcnt(kWaitThreeStages);
+      __builtin_amdgcn_s_barrier();
+      read_stage(0, ra[0], rb[0]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // Iteration s: (1) wait until stage s+1 has landed (stages s+2, s+3 may
+    // still be in flight) and every wave has finished reading stage s out of
+    // its slot; (2) read stage s+1's fragments into the other register set;
+    // (3) DMA stage s+4 into stage s's slot; (4) 64 MFMAs on stage s.
+    // Iterations run in pairs so each register set has a fixed name.
+    auto half = [&](int st, u32x4 (&rnA)[kFrag], u32x4 (&rnB)[kFrag], const u32x4 (&rcA)[kFrag],
+                    const u32x4 (&rcB)[kFrag]) {
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(kWaitTwoStages);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      if (st + 1 < nkf) read_stage((st + 1) % kRing, rnA, rnB);
+      __builtin_amdgcn_sched_barrier(0);
+      issue_stage(st % kRing, st + kRing);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_step<T>(acc, rcA, rcB);
+    };
+    int s0 = 0;
+    for (; s0 + 1 < nkf; s0 += 2) {
+      half(s0, ra[1], rb[1], ra[0], rb[0]);
+      half(s0 + 1, ra[0], rb[0], ra[1], rb[1]);
     }
     __builtin_amdgcn_sched_barrier(0);
-    mfma_step<T>(acc, af0, bf0);
-    mfma_step<T>(acc, af1, bf1);
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
+    __builtin_amdgcn_sched_barrier(0);
+    if (s0 < nkf) mfma_step<T>(acc, ra[0], rb[0]);
+  } else {
+    // fp32: an MFMA stage is long (256 v_mfma_f32_16x16x4_f32), so one
+    // register set suffices: DMA three stages ahead into the slot read one
+    // stage ago, read this stage after the barrier, then compute.
+    if (nkf > 0)
+      for (int t = 0; t < kRing - 1; ++t) issue_stage(t, t);
+    for (int st = 0; st < nkf; ++st) {
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(kWaitTwoStages);
+      __builtin_amdgcn_s_barrier();
+      read_stage(st % kRing, ra[0], rb[0]);
+      __builtin_amdgcn_sched_barrier(0);
+      issue_stage((st + kRing - 1) % kRing, st + kRing - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_step<T>(acc, ra[0], rb[0]);
+    }
   }
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-  __syncthreads();
+  if (nkf * SK < g.K) {
+    // Partial last stage: DMA the valid part, zero the rest, then one step.
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
+    __builtin_amdgcn_s_barrier();
+    la.issue(smem, nkf, wave, lane);
+    lb.issue(smem + kOpBytes, nkf, wave, lane);
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
+    __builtin_amdgcn_s_barrier();
+    read_stage(0, ra[1], rb[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_step<T>(acc, ra[1], rb[1]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(kWaitAll);
+  __builtin_amdgcn_s_barrier();
 
   // ------------------------------------------------------------ epilogue
   const int lrow = lane & 15;
