@@ -1,16 +1,27 @@
 """Build-time check of the GEMM's gfx950 assembly.
 
-The MN-major operand fragments are read with inline-asm ds_read_b64_tr_b16,
-which the compiler does not track as pending LDS loads. This script verifies,
-for every GEMM variant, that on every control-flow path no instruction reads
-or writes a destination register of such a read before an s_waitcnt that
-drains LDS operations (lgkmcnt(0)). It runs a forward dataflow over the
-kernel's basic blocks (union of pending registers at joins).
+The bf16 GEMM kernels issue their MFMAs as inline asm (accumulators tied to
+AGPRs), so the compiler's hazard recognizer does not see them and the kernel
+inserts the required wait states itself. This script verifies, on every
+control-flow path of every bf16 GEMM variant, that
+  * no non-MFMA instruction reads or writes an MFMA result register within
+    MFMA_RESULT_WAIT wait states of the MFMA that wrote it, and no MFMA reads
+    it as an operand that soon either;
+  * no MFMA reads (as A, B or C) a register that a VALU instruction wrote
+    within VALU_TO_MFMA_WAIT wait states.
+Every instruction counts as one wait state and `s_nop N` as N + 1. The
+analysis is a forward dataflow over the kernel's basic blocks keeping, per
+register, the fewest wait states since the last such write on any path.
+It also reports (as warnings) variants that spill to scratch.
 
 Usage: python check_isa.py <gemm.s>   (exit status 1 on a violation)
 """
 import re
 import sys
+
+MFMA_RESULT_WAIT = 19     # a 16-pass XDL result is readable 18 wait states later
+VALU_TO_MFMA_WAIT = 4     # VALU write -> MFMA operand read needs 2; keep margin
+CAP = 64                  # distances at or above every threshold
 
 
 def reg_set(tok):
@@ -61,29 +72,54 @@ def successors(blocks, i):
     return targets + nxt
 
 
-def transfer(instrs, pending, name, errors):
-    pending = set(pending)
+def advance(state, n):
+    return {r: d + n for r, d in state.items() if d + n < CAP}
+
+
+def transfer(instrs, entry, name, errors):
+    """entry: (mfma_dist, valu_dist) dicts register -> wait states since write."""
+    mf, va = dict(entry[0]), dict(entry[1])
     for line in instrs:
         op, args = parse(line)
-        if op == "s_waitcnt" and "lgkmcnt(0)" in line:
-            pending.clear()
+        if op == "s_nop":
+            n = int(args[0], 0) + 1
+            mf, va = advance(mf, n), advance(va, n)
             continue
-        if op.startswith("s_"):
+        regs = [reg_set(a) for a in args]
+        if op.startswith("v_mfma"):
+            srcs = set().union(*regs[1:4]) if len(regs) >= 4 else set()
+            for r in srcs:
+                if r in mf and mf[r] < MFMA_RESULT_WAIT:
+                    errors.add(f"{name}: '{line}' reads {r} {mf[r]} wait states after an MFMA wrote it")
+                if r in va and va[r] < VALU_TO_MFMA_WAIT:
+                    errors.add(f"{name}: '{line}' reads {r} {va[r]} wait states after a VALU wrote it")
+            mf, va = advance(mf, 1), advance(va, 1)
+            for r in regs[0]:
+                mf[r] = 0
+                va.pop(r, None)
             continue
-        regs = set()
-        for a in args:
-            regs |= reg_set(a)
-        if op == "ds_read_b64_tr_b16":
-            dst = reg_set(args[0])
-            if dst & pending:
-                errors.add(f"{name}: tr read overwrites a pending destination: {line}")
-            if reg_set(args[1]) & pending:
-                errors.add(f"{name}: tr read address is a pending register: {line}")
-            pending |= dst
-            continue
-        if regs & pending:
-            errors.add(f"{name}: '{line}' touches {sorted(regs & pending)} before lgkmcnt(0)")
-    return pending
+        touched = set().union(*regs) if regs else set()
+        for r in touched:
+            if r in mf and mf[r] < MFMA_RESULT_WAIT:
+                errors.add(f"{name}: '{line}' touches {r} {mf[r]} wait states after an MFMA wrote it")
+        mf, va = advance(mf, 1), advance(va, 1)
+        if op.startswith("v_") and regs:
+            for r in regs[0]:
+                va[r] = 0
+                mf.pop(r, None)
+        elif regs and (op.startswith("ds_read") or op.startswith("global_load")
+                       or op.startswith("buffer_load") or op.startswith("scratch_load")):
+            for r in regs[0]:
+                mf.pop(r, None)
+                va.pop(r, None)
+    return mf, va
+
+
+def merge(a, b):
+    out = dict(a)
+    for r, d in b.items():
+        out[r] = min(d, out.get(r, CAP))
+    return out
 
 
 warnings = set()
@@ -94,17 +130,17 @@ def check(path):
     errors = set()
     for fn in re.split(r"\n(?=_Z\w+:)", text):
         name = fn.split(":")[0]
-        if "gemm_kernel" not in name:
+        if "gemm_kernelIDF16b" not in name:
             continue
         end = fn.find("s_endpgm")
         body = fn[: fn.find("\n", end) if end >= 0 else len(fn)]
         if re.search(r"scratch_(load|store)", body):
-            warnings.add(f"{name}: spills to scratch (outside the hazard rule; check the loop)")
+            warnings.add(f"{name}: spills to scratch")
         blocks = blocks_of(body.split("\n")[1:])
         index = {b[0]: k for k, b in enumerate(blocks)}
-        entry = {k: set() for k in range(len(blocks))}
-        work = list(range(len(blocks)))
+        entry = {k: ({}, {}) for k in range(len(blocks))}
         seen_out = {}
+        work = list(range(len(blocks)))
         while work:
             k = work.pop(0)
             out = transfer(blocks[k][1], entry[k], name, errors)
@@ -115,7 +151,7 @@ def check(path):
                 j = index.get(s)
                 if j is None:
                     continue
-                merged = entry[j] | out
+                merged = (merge(entry[j][0], out[0]), merge(entry[j][1], out[1]))
                 if merged != entry[j] or j not in seen_out:
                     entry[j] = merged
                     if j not in work:

@@ -56,8 +56,7 @@ constexpr int kOpBytes = 16384;                // one operand, one stage
 constexpr int kStageBytes = 2 * kOpBytes;      // A then B
 constexpr int kRing = 4;                       // stages in flight
 constexpr int kXfers = kOpBytes / (kThreads * 16);   // DMA transfers per thread per operand
-constexpr int kMainLds = kRing * kStageBytes;  // 128 KB
-constexpr int kEpiLds = 16384;                 // epilogue scratch after the ring
+constexpr int kEpiLds = 16384;                 // epilogue scratch beside the ring
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <typename T>
@@ -92,9 +91,33 @@ constexpr int vm_wait(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
 constexpr int kWaitTwoStages = vm_wait(2 * 2 * kXfers);     // stage s+1 landed
 constexpr int kWaitThreeStages = vm_wait(3 * 2 * kXfers);   // stage 0 landed
 
-__device__ __forceinline__ void dma16(const void* g, lds_void* l) {
-  __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+// One DMA transfer: every active lane copies the 16 bytes at sbase + voff
+// into LDS at M0 + 16 * lane (global_load_lds_dwordx4, saddr form). Written as
+// inline asm so that the compiler's memory-counter bookkeeping does not see
+// the transfers: it would otherwise make every later LDS transpose read wait
+// for all of them (vmcnt(0)). The kernel orders DMA and reads itself with
+// explicit s_waitcnt + s_barrier. M0 is reserved by the compiler, hence the
+// clobber (nothing else in these kernels keeps a value in M0).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const unsigned char* sbase, uint32_t voff, unsigned char* l) {
+  // sbase and the LDS destination are wave-uniform; readfirstlane states it
+  // to the compiler so that they live in SGPRs also inside divergent code.
+  // (readfirstlane returns int: each half goes through uint32_t so that the
+  // low half is not sign-extended into the high one.)
+  const uint64_t p = reinterpret_cast<uint64_t>(sbase);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p)));
+  const uint32_t hi =
+      static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32)));
+  const uint64_t ps = (static_cast<uint64_t>(hi) << 32) | lo;
+  const uint32_t m0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)l))));
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %0"
+               :
+               : "s"(ps), "v"(voff), "s"(m0)
+               : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 __device__ __forceinline__ float wave16_max(float v) {
 #pragma unroll
@@ -160,6 +183,17 @@ struct Loader {
     }
   }
 
+  // Source of a full stage kt (all SK elements of K exist).
+  __device__ __forceinline__ const unsigned char* stage_src(int kt) const {
+    const int64_t k0 = static_cast<int64_t>(kt) * SK;
+    return KMAJOR ? base + k0 * ES : base + k0 * ld_bytes;
+  }
+  // Transfer i of a full stage whose source is s.
+  __device__ __forceinline__ void xfer(unsigned char* tile, const unsigned char* s, int i,
+                                       int wave) const {
+    dma16(s, goff[i], tile + (i * 4 + wave) * 1024);
+  }
+
   // Issue the DMA of stage kt into the LDS operand tile `tile`. Transfers past
   // K write zeros instead, so the tail stage contributes nothing.
   __device__ __forceinline__ void issue(unsigned char* tile, int kt, int wave, int lane) const {
@@ -169,13 +203,13 @@ struct Loader {
     if (krem >= SK) {
 #pragma unroll
       for (int i = 0; i < kXfers; ++i)
-        dma16(s + goff[i], (lds_void*)(tile + (i * 4 + wave) * 1024));
+        dma16(s, goff[i], tile + (i * 4 + wave) * 1024);
     } else {
 #pragma unroll
       for (int i = 0; i < kXfers; ++i) {
         unsigned char* l = tile + (i * 4 + wave) * 1024;
         if (kidx[i] < krem) {
-          dma16(s + goff[i], (lds_void*)l);
+          dma16(s, goff[i], l);
         } else {
           *reinterpret_cast<u32x4*>(l + lane * 16) = u32x4{0, 0, 0, 0};
         }
@@ -204,12 +238,8 @@ __device__ __forceinline__ u32x4 read_frag(const unsigned char* tile, int r0, in
     for (int h = 0; h < 2; ++h) {
       const int kr = kg * 32 + 8 * g + 4 * h + (m >> 2);
       const int off = kr * 512 + ((c ^ mnb_swz(kr)) << 4) + byte;
-      // Issued as inline asm: the compiler would otherwise wait for every
-      // in-flight DMA before it. The result is consumed only after the next
-      // stage's explicit s_waitcnt lgkmcnt(0).
-      u32x2 w;
-      const uint32_t addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(tile + off));
-      asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(w) : "v"(addr));
+      const u32x2 w = __builtin_bit_cast(
+          u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(tile + off)));
       out[2 * h] = w[0];
       out[2 * h + 1] = w[1];
     }
@@ -227,6 +257,78 @@ __device__ __forceinline__ u32x4 read_frag(const unsigned char* tile, int r0, in
   }
 }
 
+// Fragment reader of one bf16 operand for the interleaved main loop. It keeps
+// only the per-lane byte offsets of fragment 0 of the wave's strip (w0 = the
+// strip's first row or column):
+//   K-major:  fragment i sits 1024*i bytes further (the row swizzle depends
+//             on the row's low bits only);
+//   MN-major: one offset per transpose read h; fragment i sits at
+//             off[h] ^ (i << 5), because i only moves chunk bits 1-3 of the
+//             row, which are the bits the swizzle XORs.
+// refresh() hides the offsets from the optimiser once per stage so that the
+// 16 fragment addresses are formed next to their reads rather than kept live
+// through the loop.
+template <bool KMAJOR>
+struct FragReader {
+  uint32_t off[2];
+
+  __device__ __forceinline__ void init(int w0, int lane) {
+    const int m = lane & 15, g = lane >> 4;
+    if constexpr (KMAJOR) {
+      off[0] = static_cast<uint32_t>(kmaj_off(w0 + m, g));
+      off[1] = 0;
+    } else {
+      const int col = w0 + 4 * (m & 3);
+      const int c = col >> 3;
+      const int byte = (m & 1) * 8;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int kr = 8 * g + 4 * h + (m >> 2);
+        off[h] = static_cast<uint32_t>(kr * 512 + ((c ^ mnb_swz(kr)) << 4) + byte);
+      }
+    }
+  }
+  __device__ __forceinline__ void refresh() {
+    if constexpr (KMAJOR) {
+      asm volatile("" : "+v"(off[0]));
+    } else {
+      asm volatile("" : "+v"(off[0]), "+v"(off[1]));
+    }
+  }
+  __device__ __forceinline__ u32x4 read(const unsigned char* tile, int i) const {
+    if constexpr (KMAJOR) {
+      return *reinterpret_cast<const u32x4*>(tile + off[0] + i * 1024);
+    } else {
+      u32x4 out;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const u32x2 w = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                       (lds_i16x4*)(tile + (off[h] ^ static_cast<uint32_t>(i << 5)))));
+        out[2 * h] = w[0];
+        out[2 * h + 1] = w[1];
+      }
+      return out;
+    }
+  }
+};
+
+// One bf16 MFMA with its accumulator pinned to AGPRs (tied in/out). Written
+// as inline asm because, once fragment reads are interleaved with the MFMAs,
+// the compiler stops tying the builtin's accumulator to its result and keeps
+// shuffling the 64 accumulators between VGPRs and AGPRs. The compiler still
+// inserts the LDS waits for the operands; the MFMA hazards it cannot see
+// (accumulator initialisation before the first MFMA, results read after the
+// last one) are covered by explicit s_nop, and the build checks the
+// generated code for them.
+__device__ __forceinline__ void mfma_bf16(f32x4& acc, const u32x4& a, const u32x4& b) {
+  asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// Wait states between the last MFMA and the first read of its result, and
+// between an accumulator write by a VALU and the first MFMA reading it.
+__device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"); }
+__device__ __forceinline__ void mfma_prime() { asm volatile("s_nop 7"); }
+
 template <typename T>
 __device__ __forceinline__ void mfma_step(f32x4 (&acc)[kFrag][kFrag], const u32x4 (&a)[kFrag],
                                           const u32x4 (&b)[kFrag]) {
@@ -235,8 +337,7 @@ __device__ __forceinline__ void mfma_step(f32x4 (&acc)[kFrag][kFrag], const u32x
 #pragma unroll
     for (int j = 0; j < kFrag; ++j) {
       if constexpr (Elem<T>::kSize == 2) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            __builtin_bit_cast(bf16x8, a[i]), __builtin_bit_cast(bf16x8, b[j]), acc[i][j], 0, 0, 0);
+        mfma_bf16(acc[i][j], a[i], b[j]);
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -278,16 +379,18 @@ __device__ __forceinline__ TileCoord map_tile(const GemmArgs& g) {
   return c;
 }
 
-// Byte offset of the 16-byte chunk (row, c) of the staged bf16 logits tile
-// [256 rows][32 chunks]; rows 4 apart (the four lane groups) use distinct
-// 32-byte windows.
+// Byte offset of the 16-byte chunk (row, c) of the staged bf16 logits tile,
+// 64 rows [32 chunks] per ring slot; rows 4 apart (the four lane groups) use
+// distinct 32-byte windows.
 __device__ __forceinline__ int stage_off(int row, int c) {
   return row * 512 + ((c ^ (2 * ((row >> 2) & 3))) << 4);
 }
 
 template <typename T, bool AK, bool BK, GemmEpilogue EPI, typename LT>
 __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[kMainLds + kEpiLds];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[kRing * kStageBytes + kEpiLds];
+  unsigned char* const epi = smem + kRing * kStageBytes;
+  auto ring = [&](int s) -> unsigned char* { return smem + s * kStageBytes; };
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: M0 of the DMA
@@ -309,59 +412,95 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
   constexpr int SK = kSlab / Elem<T>::kSize;
 
   // Full stages (nkf of them) run through the ring; a partial last stage
-  // (K % SK != 0) is handled after the loop. Every half-iteration issues the
-  // same number of DMA transfers (past the last full stage, an in-bounds
-  // dummy copy of stage 0 into a slot nobody reads again), so one constant
-  // vmcnt wait always means "stage s+1 has landed".
+  // (K % SK != 0) is handled after the loop. Every iteration issues the same
+  // number of DMA transfers (past the last full stage, an in-bounds dummy
+  // copy of stage 0 into a slot nobody reads again), so one constant vmcnt
+  // wait always means "stage s+1 has landed".
   const int nkf = static_cast<int>(g.K / SK);
   u32x4 ra[2][kFrag], rb[2][kFrag];
   auto issue_stage = [&](int slot_idx, int st) {
-    unsigned char* slot = smem + slot_idx * kStageBytes;
+    unsigned char* slot = ring(slot_idx);
     const int src = st < nkf ? st : 0;
     la.issue(slot, src, wave, lane);
     lb.issue(slot + kOpBytes, src, wave, lane);
   };
   auto read_stage = [&](int slot_idx, u32x4 (&rA)[kFrag], u32x4 (&rB)[kFrag]) {
-    const unsigned char* nb = smem + slot_idx * kStageBytes;
+    const unsigned char* nb = ring(slot_idx);
 #pragma unroll
     for (int i = 0; i < kFrag; ++i) rA[i] = read_frag<T, AK>(nb, wm * 128 + i * 16, lane);
 #pragma unroll
     for (int j = 0; j < kFrag; ++j) rB[j] = read_frag<T, BK>(nb + kOpBytes, wn * 128 + j * 16, lane);
   };
   if constexpr (Elem<T>::kSize == 2) {
+    FragReader<AK> fa;
+    FragReader<BK> fb;
+    fa.init(wm * 128, lane);
+    fb.init(wn * 128, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_prime();
+    __builtin_amdgcn_sched_barrier(0);
     if (nkf > 0) {
+#pragma unroll
       for (int t = 0; t < kRing; ++t) issue_stage(t, t);
       __builtin_amdgcn_s_waitcnt(kWaitThreeStages);
       __builtin_amdgcn_s_barrier();
       read_stage(0, ra[0], rb[0]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // Iteration s: (1) wait until stage s+1 has landed (stages s+2, s+3 may
-    // still be in flight) and every wave has finished reading stage s out of
-    // its slot; (2) read stage s+1's fragments into the other register set;
-    // (3) DMA stage s+4 into stage s's slot; (4) 64 MFMAs on stage s.
-    // Iterations run in pairs so each register set has a fixed name.
-    auto half = [&](int st, u32x4 (&rnA)[kFrag], u32x4 (&rnB)[kFrag], const u32x4 (&rcA)[kFrag],
+    // Iteration s (stage s sits in slot s%4 and register set s%2):
+    // (1) wait until stage s+1 has landed (stages s+2, s+3 may still be in
+    // flight) and every wave has finished reading stage s out of its slot;
+    // (2) read stage s+1's fragments into the other register set; (3) DMA
+    // stage s+4 into stage s's slot; (4) 64 MFMAs on stage s.
+    //
+    // With one wave per SIMD nothing else fills the matrix pipe, so (2) and
+    // (3) are interleaved with (4): the MFMAs go out in 16 groups of four and
+    // each group carries two fragment reads (groups 0-7) or one DMA transfer
+    // (groups 8-15), which then issue while the previous MFMAs execute. The
+    // reads finish early enough that the next iteration's wait does not
+    // stall. An iteration whose stage s+1 does not exist reads a slot whose
+    // contents are never used.
+    auto iter = [&](int st, u32x4 (&rnA)[kFrag], u32x4 (&rnB)[kFrag], const u32x4 (&rcA)[kFrag],
                     const u32x4 (&rcB)[kFrag]) {
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_waitcnt(kWaitTwoStages);
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      if (st + 1 < nkf) read_stage((st + 1) % kRing, rnA, rnB);
-      __builtin_amdgcn_sched_barrier(0);
-      issue_stage(st % kRing, st + kRing);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_step<T>(acc, rcA, rcB);
+      const unsigned char* nb = ring((st + 1) % kRing);
+      unsigned char* slot = ring(st % kRing);
+      const int nxt = st + kRing < nkf ? st + kRing : 0;
+      const unsigned char* sa = la.stage_src(nxt);
+      const unsigned char* sb = lb.stage_src(nxt);
+      fa.refresh();
+      fb.refresh();
+#pragma unroll
+      for (int grp = 0; grp < 16; ++grp) {
+        if (grp < 8) {
+          rnA[grp] = fa.read(nb, grp);
+          rnB[grp] = fb.read(nb + kOpBytes, grp);
+        } else if (grp < 8 + kXfers) {
+          la.xfer(slot, sa, grp - 8, wave);
+        } else {
+          lb.xfer(slot + kOpBytes, sb, grp - 8 - kXfers, wave);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int i = grp >> 1, j = (grp & 1) * 4 + q;
+          mfma_bf16(acc[i][j], rcA[i], rcB[j]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
     };
+    // Iterations run in pairs so each register set has a fixed name.
     int s0 = 0;
     for (; s0 + 1 < nkf; s0 += 2) {
-      half(s0, ra[1], rb[1], ra[0], rb[0]);
-      half(s0 + 1, ra[0], rb[0], ra[1], rb[1]);
+      iter(s0, ra[1], rb[1], ra[0], rb[0]);
+      iter(s0 + 1, ra[0], rb[0], ra[1], rb[1]);
     }
+    if (s0 < nkf) iter(s0, ra[1], rb[1], ra[0], rb[0]);
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(kWaitAll);
+    mfma_drain();
     __builtin_amdgcn_sched_barrier(0);
-    if (s0 < nkf) mfma_step<T>(acc, ra[0], rb[0]);
   } else {
     // fp32: an MFMA stage is long (256 v_mfma_f32_16x16x4_f32), so one
     // register set suffices: DMA three stages ahead into the slot read one
@@ -393,6 +532,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
     __builtin_amdgcn_s_waitcnt(kWaitAll);
     __builtin_amdgcn_sched_barrier(0);
     mfma_step<T>(acc, ra[1], rb[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (Elem<T>::kSize == 2) mfma_drain();
   }
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_waitcnt(kWaitAll);
@@ -428,8 +569,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
     // Logits: per-row partial softmax statistics of this 256-column tile, the
     // label logit, and the logits themselves.
     LT* C = static_cast<LT*>(pr.c);
-    int64_t* lab = reinterpret_cast<int64_t*>(smem + kMainLds);           // [256]
-    float4* part = reinterpret_cast<float4*>(smem + kMainLds + 2048);     // [2][256]
+    int64_t* lab = reinterpret_cast<int64_t*>(epi);                      // [256]
+    float4* part = reinterpret_cast<float4*>(epi + 2048);                // [2][256]
     {
       const int64_t row = tc.m0 + tid;
       lab[tid] = row < g.M ? g.lg.labels[row] : g.lg.ignore_index;
@@ -476,7 +617,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
           if constexpr (kStage) {
             const int cl = wn * 128 + j * 16 + lrow;    // column within tile
             const __bf16 b = static_cast<__bf16>(acc[i][j][e]);
-            *reinterpret_cast<__bf16*>(smem + stage_off(rl, cl >> 3) + (cl & 7) * 2) = b;
+            *reinterpret_cast<__bf16*>(ring(rl >> 6) + stage_off(rl & 63, cl >> 3) + (cl & 7) * 2) = b;
           } else {
             if (cv[j] && row < g.M) C[row * g.ldc + col] = static_cast<LT>(acc[i][j][e]);
           }
@@ -515,7 +656,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
         const int rl = idx >> 5, c = idx & 31;
         const int64_t row = tc.m0 + rl;
         if (row < g.M && c * 8 < ncols) {
-          const u32x4 v = *reinterpret_cast<const u32x4*>(smem + stage_off(rl, c));
+          const u32x4 v = *reinterpret_cast<const u32x4*>(ring(rl >> 6) + stage_off(rl & 63, c));
           LT* dst = C + row * g.ldc + tc.n0 + c * 8;
           if (c * 8 + 8 <= ncols) {
             *reinterpret_cast<u32x4*>(dst) = v;
