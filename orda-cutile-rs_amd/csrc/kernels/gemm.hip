@@ -47,6 +47,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
 
 constexpr int kTile = 256;                     // BM = BN
 constexpr int kSlab = 64;                      // bytes of K per stage (K-major rows)
@@ -56,6 +57,7 @@ constexpr int kOpBytes = 16384;                // one operand, one stage
 constexpr int kStageBytes = 2 * kOpBytes;      // A then B
 constexpr int kRing = 4;                       // stages in flight
 constexpr int kXfers = kOpBytes / (kThreads * 16);   // DMA transfers per thread per operand
+static_assert(kXfers == 4, "the main loop's DMA schedule assumes four transfers per operand");
 constexpr int kEpiLds = 16384;                 // epilogue scratch beside the ring
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -117,7 +119,24 @@ __device__ __forceinline__ void dma16(const unsigned char* sbase, uint32_t voff,
                : "s"(ps), "v"(voff), "s"(m0)
                : "memory", "m0");
 }
+// Main-loop form: M0 = m0base + imm in one SALU add (the caller keeps
+// m0base = the stage slot's LDS offset + this wave's 1 KB block).
+template <int IMM>
+__device__ __forceinline__ void dma16_at(uint64_t sbase, uint32_t voff, uint32_t m0base) {
+  asm volatile("s_add_u32 m0, %2, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %0"
+               :
+               : "s"(sbase), "v"(voff), "s"(m0base), "n"(IMM)
+               : "memory", "m0", "scc");
+}
 #pragma clang diagnostic pop
+// A wave-uniform 64-bit value in an SGPR pair.
+__device__ __forceinline__ uint64_t uniform64(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v)));
+  const uint32_t hi =
+      static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32)));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
 
 __device__ __forceinline__ float wave16_max(float v) {
 #pragma unroll
@@ -188,11 +207,6 @@ struct Loader {
     const int64_t k0 = static_cast<int64_t>(kt) * SK;
     return KMAJOR ? base + k0 * ES : base + k0 * ld_bytes;
   }
-  // Transfer i of a full stage whose source is s.
-  __device__ __forceinline__ void xfer(unsigned char* tile, const unsigned char* s, int i,
-                                       int wave) const {
-    dma16(s, goff[i], tile + (i * 4 + wave) * 1024);
-  }
 
   // Issue the DMA of stage kt into the LDS operand tile `tile`. Transfers past
   // K write zeros instead, so the tail stage contributes nothing.
@@ -258,25 +272,26 @@ __device__ __forceinline__ u32x4 read_frag(const unsigned char* tile, int r0, in
 }
 
 // Fragment reader of one bf16 operand for the interleaved main loop. It keeps
-// only the per-lane byte offsets of fragment 0 of the wave's strip (w0 = the
-// strip's first row or column):
-//   K-major:  fragment i sits 1024*i bytes further (the row swizzle depends
-//             on the row's low bits only);
-//   MN-major: one offset per transpose read h; fragment i sits at
-//             off[h] ^ (i << 5), because i only moves chunk bits 1-3 of the
-//             row, which are the bits the swizzle XORs.
-// refresh() hides the offsets from the optimiser once per stage so that the
-// 16 fragment addresses are formed next to their reads rather than kept live
-// through the loop.
+// each lane's LDS byte address of every read of ring slot 0; slot s lies
+// s * kOpBytes further, which the read takes as its immediate offset:
+//   K-major:  fragment i sits 1024*i bytes after fragment 0 (the row swizzle
+//             depends on the row's low bits only) — one ds_read_b128 each;
+//   MN-major: two transpose reads per fragment (h = 0, 1); fragment i of read
+//             h sits at off[h] ^ (i << 5), because i only moves chunk bits 1-3
+//             of the row, which are the bits the swizzle XORs.
+// read_op<SLOT>(o) issues LDS instruction o of a stage: fragment o (K-major)
+// or half o%2 of fragment o/2 (MN-major).
 template <bool KMAJOR>
 struct FragReader {
-  uint32_t off[2];
+  static constexpr int kOps = KMAJOR ? kFrag : 2 * kFrag;
+  uint32_t addr[KMAJOR ? 1 : 2 * kFrag];
 
-  __device__ __forceinline__ void init(int w0, int lane) {
+  // tile0: LDS byte address of this operand's tile in slot 0; w0: the wave
+  // strip's first row (K-major) or column (MN-major).
+  __device__ __forceinline__ void init(uint32_t tile0, int w0, int lane) {
     const int m = lane & 15, g = lane >> 4;
     if constexpr (KMAJOR) {
-      off[0] = static_cast<uint32_t>(kmaj_off(w0 + m, g));
-      off[1] = 0;
+      addr[0] = tile0 + static_cast<uint32_t>(kmaj_off(w0 + m, g));
     } else {
       const int col = w0 + 4 * (m & 3);
       const int c = col >> 3;
@@ -284,33 +299,30 @@ struct FragReader {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int kr = 8 * g + 4 * h + (m >> 2);
-        off[h] = static_cast<uint32_t>(kr * 512 + ((c ^ mnb_swz(kr)) << 4) + byte);
-      }
-    }
-  }
-  __device__ __forceinline__ void refresh() {
-    if constexpr (KMAJOR) {
-      asm volatile("" : "+v"(off[0]));
-    } else {
-      asm volatile("" : "+v"(off[0]), "+v"(off[1]));
-    }
-  }
-  __device__ __forceinline__ u32x4 read(const unsigned char* tile, int i) const {
-    if constexpr (KMAJOR) {
-      return *reinterpret_cast<const u32x4*>(tile + off[0] + i * 1024);
-    } else {
-      u32x4 out;
+        const uint32_t off = static_cast<uint32_t>(kr * 512 + ((c ^ mnb_swz(kr)) << 4) + byte);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const u32x2 w = __builtin_bit_cast(
-            u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                       (lds_i16x4*)(tile + (off[h] ^ static_cast<uint32_t>(i << 5)))));
-        out[2 * h] = w[0];
-        out[2 * h + 1] = w[1];
+        for (int f = 0; f < kFrag; ++f)
+          addr[2 * f + h] = tile0 + (off ^ static_cast<uint32_t>(f << 5));
       }
-      return out;
     }
   }
+  template <int SLOT>
+  __device__ __forceinline__ void read_op(int o, u32x4 (&r)[kFrag]) const {
+    if constexpr (KMAJOR) {
+      r[o] = *(const lds_u32x4*)(static_cast<uintptr_t>(addr[0] + (o * 1024 + SLOT * kOpBytes)));
+    } else {
+      const u32x2 w = __builtin_bit_cast(
+          u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                     (lds_i16x4*)(static_cast<uintptr_t>(addr[o] + SLOT * kOpBytes))));
+      r[o >> 1][2 * (o & 1)] = w[0];
+      r[o >> 1][2 * (o & 1) + 1] = w[1];
+    }
+  }
+};
+
+template <int S>
+struct SlotC {
+  static constexpr int value = S;
 };
 
 // One bf16 MFMA with its accumulator pinned to AGPRs (tied in/out). Written
@@ -379,18 +391,21 @@ __device__ __forceinline__ TileCoord map_tile(const GemmArgs& g) {
   return c;
 }
 
-// Byte offset of the 16-byte chunk (row, c) of the staged bf16 logits tile,
-// 64 rows [32 chunks] per ring slot; rows 4 apart (the four lane groups) use
-// distinct 32-byte windows.
+// Byte offset of the 16-byte chunk (row, c) of the staged bf16 logits tile
+// [256 rows][32 chunks] (it reuses the ring); rows 4 apart (the four lane
+// groups) use distinct 32-byte windows.
 __device__ __forceinline__ int stage_off(int row, int c) {
   return row * 512 + ((c ^ (2 * ((row >> 2) & 3))) << 4);
 }
 
 template <typename T, bool AK, bool BK, GemmEpilogue EPI, typename LT>
 __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
+  // Ring layout: A tiles of slots 0-3, then B tiles of slots 0-3 (16 KB
+  // each), so every slot offset fits a DS instruction's immediate.
   __shared__ __attribute__((aligned(1024))) unsigned char smem[kRing * kStageBytes + kEpiLds];
   unsigned char* const epi = smem + kRing * kStageBytes;
-  auto ring = [&](int s) -> unsigned char* { return smem + s * kStageBytes; };
+  auto tileA = [&](int s) -> unsigned char* { return smem + s * kOpBytes; };
+  auto tileB = [&](int s) -> unsigned char* { return smem + (kRing + s) * kOpBytes; };
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: M0 of the DMA
@@ -419,23 +434,29 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
   const int nkf = static_cast<int>(g.K / SK);
   u32x4 ra[2][kFrag], rb[2][kFrag];
   auto issue_stage = [&](int slot_idx, int st) {
-    unsigned char* slot = ring(slot_idx);
     const int src = st < nkf ? st : 0;
-    la.issue(slot, src, wave, lane);
-    lb.issue(slot + kOpBytes, src, wave, lane);
+    la.issue(tileA(slot_idx), src, wave, lane);
+    lb.issue(tileB(slot_idx), src, wave, lane);
   };
   auto read_stage = [&](int slot_idx, u32x4 (&rA)[kFrag], u32x4 (&rB)[kFrag]) {
-    const unsigned char* nb = ring(slot_idx);
 #pragma unroll
-    for (int i = 0; i < kFrag; ++i) rA[i] = read_frag<T, AK>(nb, wm * 128 + i * 16, lane);
+    for (int i = 0; i < kFrag; ++i) rA[i] = read_frag<T, AK>(tileA(slot_idx), wm * 128 + i * 16, lane);
 #pragma unroll
-    for (int j = 0; j < kFrag; ++j) rB[j] = read_frag<T, BK>(nb + kOpBytes, wn * 128 + j * 16, lane);
+    for (int j = 0; j < kFrag; ++j) rB[j] = read_frag<T, BK>(tileB(slot_idx), wn * 128 + j * 16, lane);
   };
   if constexpr (Elem<T>::kSize == 2) {
+    // LDS byte address of the ring and of this wave's 1 KB DMA block.
+    // The base is hidden from the optimiser: otherwise it folds the B tiles'
+    // 64 KB offset into the per-read constant, which then no longer fits the
+    // 16-bit immediate and costs a VALU op per read.
+    uint32_t lds0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+        static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)smem))));
+    asm volatile("" : "+s"(lds0));
+    const uint32_t m0wave = lds0 + static_cast<uint32_t>(wave) * 1024;
     FragReader<AK> fa;
     FragReader<BK> fb;
-    fa.init(wm * 128, lane);
-    fb.init(wn * 128, lane);
+    fa.init(lds0, wm * 128, lane);
+    fb.init(lds0 + kRing * kOpBytes, wn * 128, lane);
     __builtin_amdgcn_sched_barrier(0);
     mfma_prime();
     __builtin_amdgcn_sched_barrier(0);
@@ -454,50 +475,77 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
     // stage s+4 into stage s's slot; (4) 64 MFMAs on stage s.
     //
     // With one wave per SIMD nothing else fills the matrix pipe, so (2) and
-    // (3) are interleaved with (4): the MFMAs go out in 16 groups of four and
-    // each group carries two fragment reads (groups 0-7) or one DMA transfer
-    // (groups 8-15), which then issue while the previous MFMAs execute. The
-    // reads finish early enough that the next iteration's wait does not
-    // stall. An iteration whose stage s+1 does not exist reads a slot whose
-    // contents are never used.
-    auto iter = [&](int st, u32x4 (&rnA)[kFrag], u32x4 (&rnB)[kFrag], const u32x4 (&rcA)[kFrag],
-                    const u32x4 (&rcB)[kFrag]) {
+    // (3) ride between the MFMAs: the 64 MFMAs go out as 32 pairs and side
+    // operation o (the stage's LDS reads first, then its eight DMA
+    // transfers) issues with pair (o * 32) / kSide, while the MFMAs before
+    // it execute. The reads finish early enough that the next iteration's
+    // wait does not stall. An iteration whose stage s+1 does not exist reads
+    // a slot whose contents are never used.
+    constexpr int kOpsA = FragReader<AK>::kOps, kOpsB = FragReader<BK>::kOps;
+    constexpr int kReads = kOpsA + kOpsB;
+    constexpr int kSide = kReads + 2 * kXfers;
+    constexpr int kPairDma = (kReads * 32) / kSide;   // first pair carrying a DMA
+    auto iter = [&](auto slot_c, int st, u32x4 (&rnA)[kFrag], u32x4 (&rnB)[kFrag],
+                    const u32x4 (&rcA)[kFrag], const u32x4 (&rcB)[kFrag]) {
+      constexpr int S = decltype(slot_c)::value;       // slot of stage s
+      constexpr int SN = (S + 1) % kRing;              // slot of stage s+1
+      constexpr int MA = S * kOpBytes;                 // DMA targets, from m0wave
+      constexpr int MB = (kRing + S) * kOpBytes;
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_waitcnt(kWaitTwoStages);
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      const unsigned char* nb = ring((st + 1) % kRing);
-      unsigned char* slot = ring(st % kRing);
-      const int nxt = st + kRing < nkf ? st + kRing : 0;
-      const unsigned char* sa = la.stage_src(nxt);
-      const unsigned char* sb = lb.stage_src(nxt);
-      fa.refresh();
-      fb.refresh();
+      uint64_t sa = 0, sb = 0;
 #pragma unroll
-      for (int grp = 0; grp < 16; ++grp) {
-        if (grp < 8) {
-          rnA[grp] = fa.read(nb, grp);
-          rnB[grp] = fb.read(nb + kOpBytes, grp);
-        } else if (grp < 8 + kXfers) {
-          la.xfer(slot, sa, grp - 8, wave);
-        } else {
-          lb.xfer(slot + kOpBytes, sb, grp - 8 - kXfers, wave);
+      for (int pr = 0; pr < 32; ++pr) {
+        if (pr == kPairDma - 2) {
+          // DMA sources of stage s+4, computed here so the scalar work
+          // overlaps MFMAs instead of delaying the first one.
+          const int nxt = st + kRing < nkf ? st + kRing : 0;
+          sa = uniform64(la.stage_src(nxt));
+          sb = uniform64(lb.stage_src(nxt));
         }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int i = grp >> 1, j = (grp & 1) * 4 + q;
-          mfma_bf16(acc[i][j], rcA[i], rcB[j]);
+        for (int o = 0; o < kSide; ++o) {
+          if ((o * 32) / kSide != pr) continue;
+          if (o < kOpsA) {
+            fa.template read_op<SN>(o, rnA);
+          } else if (o < kReads) {
+            fb.template read_op<SN>(o - kOpsA, rnB);
+          } else {
+            switch (o - kReads) {   // 0-3: A transfers, 4-7: B transfers
+              case 0: dma16_at<MA + 0 * 4096>(sa, la.goff[0], m0wave); break;
+              case 1: dma16_at<MA + 1 * 4096>(sa, la.goff[1], m0wave); break;
+              case 2: dma16_at<MA + 2 * 4096>(sa, la.goff[2], m0wave); break;
+              case 3: dma16_at<MA + 3 * 4096>(sa, la.goff[3], m0wave); break;
+              case 4: dma16_at<MB + 0 * 4096>(sb, lb.goff[0], m0wave); break;
+              case 5: dma16_at<MB + 1 * 4096>(sb, lb.goff[1], m0wave); break;
+              case 6: dma16_at<MB + 2 * 4096>(sb, lb.goff[2], m0wave); break;
+              default: dma16_at<MB + 3 * 4096>(sb, lb.goff[3], m0wave); break;
+            }
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int mm = 2 * pr + q;
+          mfma_bf16(acc[mm >> 3][mm & 7], rcA[mm >> 3], rcB[mm & 7]);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
     };
-    // Iterations run in pairs so each register set has a fixed name.
+    // Unrolled by the ring depth so each slot is a compile-time immediate;
+    // the register sets alternate.
     int s0 = 0;
-    for (; s0 + 1 < nkf; s0 += 2) {
-      iter(s0, ra[1], rb[1], ra[0], rb[0]);
-      iter(s0 + 1, ra[0], rb[0], ra[1], rb[1]);
+    for (; s0 + 3 < nkf; s0 += 4) {
+      iter(SlotC<0>{}, s0, ra[1], rb[1], ra[0], rb[0]);
+      iter(SlotC<1>{}, s0 + 1, ra[0], rb[0], ra[1], rb[1]);
+      iter(SlotC<2>{}, s0 + 2, ra[1], rb[1], ra[0], rb[0]);
+      iter(SlotC<3>{}, s0 + 3, ra[0], rb[0], ra[1], rb[1]);
     }
-    if (s0 < nkf) iter(s0, ra[1], rb[1], ra[0], rb[0]);
+    const int rem = nkf - s0;
+    if (rem >= 1) iter(SlotC<0>{}, s0, ra[1], rb[1], ra[0], rb[0]);
+    if (rem >= 2) iter(SlotC<1>{}, s0 + 1, ra[0], rb[0], ra[1], rb[1]);
+    if (rem >= 3) iter(SlotC<2>{}, s0 + 2, ra[1], rb[1], ra[0], rb[0]);
     __builtin_amdgcn_sched_barrier(0);
     mfma_drain();
     __builtin_amdgcn_sched_barrier(0);
@@ -523,8 +571,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kWaitAll);
     __builtin_amdgcn_s_barrier();
-    la.issue(smem, nkf, wave, lane);
-    lb.issue(smem + kOpBytes, nkf, wave, lane);
+    la.issue(tileA(0), nkf, wave, lane);
+    lb.issue(tileB(0), nkf, wave, lane);
     __builtin_amdgcn_s_waitcnt(kWaitAll);
     __builtin_amdgcn_s_barrier();
     read_stage(0, ra[1], rb[1]);
@@ -617,7 +665,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
           if constexpr (kStage) {
             const int cl = wn * 128 + j * 16 + lrow;    // column within tile
             const __bf16 b = static_cast<__bf16>(acc[i][j][e]);
-            *reinterpret_cast<__bf16*>(ring(rl >> 6) + stage_off(rl & 63, cl >> 3) + (cl & 7) * 2) = b;
+            *reinterpret_cast<__bf16*>(smem + stage_off(rl, cl >> 3) + (cl & 7) * 2) = b;
           } else {
             if (cv[j] && row < g.M) C[row * g.ldc + col] = static_cast<LT>(acc[i][j][e]);
           }
@@ -656,7 +704,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
         const int rl = idx >> 5, c = idx & 31;
         const int64_t row = tc.m0 + rl;
         if (row < g.M && c * 8 < ncols) {
-          const u32x4 v = *reinterpret_cast<const u32x4*>(ring(rl >> 6) + stage_off(rl & 63, c));
+          const u32x4 v = *reinterpret_cast<const u32x4*>(smem + stage_off(rl, c));
           LT* dst = C + row * g.ldc + tc.n0 + c * 8;
           if (c * 8 + 8 <= ncols) {
             *reinterpret_cast<u32x4*>(dst) = v;
