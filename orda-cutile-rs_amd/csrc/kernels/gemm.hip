@@ -341,20 +341,27 @@ __device__ __forceinline__ void mfma_bf16(f32x4& acc, const u32x4& a, const u32x
 __device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"); }
 __device__ __forceinline__ void mfma_prime() { asm volatile("s_nop 7"); }
 
-template <typename T>
+// One stage of MFMAs: acc[i][j] += A-fragment i x B-fragment j. With SWAP the
+// operands enter the MFMA the other way round, so acc[i][j] holds the
+// transposed 16x16 block: lane (r = lane%16, g = lane/16) then owns row r of
+// A-fragment i and the four consecutive columns 4g..4g+3 of B-fragment j,
+// instead of four consecutive rows of one column.
+template <typename T, bool SWAP>
 __device__ __forceinline__ void mfma_step(f32x4 (&acc)[kFrag][kFrag], const u32x4 (&a)[kFrag],
                                           const u32x4 (&b)[kFrag]) {
 #pragma unroll
   for (int i = 0; i < kFrag; ++i) {
 #pragma unroll
     for (int j = 0; j < kFrag; ++j) {
+      const u32x4& x = SWAP ? b[j] : a[i];
+      const u32x4& y = SWAP ? a[i] : b[j];
       if constexpr (Elem<T>::kSize == 2) {
-        mfma_bf16(acc[i][j], a[i], b[j]);
+        mfma_bf16(acc[i][j], x, y);
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[i][q]),
-                                                           __uint_as_float(b[j][q]), acc[i][j],
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(x[q]),
+                                                           __uint_as_float(y[q]), acc[i][j],
                                                            0, 0, 0);
       }
     }
@@ -391,11 +398,11 @@ __device__ __forceinline__ TileCoord map_tile(const GemmArgs& g) {
   return c;
 }
 
-// Byte offset of the 16-byte chunk (row, c) of the staged bf16 logits tile
-// [256 rows][32 chunks] (it reuses the ring); rows 4 apart (the four lane
-// groups) use distinct 32-byte windows.
-__device__ __forceinline__ int stage_off(int row, int c) {
-  return row * 512 + ((c ^ (2 * ((row >> 2) & 3))) << 4);
+// Two floats as packed bf16 (round to nearest even), low half first.
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 template <typename T, bool AK, bool BK, GemmEpilogue EPI, typename LT>
@@ -425,6 +432,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
     for (int j = 0; j < kFrag; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   constexpr int SK = kSlab / Elem<T>::kSize;
+  // The logits epilogue wants each lane to own consecutive columns of a row.
+  constexpr bool kSwapAB = EPI == GemmEpilogue::Logits;
 
   // Full stages (nkf of them) run through the ring; a partial last stage
   // (K % SK != 0) is handled after the loop. Every iteration issues the same
@@ -528,7 +537,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           const int mm = 2 * pr + q;
-          mfma_bf16(acc[mm >> 3][mm & 7], rcA[mm >> 3], rcB[mm & 7]);
+          if constexpr (kSwapAB)
+            mfma_bf16(acc[mm >> 3][mm & 7], rcB[mm & 7], rcA[mm >> 3]);
+          else
+            mfma_bf16(acc[mm >> 3][mm & 7], rcA[mm >> 3], rcB[mm & 7]);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -563,7 +575,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
       __builtin_amdgcn_sched_barrier(0);
       issue_stage((st + kRing - 1) % kRing, st + kRing - 1);
       __builtin_amdgcn_sched_barrier(0);
-      mfma_step<T>(acc, ra[0], rb[0]);
+      mfma_step<T, kSwapAB>(acc, ra[0], rb[0]);
     }
   }
   if (nkf * SK < g.K) {
@@ -579,7 +591,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(kWaitAll);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_step<T>(acc, ra[1], rb[1]);
+    mfma_step<T, kSwapAB>(acc, ra[1], rb[1]);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (Elem<T>::kSize == 2) mfma_drain();
   }
@@ -615,7 +627,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
     }
   } else {
     // Logits: per-row partial softmax statistics of this 256-column tile, the
-    // label logit, and the logits themselves.
+    // label logit, and the logits themselves. The accumulators hold
+    // transposed blocks (kSwapAB): acc[i][j][e] is row wm*128 + 16i + lrow,
+    // column wn*128 + 16j + 4*lgrp + e, so a lane owns 8 rows x 32 columns
+    // and each row's 128 columns of this wave sit in the 4 lanes lrow + 16g.
     LT* C = static_cast<LT*>(pr.c);
     int64_t* lab = reinterpret_cast<int64_t*>(epi);                      // [256]
     float4* part = reinterpret_cast<float4*>(epi + 2048);                // [2][256]
@@ -624,54 +639,92 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
       lab[tid] = row < g.M ? g.lg.labels[row] : g.lg.ignore_index;
     }
     __syncthreads();
-    constexpr bool kStage = Elem<LT>::kSize == 2;   // bf16 logits go through LDS
     const float it2 = g.lg.inv_t * kLog2e;
-    bool cv[kFrag];
+    const int64_t colw = static_cast<int64_t>(tc.n0) + wn * 128 + 4 * lgrp;   // (j, e) = (0, 0)
+    const int64_t ncol64 = g.N - colw;                    // (j, e) valid iff 16j + e < ncol
+    const int ncol = static_cast<int>(ncol64 < 128 ? (ncol64 < 0 ? 0 : ncol64) : 128);
+    // Full tiles (all but the last column tile when N % 256 != 0) take a
+    // path without per-column checks.
+    auto rows = [&](auto full_c) {
+      constexpr bool kFull = decltype(full_c)::value;
 #pragma unroll
-    for (int j = 0; j < kFrag; ++j) cv[j] = (col_l + j * 16) < g.N;
-#pragma unroll
-    for (int i = 0; i < kFrag; ++i) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int rl = wm * 128 + i * 16 + lgrp * 4 + e;   // row within tile
+      for (int i = 0; i < kFrag; ++i) {
+        const int rl = wm * 128 + i * 16 + lrow;           // row within tile
         const int64_t row = tc.m0 + rl;
-        const int64_t y = lab[rl];
+        const int64_t yl64 = lab[rl] - colw;
+        const int yl = (yl64 >= 0 && yl64 < 128) ? static_cast<int>(yl64) : -1;
         float mx = -INFINITY;
 #pragma unroll
         for (int j = 0; j < kFrag; ++j)
-          if (cv[j]) mx = fmaxf(mx, acc[i][j][e]);
-        mx = wave16_max(mx);
-        float d1 = 0.f, dT = 0.f, sx = 0.f;
-        if (mx != -INFINITY) {
 #pragma unroll
-          for (int j = 0; j < kFrag; ++j) {
-            if (cv[j]) {
-              const float x = acc[i][j][e];
-              const float dx = x - mx;
-              d1 += __builtin_amdgcn_exp2f(dx * kLog2e);
-              dT += __builtin_amdgcn_exp2f(dx * it2);
+          for (int e = 0; e < 4; ++e)
+            if (kFull || j * 16 + e < ncol) mx = fmaxf(mx, acc[i][j][e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        float d1 = 0.f, dT = 0.f, sx = 0.f;
+#pragma unroll
+        for (int j = 0; j < kFrag; ++j) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float x = acc[i][j][e];
+            const float dx = x - mx;
+            const float a1 = __builtin_amdgcn_exp2f(dx * kLog2e);
+            const float aT = __builtin_amdgcn_exp2f(dx * it2);
+            if (kFull || j * 16 + e < ncol) {
+              d1 += a1;
+              dT += aT;
               sx += x;
             }
           }
         }
-        d1 = wave16_sum(d1);
-        dT = wave16_sum(dT);
-        sx = wave16_sum(sx);
-        if (lrow == 0) part[wn * 256 + rl] = make_float4(mx, d1, dT, sx);
+        // The label's logit, if this lane holds its column (16j + e == yl):
+        // select e, then j.
+        const bool hit = yl >= 0 && (yl & 12) == 0;
+        const int jy = yl >> 4, ey = yl & 3;
+        float xy = 0.f;
 #pragma unroll
         for (int j = 0; j < kFrag; ++j) {
-          const int64_t col = col_l + j * 16;
-          if (col == y && row < g.M) g.lg.xy[tc.p * g.M + row] = acc[i][j][e];
-          if constexpr (kStage) {
-            const int cl = wn * 128 + j * 16 + lrow;    // column within tile
-            const __bf16 b = static_cast<__bf16>(acc[i][j][e]);
-            *reinterpret_cast<__bf16*>(smem + stage_off(rl, cl >> 3) + (cl & 7) * 2) = b;
-          } else {
-            if (cv[j] && row < g.M) C[row * g.ldc + col] = static_cast<LT>(acc[i][j][e]);
+          float t = acc[i][j][0];
+          t = ey == 1 ? acc[i][j][1] : t;
+          t = ey == 2 ? acc[i][j][2] : t;
+          t = ey == 3 ? acc[i][j][3] : t;
+          xy = jy == j ? t : xy;
+        }
+        d1 += __shfl_xor(d1, 16);
+        dT += __shfl_xor(dT, 16);
+        sx += __shfl_xor(sx, 16);
+        d1 += __shfl_xor(d1, 32);
+        dT += __shfl_xor(dT, 32);
+        sx += __shfl_xor(sx, 32);
+        if (lgrp == 0) part[wn * 256 + rl] = make_float4(mx, d1, dT, sx);
+        if (row < g.M) {
+          if (hit) g.lg.xy[tc.p * g.M + row] = xy;
+          LT* crow = C + row * g.ldc + colw;
+#pragma unroll
+          for (int j = 0; j < kFrag; ++j) {
+            const f32x4 v = acc[i][j];
+            if (kFull || j * 16 + 4 <= ncol) {
+              if constexpr (Elem<LT>::kSize == 2) {
+                u32x2 w;
+                w[0] = pack_bf16(v[0], v[1]);
+                w[1] = pack_bf16(v[2], v[3]);
+                *reinterpret_cast<u32x2*>(crow + j * 16) = w;
+              } else {
+                *reinterpret_cast<f32x4*>(crow + j * 16) = v;
+              }
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (j * 16 + e < ncol) crow[j * 16 + e] = static_cast<LT>(v[e]);
+            }
           }
         }
       }
-    }
+    };
+    if (tc.n0 + kTile <= g.N)
+      rows(SlotC<1>{});
+    else
+      rows(SlotC<0>{});
     __syncthreads();
     {
       const int64_t row = tc.m0 + tid;
@@ -693,26 +746,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
           s.z = a.z * fa + b.z * fb;
         }
         g.lg.stats[(static_cast<int64_t>(tc.p) * g.M + row) * g.lg.stats_ld + tc.ntile] = s;
-      }
-    }
-    if constexpr (kStage) {
-      // 256 rows x 32 chunks of 16 B; a wave covers two rows per instruction.
-      const int ncols = static_cast<int>(g.N - tc.n0 < 256 ? g.N - tc.n0 : 256);
-#pragma unroll 4
-      for (int it = 0; it < 32; ++it) {
-        const int idx = it * kThreads + tid;
-        const int rl = idx >> 5, c = idx & 31;
-        const int64_t row = tc.m0 + rl;
-        if (row < g.M && c * 8 < ncols) {
-          const u32x4 v = *reinterpret_cast<const u32x4*>(smem + stage_off(rl, c));
-          LT* dst = C + row * g.ldc + tc.n0 + c * 8;
-          if (c * 8 + 8 <= ncols) {
-            *reinterpret_cast<u32x4*>(dst) = v;
-          } else {
-            const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
-            for (int q = 0; c * 8 + q < ncols; ++q) reinterpret_cast<uint16_t*>(dst)[q] = h[q];
-          }
-        }
       }
     }
   }
