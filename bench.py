@@ -158,6 +158,112 @@ def cpu_baseline(wl, budget_rows=(2, 6)):
                        f"({est:.0f} s)")}
 
 
+# ------------------------------------------------------------ profiles
+KERNEL_CLASSES = (
+    # (substring of the kernel name, kernel kind)
+    ("gemm_kk_logits_", "gemm_logits"),
+    ("gemm_km_", "gemm_grad_hidden"),
+    ("gemm_mm_", "gemm_grad_weight"),
+    ("gemm_kk_", "gemm_nt"),
+    ("row_pass_kernel", "row_pass"),
+    ("row_stats_kernel", "row_stats"),
+    ("finalize_kernel", "finalize"),
+    ("quant_kernel", "quant"),
+    ("mark_targets", "mark_targets"),
+    ("convert_rows", "convert_rows"),
+    ("zero_pad", "zero_pad"),
+)
+COPY_KERNEL = "copyBuffer"          # HIP runtime's device-to-device copy kernel
+
+
+def kernel_kind(name):
+    for key, kind in KERNEL_CLASSES:
+        if key in name:
+            return kind
+    if "copyBufferRect" in name:
+        return "copy_rect"
+    if COPY_KERNEL in name:
+        return "copy"
+    return None
+
+
+def traffic_path(workload):
+    return os.path.join(ROOT, "profiles", f"{workload.replace('-', '_')}_hbm_traffic.md")
+
+
+def read_traffic(workload, kind):
+    """HBM bytes per launch of `kind` from the committed PMC summary, or None."""
+    import re
+    path = traffic_path(workload)
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"^traffic-json: (\{.*\})$", open(path).read(), flags=re.M)
+    if not m:
+        return None
+    rec = json.loads(m.group(1)).get(kind)
+    return None if rec is None else rec["bytes_per_launch"]
+
+
+def summarize(dirs, copy_bytes):
+    """Markdown summary of rocprofv3 output directories: kernel-trace stats
+    (per kernel kind) and, where present, FETCH_SIZE / WRITE_SIZE counter
+    collections turned into HBM bytes per launch with the copy-kernel factor
+    (bytes the copy moves / bytes the counter reports for it)."""
+    import csv
+    import glob
+    from collections import defaultdict
+    stats = defaultdict(lambda: [0, 0.0])           # kind -> [calls, total ns]
+    counters = defaultdict(lambda: defaultdict(list))   # counter -> kind -> [KiB per dispatch]
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                k = kernel_kind(r["Name"])
+                if k:
+                    stats[k][0] += int(r["Calls"])
+                    stats[k][1] += float(r["TotalDurationNs"])
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                k = kernel_kind(r["Kernel_Name"])
+                if k:
+                    counters[r["Counter_Name"]][k].append(float(r["Counter_Value"]))
+    out = []
+    if stats:
+        out.append("| kernel | calls | avg duration (ms) | total (ms) |")
+        out.append("|---|---|---|---|")
+        for k, (n, ns) in sorted(stats.items(), key=lambda x: -x[1][1]):
+            out.append(f"| {k} | {n} | {ns / n / 1e6:.4f} | {ns / 1e6:.3f} |")
+    traffic = {}
+    if counters:
+        factors = {}
+        for c in ("FETCH_SIZE", "WRITE_SIZE"):
+            cp = counters.get(c, {}).get("copy")
+            if cp and copy_bytes:
+                factors[c] = copy_bytes / (max(cp) * 1024.0)
+        out.append("")
+        out.append("| kernel | FETCH_SIZE KiB/launch | WRITE_SIZE KiB/launch | "
+                   "HBM bytes/launch (calibrated) |")
+        out.append("|---|---|---|---|")
+        kinds = sorted(set(counters.get("FETCH_SIZE", {})) | set(counters.get("WRITE_SIZE", {})))
+        for k in kinds:
+            fe = counters.get("FETCH_SIZE", {}).get(k, [])
+            wr = counters.get("WRITE_SIZE", {}).get(k, [])
+            fe_avg = sum(fe) / len(fe) if fe else 0.0
+            wr_avg = sum(wr) / len(wr) if wr else 0.0
+            b = None
+            if "FETCH_SIZE" in factors and "WRITE_SIZE" in factors:
+                b = fe_avg * 1024 * factors["FETCH_SIZE"] + wr_avg * 1024 * factors["WRITE_SIZE"]
+                traffic[k] = {"bytes_per_launch": round(b), "fetch_kib": round(fe_avg, 1),
+                              "write_kib": round(wr_avg, 1)}
+            out.append(f"| {k} | {fe_avg:.1f} | {wr_avg:.1f} | "
+                       f"{'-' if b is None else f'{b:.4g}'} |")
+        for c, f in factors.items():
+            out.append(f"\n{c} calibration: copy of {copy_bytes} bytes -> factor {f:.4f} "
+                       "bytes per reported byte")
+        out.append("")
+        out.append("traffic-json: " + json.dumps(traffic))
+    return "\n".join(out)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -165,7 +271,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="before the timed steps, run one device-to-device copy of BYTES "
+                         "(reference kernel for HBM counter calibration)")
+    ap.add_argument("--summarize", nargs="+", metavar="DIR",
+                    help="print a markdown summary of rocprofv3 output directories and exit")
     args = ap.parse_args()
+    if args.summarize:
+        print(summarize(args.summarize, args.copy_calibration))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(this build has no multi-GPU path).", file=sys.stderr)
@@ -193,6 +307,15 @@ def main():
     if out.grad_teacher_weight is not None:
         outputs["grad_teacher_weight"] = out.grad_teacher_weight
     plan = out.chunk_plan
+    if args.copy_calibration:
+        n = args.copy_calibration // 4
+        src = torch.ones(n, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy of {n * 4} bytes done")
+        del src, dst
     ctx.reset_timing()
     ctx.set_timing(True)
     torch.cuda.synchronize()
@@ -231,7 +354,8 @@ def main():
     roofline = {"bound": d["bound"], "kernel": dom, "achieved": d["achieved"], "peak": d["peak"],
                 "unit": d["unit"], "frac": d["frac"],
                 "work_per_launch": d["work_per_step"] / n_launch,
-                "avg_launch_ms": d["ms_per_step"] / n_launch, "traffic": None}
+                "avg_launch_ms": d["ms_per_step"] / n_launch,
+                "traffic": read_traffic(args.workload, dom)}
     rows_per_s = bt * args.steps / elapsed
     line = {
         "metric": "fwd+bwd rows/sec at BT=8192 H=4096 V=131072; MFMA util %; row-pass HBM GB/s",

@@ -128,10 +128,12 @@ warnings = set()
 def check(path):
     text = open(path).read()
     errors = set()
+    checked = 0
     for fn in re.split(r"\n(?=_Z\w+:)", text):
         name = fn.split(":")[0]
-        if "gemm_kernelIDF16b" not in name:
+        if not re.search(r"gemm_(kk|km|mm)_(logits|store|accum)_bf16", name):
             continue
+        checked += 1
         end = fn.find("s_endpgm")
         body = fn[: fn.find("\n", end) if end >= 0 else len(fn)]
         if re.search(r"scratch_(load|store)", body):
@@ -156,6 +158,8 @@ def check(path):
                     entry[j] = merged
                     if j not in work:
                         work.append(j)
+    if checked < 8:
+        errors.add(f"expected the 8 bf16 GEMM variants, found {checked}")
     return sorted(errors)
 
 

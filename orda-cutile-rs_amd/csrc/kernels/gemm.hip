@@ -406,7 +406,7 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
 }
 
 template <typename T, bool AK, bool BK, GemmEpilogue EPI, typename LT>
-__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
+__device__ __forceinline__ void gemm_body(const GemmArgs& g) {
   // Ring layout: A tiles of slots 0-3, then B tiles of slots 0-3 (16 KB
   // each), so every slot offset fits a DS instruction's immediate.
   __shared__ __attribute__((aligned(1024))) unsigned char smem[kRing * kStageBytes + kEpiLds];
@@ -751,38 +751,47 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs g) {
   }
 }
 
-template <typename T, bool AK, bool BK, GemmEpilogue EPI, typename LT>
-hipError_t launch_t(const GemmArgs& g, hipStream_t s) {
-  const int64_t Mt = (g.M + kTile - 1) / kTile;
-  const int64_t Nt = (g.N + kTile - 1) / kTile;
-  const int64_t tiles = Mt * Nt * g.nprob;
-  if (tiles == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_kernel<T, AK, BK, EPI, LT>), dim3(static_cast<unsigned>(tiles)),
-                     dim3(kThreads), 0, s, g);
-  return hipGetLastError();
-}
+// One named entry point per variant, so that profiles and the build's ISA
+// check can tell them apart: gemm_<A layout><B layout>_<epilogue>_<input>
+// [_<logits type>], layout k = K-major, m = M/N-major.
+#define ORDA_GEMM(NAME, T, AK, BK, EPI, LT) \
+  __global__ __launch_bounds__(kThreads, 1) void NAME(GemmArgs g) { gemm_body<T, AK, BK, EPI, LT>(g); }
+ORDA_GEMM(gemm_kk_logits_bf16_bf16, __bf16, true, true, GemmEpilogue::Logits, __bf16)
+ORDA_GEMM(gemm_kk_logits_bf16_f32, __bf16, true, true, GemmEpilogue::Logits, float)
+ORDA_GEMM(gemm_kk_store_bf16, __bf16, true, true, GemmEpilogue::StoreF32, float)
+ORDA_GEMM(gemm_kk_accum_bf16, __bf16, true, true, GemmEpilogue::AccumF32, float)
+ORDA_GEMM(gemm_km_store_bf16, __bf16, true, false, GemmEpilogue::StoreF32, float)
+ORDA_GEMM(gemm_km_accum_bf16, __bf16, true, false, GemmEpilogue::AccumF32, float)
+ORDA_GEMM(gemm_mm_store_bf16, __bf16, false, false, GemmEpilogue::StoreF32, float)
+ORDA_GEMM(gemm_mm_accum_bf16, __bf16, false, false, GemmEpilogue::AccumF32, float)
+ORDA_GEMM(gemm_kk_logits_f32_bf16, float, true, true, GemmEpilogue::Logits, __bf16)
+ORDA_GEMM(gemm_kk_logits_f32_f32, float, true, true, GemmEpilogue::Logits, float)
+ORDA_GEMM(gemm_kk_store_f32, float, true, true, GemmEpilogue::StoreF32, float)
+ORDA_GEMM(gemm_kk_accum_f32, float, true, true, GemmEpilogue::AccumF32, float)
+ORDA_GEMM(gemm_km_store_f32, float, true, false, GemmEpilogue::StoreF32, float)
+ORDA_GEMM(gemm_km_accum_f32, float, true, false, GemmEpilogue::AccumF32, float)
+ORDA_GEMM(gemm_mm_store_f32, float, false, false, GemmEpilogue::StoreF32, float)
+ORDA_GEMM(gemm_mm_accum_f32, float, false, false, GemmEpilogue::AccumF32, float)
+#undef ORDA_GEMM
 
-template <typename T>
-hipError_t dispatch_layout(const GemmArgs& g, hipStream_t s) {
+typedef void (*GemmKernel)(GemmArgs);
+
+GemmKernel select_kernel(const GemmArgs& g) {
   using E = GemmEpilogue;
+  const bool bf = g.in_type == DType::BF16;
   if (g.epi == E::Logits) {
-    if (!g.a_kmajor || !g.b_kmajor) return hipErrorInvalidValue;
-    if (g.logits_type == DType::BF16) return launch_t<T, true, true, E::Logits, __bf16>(g, s);
-    return launch_t<T, true, true, E::Logits, float>(g, s);
+    if (!g.a_kmajor || !g.b_kmajor) return nullptr;
+    if (g.logits_type == DType::BF16) return bf ? gemm_kk_logits_bf16_bf16 : gemm_kk_logits_f32_bf16;
+    return bf ? gemm_kk_logits_bf16_f32 : gemm_kk_logits_f32_f32;
   }
-  if (g.a_kmajor && !g.b_kmajor) {
-    if (g.epi == E::StoreF32) return launch_t<T, true, false, E::StoreF32, float>(g, s);
-    return launch_t<T, true, false, E::AccumF32, float>(g, s);
-  }
-  if (!g.a_kmajor && !g.b_kmajor) {
-    if (g.epi == E::StoreF32) return launch_t<T, false, false, E::StoreF32, float>(g, s);
-    return launch_t<T, false, false, E::AccumF32, float>(g, s);
-  }
-  if (g.a_kmajor && g.b_kmajor) {
-    if (g.epi == E::StoreF32) return launch_t<T, true, true, E::StoreF32, float>(g, s);
-    return launch_t<T, true, true, E::AccumF32, float>(g, s);
-  }
-  return hipErrorInvalidValue;
+  const bool st = g.epi == E::StoreF32;
+  if (g.a_kmajor && g.b_kmajor)
+    return bf ? (st ? gemm_kk_store_bf16 : gemm_kk_accum_bf16) : (st ? gemm_kk_store_f32 : gemm_kk_accum_f32);
+  if (g.a_kmajor && !g.b_kmajor)
+    return bf ? (st ? gemm_km_store_bf16 : gemm_km_accum_bf16) : (st ? gemm_km_store_f32 : gemm_km_accum_f32);
+  if (!g.a_kmajor && !g.b_kmajor)
+    return bf ? (st ? gemm_mm_store_bf16 : gemm_mm_accum_bf16) : (st ? gemm_mm_store_f32 : gemm_mm_accum_f32);
+  return nullptr;
 }
 
 }  // namespace
@@ -794,8 +803,11 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
   if ((g.lda % 8) || (g.ldb % 8) || (g.ldc % 8 && g.epi == GemmEpilogue::Logits))
     return hipErrorInvalidValue;
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
-  if (g.in_type == DType::BF16) return dispatch_layout<__bf16>(g, stream);
-  return dispatch_layout<float>(g, stream);
+  const GemmKernel k = select_kernel(g);
+  if (k == nullptr) return hipErrorInvalidValue;
+  const int64_t tiles = ((g.M + kTile - 1) / kTile) * ((g.N + kTile - 1) / kTile) * g.nprob;
+  hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, stream, g);
+  return hipGetLastError();
 }
 
 }  // namespace orda
