@@ -105,9 +105,10 @@ def work_per_step(wl, plan):
         dgrad = 2 * bt * v * h
         wgrad = dgrad
         t_rows_written = 0
-    # row pass: read student + teacher logits once, write the gradient rows
+    # row pass: read student + teacher logits once (kept in fp32), write the
+    # gradient rows in the input dtype
     rows_read = 2 * bt
-    rowpass = (rows_read + bt + t_rows_written) * v * es
+    rowpass = rows_read * v * 4 + (bt + t_rows_written) * v * es
     quant_b = v * h * 8 if quant else 0
     return {"gemm_logits": ("mfma", fwd), "gemm_grad_hidden": ("mfma", dgrad),
             "gemm_grad_weight": ("mfma", wgrad), "row_pass": ("hbm", rowpass),

@@ -10,13 +10,15 @@
 // the optional INT8 round trip and the f64 loss assembly.
 //
 // Device-first layout: the logits of consecutive chunks are kept side by
-// side in one staging buffer (student block, then teacher block, each
-// [rows, round_up(V, 8)]); each chunk's logits_chunk is a slice of it, and
-// the backward GEMMs run once per group of chunks so grad_W is written once
-// per group instead of read-modified-written per chunk. The group size is
-// bounded by the context's staging budget; an out-of-memory failure first
-// halves the group, then walks the reference's chunk-doubling schedule
-// (resolver.rs:107-126).
+// side in one fp32 staging buffer (student block, then teacher block, each
+// [rows, round_up(V, 8)]); each chunk's logits_chunk is a slice of it. The
+// logits GEMM and the row pass run once per group of chunks, and so do the
+// backward GEMMs, which read the gradient rows (in place for f32 inputs, a
+// bf16 copy for bf16 inputs); grad_W is therefore written once per group
+// instead of read-modified-written per chunk. The group size is bounded by
+// the context's staging budget (16 GiB by default); an out-of-memory
+// failure first halves the group, then walks the reference's
+// chunk-doubling schedule (resolver.rs:107-126).
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -38,7 +40,7 @@ struct orda_ctx {
   hipStream_t stream = nullptr;
   int64_t mem_limit = 0;
   int64_t held = 0;
-  int64_t staging_budget = int64_t(8) << 30;
+  int64_t staging_budget = int64_t(16) << 30;
   struct Buf {
     void* p = nullptr;
     int64_t bytes = 0;
@@ -360,10 +362,18 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   const int blocks = P.need_teacher ? 2 : 1;
   const bool tied_tce = P.mode == ORDA_TEACHER_TIED && P.w_t > 0.f;
 
-  void* L = ws(c, "logits", blocks * cap * ldl * es);
-  float4* stats = static_cast<float4*>(ws(c, "stats", 2 * cs * nst * 16));
-  float* xy = static_cast<float*>(ws(c, "xy", 2 * cs * 4));
-  hip_check(hipMemsetAsync(xy, 0, 2 * cs * 4, c->stream), "hipMemsetAsync");
+  // Logits are kept in fp32 so that the loss terms (statistics, label logits,
+  // the KL cross term) use the same values as the reference. The gradient
+  // rows the backward GEMMs read are in the input dtype: in place for f32
+  // inputs, a separate bf16 buffer for bf16 inputs.
+  const DType lt = DType::F32;
+  void* L = ws(c, "logits", blocks * cap * ldl * 4);
+  void* Gb = dt == DType::F32 ? L : ws(c, "dlogits", blocks * cap * ldl * es);
+  // Statistics and label logits of a whole group: student rows, then teacher
+  // rows (the logits GEMM of problem p writes row p*M + r).
+  float4* stats = static_cast<float4*>(ws(c, "stats", 2 * cap * nst * 16));
+  float* xy = static_cast<float*>(ws(c, "xy", 2 * cap * 4));
+  hip_check(hipMemsetAsync(xy, 0, 2 * cap * 4, c->stream), "hipMemsetAsync");
   float* rnll_s = row3_out;
   float* rnll_t = row3_out + bt;
   float* rkl = row3_out + 2 * bt;
@@ -378,95 +388,98 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
     const int64_t ge = std::min(bt, g1 * cs);
     const int64_t btg = ge - gs;
     void* Ls = L;
-    void* Lt = at(L, btg * ldl, dt);
+    void* Lt = at(L, btg * ldl, lt);
+    void* Gs = Gb;
+    void* Gt = at(Gb, btg * ldl, dt);
     const bool first = g0 == 0;
     const bool last = ge >= bt;
 
-    for (int64_t ci = g0; ci < g1; ++ci) {
-      const int64_t start = ci * cs;
-      if (start >= bt) break;
-      const int64_t end = std::min(start + cs, bt);
-      const int64_t n = end - start;
-      const int64_t sc = start - gs;
+    // The chunks of a group are computed together: each logit, each row's
+    // statistics and each row's gradient depend on that row alone, so one
+    // launch over the group's rows gives the per-chunk results of
+    // src/api.rs:263-344 exactly; the per-chunk sums are formed from the
+    // per-row values in finalize.
 
-      // ---- logits_chunk = [h_s; h_t] · Wᵀ (api.rs:272-299) with statistics
-      GemmArgs f{};
-      f.M = n;
-      f.N = v;
-      f.K = h;
-      f.lda = in.hs.ld;
-      f.ldb = in.W.ld;
-      f.ldc = ldl;
-      f.a_kmajor = f.b_kmajor = true;
-      f.in_type = dt;
-      f.logits_type = dt;
-      f.epi = GemmEpilogue::Logits;
-      f.alpha = 1.f;
-      f.lg.stats = stats;
-      f.lg.stats_ld = nst;
-      f.lg.xy = xy;
-      f.lg.labels = in.labels + start;
-      f.lg.ignore_index = P.ignore;
-      f.lg.inv_t = inv_t;
-      f.nprob = 1;
-      f.prob[0] = {at(in.hs.p, start * in.hs.ld, dt), in.W.p, at(Ls, sc * ldl, dt)};
-      const bool fuse_t = P.need_teacher && P.mode == ORDA_TEACHER_TIED && in.th.ld == in.hs.ld;
-      if (fuse_t) {
-        f.nprob = 2;
-        f.prob[1] = {at(in.th.p, start * in.th.ld, dt), in.W.p, at(Lt, sc * ldl, dt)};
+    // ---- logits = [h_s; h_t] · Wᵀ (api.rs:272-299) with tile statistics
+    GemmArgs f{};
+    f.M = btg;
+    f.N = v;
+    f.K = h;
+    f.lda = in.hs.ld;
+    f.ldb = in.W.ld;
+    f.ldc = ldl;
+    f.a_kmajor = f.b_kmajor = true;
+    f.in_type = dt;
+    f.logits_type = lt;
+    f.epi = GemmEpilogue::Logits;
+    f.alpha = 1.f;
+    f.lg.stats = stats;
+    f.lg.stats_ld = nst;
+    f.lg.xy = xy;
+    f.lg.labels = in.labels + gs;
+    f.lg.ignore_index = P.ignore;
+    f.lg.inv_t = inv_t;
+    f.nprob = 1;
+    f.prob[0] = {at(in.hs.p, gs * in.hs.ld, dt), in.W.p, Ls};
+    const bool fuse_t = P.need_teacher && P.mode == ORDA_TEACHER_TIED && in.th.ld == in.hs.ld;
+    if (fuse_t) {
+      f.nprob = 2;
+      f.prob[1] = {at(in.th.p, gs * in.th.ld, dt), in.W.p, Lt};
+    }
+    f.group_m = 8;
+    timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_gemm(f, c->stream); });
+    if (P.need_teacher && !fuse_t) {
+      if (P.mode == ORDA_TEACHER_PRECOMPUTED) {
+        RowStatsArgs r{};
+        r.src_type = in.tl.t;
+        r.src = at(in.tl.p, gs * in.tl.ld, in.tl.t);
+        r.lds = in.tl.ld;
+        r.dst_type = lt;
+        r.dst = Lt;
+        r.ldd = ldl;
+        r.n_rows = btg;
+        r.v = v;
+        r.stats = stats + btg * nst;
+        r.stats_ld = nst;
+        r.xy = xy + btg;
+        r.labels = in.labels + gs;
+        r.ignore_index = P.ignore;
+        r.inv_t = inv_t;
+        timed(c, ORDA_KERNEL_OTHER, [&] { return launch_row_stats(r, c->stream); });
+      } else {
+        GemmArgs t = f;
+        t.nprob = 1;
+        const bool sep = P.mode == ORDA_TEACHER_SEPARATE;
+        t.K = sep ? P.ht : h;
+        t.lda = in.th.ld;
+        t.ldb = sep ? in.tw.ld : in.W.ld;
+        t.prob[0] = {at(in.th.p, gs * in.th.ld, dt), sep ? in.tw.p : in.W.p, Lt};
+        t.lg.stats = stats + btg * nst;
+        t.lg.xy = xy + btg;
+        timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_gemm(t, c->stream); });
       }
-      f.group_m = static_cast<int>(((n + 255) / 256) * f.nprob);
-      timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_gemm(f, c->stream); });
-      if (P.need_teacher && !fuse_t) {
-        if (P.mode == ORDA_TEACHER_PRECOMPUTED) {
-          RowStatsArgs r{};
-          r.src_type = in.tl.t;
-          r.src = at(in.tl.p, start * in.tl.ld, in.tl.t);
-          r.lds = in.tl.ld;
-          r.dst_type = dt;
-          r.dst = at(Lt, sc * ldl, dt);
-          r.ldd = ldl;
-          r.n_rows = n;
-          r.v = v;
-          r.stats = stats + n * nst;
-          r.stats_ld = nst;
-          r.xy = xy + n;
-          r.labels = in.labels + start;
-          r.ignore_index = P.ignore;
-          r.inv_t = inv_t;
-          timed(c, ORDA_KERNEL_OTHER, [&] { return launch_row_stats(r, c->stream); });
-        } else {
-          GemmArgs t = f;
-          t.nprob = 1;
-          const bool sep = P.mode == ORDA_TEACHER_SEPARATE;
-          t.K = sep ? P.ht : h;
-          t.lda = in.th.ld;
-          t.ldb = sep ? in.tw.ld : in.W.ld;
-          t.prob[0] = {at(in.th.p, start * in.th.ld, dt), sep ? in.tw.p : in.W.p,
-                       at(Lt, sc * ldl, dt)};
-          t.lg.stats = stats + n * nst;
-          t.lg.xy = xy + n;
-          t.group_m = static_cast<int>((n + 255) / 256);
-          timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_gemm(t, c->stream); });
-        }
-      }
+    }
 
-      // ---- KL + CE + merge, in place (api.rs:301-344)
+    // ---- KL + CE + merge, in place (api.rs:301-344)
+    {
       RowPassArgs r{};
-      r.ltype = dt;
-      r.student = at(Ls, sc * ldl, dt);
-      r.teacher = P.need_teacher ? at(Lt, sc * ldl, dt) : nullptr;
+      r.ltype = lt;
+      r.student = Ls;
+      r.teacher = P.need_teacher ? Lt : nullptr;
+      r.grad_s = dt == lt ? nullptr : Gs;
+      r.grad_t = dt == lt ? nullptr : Gt;
+      r.gtype = dt;
       r.ld = ldl;
-      r.n_rows = n;
+      r.n_rows = btg;
       r.v = v;
       r.stats_s = stats;
-      r.stats_t = stats + n * nst;
+      r.stats_t = stats + btg * nst;
       r.stats_ld = nst;
       r.stats_tiles = nst;
       r.stats_tiles_t = P.mode == ORDA_TEACHER_PRECOMPUTED ? 1 : nst;
       r.xy_s = xy;
-      r.xy_t = xy + n;
-      r.labels = in.labels + start;
+      r.xy_t = xy + btg;
+      r.labels = in.labels + gs;
       r.ignore_index = P.ignore;
       r.w_s = P.w_s;
       r.w_t = P.w_t;
@@ -476,9 +489,9 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       r.teacher_ce = P.w_t > 0.f;
       r.teacher_grad = P.w_t > 0.f && P.mode != ORDA_TEACHER_PRECOMPUTED;
       r.kl = P.kd > 0.f;
-      r.row_nll_s = rnll_s + start;
-      r.row_nll_t = rnll_t + start;
-      r.row_kl = rkl + start;
+      r.row_nll_s = rnll_s + gs;
+      r.row_nll_t = rnll_t + gs;
+      r.row_kl = rkl + gs;
       r.split = false;
       timed(c, ORDA_KERNEL_ROW_PASS, [&] { return launch_row_pass(r, c->stream); });
     }
@@ -499,11 +512,11 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       d.alpha = P.mean_scale;
       d.group_m = 4;
       d.nprob = 1;
-      d.prob[0] = {Ls, in.W.p, in.gh.p + gs * in.gh.ld};
+      d.prob[0] = {Gs, in.W.p, in.gh.p + gs * in.gh.ld};
       const bool fuse = P.has_ght && P.mode == ORDA_TEACHER_TIED && in.ght.ld == in.gh.ld;
       if (fuse) {
         d.nprob = 2;
-        d.prob[1] = {Lt, in.W.p, in.ght.p + gs * in.ght.ld};
+        d.prob[1] = {Gt, in.W.p, in.ght.p + gs * in.ght.ld};
       }
       timed(c, ORDA_KERNEL_GEMM_GRAD_HIDDEN, [&] { return launch_gemm(d, c->stream); });
       if (P.has_ght && !fuse) {
@@ -513,7 +526,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
         t.N = sep ? P.ht : h;
         t.ldb = sep ? in.tw.ld : in.W.ld;
         t.ldc = in.ght.ld;
-        t.prob[0] = {Lt, sep ? in.tw.p : in.W.p, in.ght.p + gs * in.ght.ld};
+        t.prob[0] = {Gt, sep ? in.tw.p : in.W.p, in.ght.p + gs * in.ght.ld};
         timed(c, ORDA_KERNEL_GEMM_GRAD_HIDDEN, [&] { return launch_gemm(t, c->stream); });
       }
     }
@@ -543,11 +556,11 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
                   "stage hidden");
         w.K = 2 * btg;
         w.ldb = ldh_cat;
-        w.prob[0] = {Ls, hcat, in.gw.p};
+        w.prob[0] = {Gs, hcat, in.gw.p};
       } else {
         w.K = btg;
         w.ldb = in.hs.ld;
-        w.prob[0] = {Ls, at(in.hs.p, gs * in.hs.ld, dt), in.gw.p};
+        w.prob[0] = {Gs, at(in.hs.p, gs * in.hs.ld, dt), in.gw.p};
       }
       timed(c, ORDA_KERNEL_GEMM_GRAD_WEIGHT, [&] { return launch_gemm(w, c->stream); });
       if (P.has_gwt) {
@@ -556,7 +569,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
         t.N = P.ht;
         t.ldb = in.th.ld;
         t.ldc = in.gwt.ld;
-        t.prob[0] = {Lt, at(in.th.p, gs * in.th.ld, dt), in.gwt.p};
+        t.prob[0] = {Gt, at(in.th.p, gs * in.th.ld, dt), in.gwt.p};
         timed(c, ORDA_KERNEL_GEMM_GRAD_WEIGHT, [&] { return launch_gemm(t, c->stream); });
       }
     }
@@ -718,7 +731,10 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
   // ---- chunk plan, staging group, OOM retry (resolver.rs:103-126)
   orda::ChunkPlan plan = plan0;
   const int64_t limit = o->config.has_max_chunks ? o->config.max_chunks : default_max_chunks_limit(bt);
-  const int64_t chunk_bytes = (P.need_teacher ? 2 : 1) * plan.chunk_size * round8(v) * dtype_size(P.dt);
+  const int64_t chunk_bytes =
+      plan.chunk_size * ((P.need_teacher ? 2 : 1) * round8(v) *
+                             (4 + (P.dt == DType::F32 ? 0 : dtype_size(P.dt))) +
+                         2 * gemm_stat_tiles(v) * 16);
   int64_t G = std::max<int64_t>(1, std::min<int64_t>(plan.num_chunks, c->staging_budget / std::max<int64_t>(chunk_bytes, 1)));
   for (;;) {
     try {
@@ -730,6 +746,9 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
       (void)hipGetLastError();
       ws_release(c, "logits");
       ws_release(c, "hcat");
+      ws_release(c, "stats");
+      ws_release(c, "xy");
+      ws_release(c, "dlogits");
       if (G > 1) {
         G /= 2;
         continue;

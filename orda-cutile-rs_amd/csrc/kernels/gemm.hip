@@ -138,17 +138,6 @@ __device__ __forceinline__ uint64_t uniform64(const void* p) {
   return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
-__device__ __forceinline__ float wave16_max(float v) {
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 16));
-  return v;
-}
-__device__ __forceinline__ float wave16_sum(float v) {
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) v += __shfl_xor(v, o, 16);
-  return v;
-}
-
 // ---------------------------------------------------------------- loaders
 // Per-thread description of one operand's 8 DMA transfers per stage.
 // KMAJOR: operand stored [rows of M or N][ld], a stage covers rows

@@ -86,6 +86,11 @@ struct RowPassArgs {
   float* row_nll_s;        // [n_rows] outputs (never null)
   float* row_nll_t;
   float* row_kl;           // KL_row * T^2 (T^2 in f32), 0 when ignored
+  // Gradient rows: written at grad_s/grad_t + r*ld in gtype. Null grad_s
+  // means in place (gtype == ltype).
+  void* grad_s;
+  void* grad_t;
+  DType gtype;
   // Split mode (chunk-launcher entry point): gradients go to separate
   // buffers instead of overwriting the logits, and are not merged.
   bool split;

@@ -262,6 +262,178 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(RowPassArgs a) {
   }
 }
 
+// Eight consecutive logits (16-byte aligned) as fp32, and eight gradients
+// back in the storage type.
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float (&x)[8]);
+template <>
+__device__ __forceinline__ void load8(const float* p, float (&x)[8]) {
+  const u32x4 a = reinterpret_cast<const u32x4*>(p)[0], b = reinterpret_cast<const u32x4*>(p)[1];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[i] = __uint_as_float(a[i]);
+    x[4 + i] = __uint_as_float(b[i]);
+  }
+}
+template <>
+__device__ __forceinline__ void load8(const __bf16* p, float (&x)[8]) {
+  Vec<__bf16>::unpack(*reinterpret_cast<const u32x4*>(p), x);
+}
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const float (&g)[8]);
+template <>
+__device__ __forceinline__ void store8(float* p, const float (&g)[8]) {
+  reinterpret_cast<u32x4*>(p)[0] = u32x4{__float_as_uint(g[0]), __float_as_uint(g[1]),
+                                         __float_as_uint(g[2]), __float_as_uint(g[3])};
+  reinterpret_cast<u32x4*>(p)[1] = u32x4{__float_as_uint(g[4]), __float_as_uint(g[5]),
+                                         __float_as_uint(g[6]), __float_as_uint(g[7])};
+}
+template <>
+__device__ __forceinline__ void store8(__bf16* p, const float (&g)[8]) {
+  *reinterpret_cast<u32x4*>(p) = Vec<__bf16>::pack(g);
+}
+
+// The row pass of distillation_loss, specialised on the logits type LT, the
+// gradient type GT and whether the KL term (KL) and the teacher CE gradient
+// (TG) are present. Same results as row_pass_kernel<LT, false>, with the
+// per-element work cut down for the bandwidth-bound case:
+//  * the CE and KL weights are folded into the exponents,
+//      w_s·p_s = 2^(x_s·log2e − lse_s·log2e + log2|w_s|), likewise kd·T·p_s^T,
+//      kd·T·p_t^T and w_t·p_t, and Σp_t^T(x_t − x_s), Σp_t^T are formed from
+//      kd·T·p_t^T and divided by kd·T once;
+//  * the label column is fixed up by the one thread that holds it, and only
+//    the last, partial group of a row checks column bounds;
+//  * two 8-element groups per row and thread are in flight per iteration;
+//  * an ignored row is a zero fill.
+// Logits are read in LT (fp32, or bf16 only when the inputs are bf16 and
+// the loss terms do not need fp32 logits) and gradients written in GT, in
+// place when grad_s is null.
+template <typename LT, typename GT, bool KL, bool TG>
+__global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a) {
+  __shared__ Stat sstat[kThreads / 64];
+  __shared__ float ssum[kThreads / 64];
+  constexpr int NV = 8;
+  constexpr bool HT = KL || TG;   // the teacher row is read
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t y = a.labels[r];
+  const int64_t v = a.v;
+  const int nvec = static_cast<int>((v + NV - 1) / NV);
+  const int nfull = static_cast<int>(v / NV);
+  const LT* srow = static_cast<const LT*>(a.student) + r * a.ld;
+  const LT* trow = HT ? static_cast<const LT*>(a.teacher) + r * a.ld : nullptr;
+  GT* gsrow = static_cast<GT*>(a.grad_s ? a.grad_s : a.student) + r * a.ld;
+  GT* gtrow = TG ? static_cast<GT*>(a.grad_s ? a.grad_t : a.teacher) + r * a.ld : nullptr;
+
+  if (y == a.ignore_index) {   // cross_entropy.rs:59, kl.rs:92: zero gradient and losses
+    const float z[NV] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int vi = tid; vi < nvec; vi += kThreads) {
+      store8(gsrow + static_cast<int64_t>(vi) * NV, z);
+      if (TG) store8(gtrow + static_cast<int64_t>(vi) * NV, z);
+    }
+    if (tid == 0) {
+      a.row_nll_s[r] = 0.f;
+      a.row_nll_t[r] = 0.f;
+      a.row_kl[r] = 0.f;
+    }
+    return;
+  }
+
+  const float T = a.temperature;
+  const float inv_t = 1.0f / T;
+  const float it2 = inv_t * kLog2e;
+  const Stat ss = load_row_stats(a.stats_s + r * a.stats_ld, a.stats_tiles, it2, sstat);
+  Stat st{-INFINITY, 0.f, 0.f, 0.f};
+  if (HT || a.teacher_ce) st = load_row_stats(a.stats_t + r * a.stats_ld, a.stats_tiles_t, it2, sstat);
+
+  const double alpha = static_cast<double>(a.label_smoothing);
+  const float lse1_s = ss.m + logf(ss.d1);
+  const float lseT_s = ss.m * inv_t + logf(ss.dT);
+  const float lse1_t = st.m + logf(st.d1);
+  const float lseT_t = st.m * inv_t + logf(st.dT);
+  const float eps = static_cast<float>(alpha / static_cast<double>(v));
+  const float one_m_a = 1.0f - a.label_smoothing;
+  const float ws = a.w_s, wt = a.w_t;
+  const float gsc = a.kd * T;                              // kl.rs:85
+  // w_s·p_s (w_s may be any sign; w_t, kd >= 0 are validated by the caller)
+  const float ca = log2f(fabsf(ws)) - lse1_s * kLog2e;
+  const float sgn = ws < 0.f ? -1.f : 1.f;
+  const float cb = KL ? log2f(gsc) - lseT_s * kLog2e : 0.f;   // kd·T·p_s^T
+  const float cc = KL ? log2f(gsc) - lseT_t * kLog2e : 0.f;   // kd·T·p_t^T
+  const float cd = TG ? log2f(wt) - lse1_t * kLog2e : 0.f;    // w_t·p_t
+  const float k0 = -ws * eps, kt0 = -wt * eps;
+  const float ky = ws * one_m_a, kyt = wt * one_m_a;
+
+  float cross = 0.f, sum_c = 0.f;
+  auto compute = [&](int vi, const float (&xs)[NV], const float (&xt)[NV], bool full) {
+    float g[NV], gt[NV];
+    const int64_t j0 = static_cast<int64_t>(vi) * NV;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const bool valid = full || j0 + i < v;
+      float gi = fmaf(sgn, __builtin_amdgcn_exp2f(fmaf(xs[i], kLog2e, ca)), k0);
+      if (KL) {
+        const float b = __builtin_amdgcn_exp2f(fmaf(xs[i], it2, cb));
+        const float c = __builtin_amdgcn_exp2f(fmaf(xt[i], it2, cc));
+        gi += b - c;
+        const float cx = c * (xt[i] - xs[i]);
+        cross += valid ? cx : 0.f;
+        sum_c += valid ? c : 0.f;
+      }
+      g[i] = valid ? gi : 0.f;
+      if (TG) {
+        const float d = __builtin_amdgcn_exp2f(fmaf(xt[i], kLog2e, cd)) + kt0;
+        gt[i] = valid ? d : 0.f;
+      }
+    }
+    const int64_t yl = y - j0;
+    if (yl >= 0 && yl < NV) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        if (i == yl) {
+          g[i] -= ky;
+          if (TG) gt[i] -= kyt;
+        }
+      }
+    }
+    store8(gsrow + j0, g);
+    if (TG) store8(gtrow + j0, gt);
+  };
+  int vi = tid;
+  for (; vi + kThreads < nfull; vi += 2 * kThreads) {
+    const int64_t j0 = static_cast<int64_t>(vi) * NV, j1 = j0 + kThreads * NV;
+    float s0[NV], s1[NV], t0[NV], t1[NV];
+    load8(srow + j0, s0);
+    load8(srow + j1, s1);
+    if (HT) {
+      load8(trow + j0, t0);
+      load8(trow + j1, t1);
+    }
+    compute(vi, s0, t0, true);
+    compute(vi + kThreads, s1, t1, true);
+  }
+  for (; vi < nvec; vi += kThreads) {
+    const int64_t j0 = static_cast<int64_t>(vi) * NV;
+    float s0[NV], t0[NV];
+    load8(srow + j0, s0);
+    if (HT) load8(trow + j0, t0);
+    if (vi < nfull) compute(vi, s0, t0, true);
+    else compute(vi, s0, t0, false);
+  }
+
+  if (KL) {
+    cross = block_sum(cross, ssum);
+    sum_c = block_sum(sum_c, ssum);
+  }
+  if (tid == 0) {
+    a.row_nll_s[r] = static_cast<float>(row_nll(ss, a.xy_s[r], alpha, v));
+    float kl_row = 0.f;
+    if (KL) kl_row = ((cross / gsc) * inv_t + (lseT_s - lseT_t) * (sum_c / gsc)) * (T * T);
+    a.row_kl[r] = kl_row;
+    a.row_nll_t[r] = a.teacher_ce ? static_cast<float>(row_nll(st, a.xy_t[r], alpha, v)) : 0.f;
+  }
+}
+
 // ------------------------------------------------------------------ row stats
 template <typename ST, typename DT>
 __global__ __launch_bounds__(kThreads) void row_stats_kernel(RowStatsArgs a) {
@@ -341,13 +513,34 @@ hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
   if (a.n_rows <= 0) return hipSuccess;
   if (a.ld % 8) return hipErrorInvalidValue;
   dim3 grid(static_cast<unsigned>(a.n_rows));
-  if (a.ltype == DType::BF16) {
-    if (a.split) hipLaunchKernelGGL((row_pass_kernel<__bf16, true>), grid, dim3(kThreads), 0, s, a);
-    else hipLaunchKernelGGL((row_pass_kernel<__bf16, false>), grid, dim3(kThreads), 0, s, a);
-  } else {
-    if (a.split) hipLaunchKernelGGL((row_pass_kernel<float, true>), grid, dim3(kThreads), 0, s, a);
-    else hipLaunchKernelGGL((row_pass_kernel<float, false>), grid, dim3(kThreads), 0, s, a);
+  if (a.split) {
+    if (a.ltype == DType::BF16)
+      hipLaunchKernelGGL((row_pass_kernel<__bf16, true>), grid, dim3(kThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((row_pass_kernel<float, true>), grid, dim3(kThreads), 0, s, a);
+    return hipGetLastError();
   }
+  const bool has_t = a.teacher != nullptr;
+  const bool kl = a.kl && has_t;
+  const bool tg = a.teacher_grad && has_t;
+  if ((a.teacher_ce || kl || tg) && a.stats_t == nullptr) return hipErrorInvalidValue;
+  const DType gt = a.grad_s ? a.gtype : a.ltype;
+  if (a.grad_s && (tg && a.grad_t == nullptr)) return hipErrorInvalidValue;
+#define ORDA_ROWPASS(LT, GT)                                                                          \
+  if (kl && tg) hipLaunchKernelGGL((row_pass_fused_kernel<LT, GT, true, true>), grid, dim3(kThreads), 0, s, a);   \
+  else if (kl) hipLaunchKernelGGL((row_pass_fused_kernel<LT, GT, true, false>), grid, dim3(kThreads), 0, s, a);  \
+  else if (tg) hipLaunchKernelGGL((row_pass_fused_kernel<LT, GT, false, true>), grid, dim3(kThreads), 0, s, a);  \
+  else hipLaunchKernelGGL((row_pass_fused_kernel<LT, GT, false, false>), grid, dim3(kThreads), 0, s, a);
+  if (a.ltype == DType::F32 && gt == DType::BF16) {
+    ORDA_ROWPASS(float, __bf16)
+  } else if (a.ltype == DType::F32 && gt == DType::F32) {
+    ORDA_ROWPASS(float, float)
+  } else if (a.ltype == DType::BF16 && gt == DType::BF16) {
+    ORDA_ROWPASS(__bf16, __bf16)
+  } else {
+    return hipErrorInvalidValue;
+  }
+#undef ORDA_ROWPASS
   return hipGetLastError();
 }
 
