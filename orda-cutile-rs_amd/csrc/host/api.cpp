@@ -101,6 +101,14 @@ std::string fmt_f32(float x) {
 
 int64_t round8(int64_t x) { return (x + 7) / 8 * 8; }
 
+// Pitch of the logits staging rows: V rounded up to 8 elements, plus 64 when
+// that is a multiple of 1024, so that rows (and the many row streams the row
+// pass and the GEMMs walk in step) do not sit a power of two apart.
+int64_t logits_pitch(int64_t v) {
+  const int64_t p = round8(v);
+  return p % 1024 == 0 ? p + 64 : p;
+}
+
 int64_t tensor_ld(const orda_tensor& t) { return t.ld ? t.ld : t.cols; }
 
 DType to_dtype(int32_t d, const char* what) {
@@ -356,7 +364,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   const int64_t bt = P.bt, v = P.v, h = P.h;
   const DType dt = P.dt;
   const int es = dtype_size(dt);
-  const int64_t ldl = round8(v);
+  const int64_t ldl = logits_pitch(v);
   const int64_t nst = gemm_stat_tiles(v);
   const int64_t cap = std::min(bt, G * cs);
   const int blocks = P.need_teacher ? 2 : 1;
@@ -732,7 +740,7 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
   orda::ChunkPlan plan = plan0;
   const int64_t limit = o->config.has_max_chunks ? o->config.max_chunks : default_max_chunks_limit(bt);
   const int64_t chunk_bytes =
-      plan.chunk_size * ((P.need_teacher ? 2 : 1) * round8(v) *
+      plan.chunk_size * ((P.need_teacher ? 2 : 1) * logits_pitch(v) *
                              (4 + (P.dt == DType::F32 ? 0 : dtype_size(P.dt))) +
                          2 * gemm_stat_tiles(v) * 16);
   int64_t G = std::max<int64_t>(1, std::min<int64_t>(plan.num_chunks, c->staging_budget / std::max<int64_t>(chunk_bytes, 1)));

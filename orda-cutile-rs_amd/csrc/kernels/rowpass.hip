@@ -121,13 +121,13 @@ struct Vec<__bf16> {
     }
   }
   static __device__ __forceinline__ raw pack(const float (&x)[N]) {
+    // one v_cvt_pk_bf16_f32 (round to nearest even) per pair
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
     raw r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const __bf16 lo = static_cast<__bf16>(x[2 * i]);
-      const __bf16 hi = static_cast<__bf16>(x[2 * i + 1]);
-      r[i] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
-             (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
+      const bf16x2 p = {static_cast<__bf16>(x[2 * i]), static_cast<__bf16>(x[2 * i + 1])};
+      r[i] = __builtin_bit_cast(uint32_t, p);
     }
     return r;
   }
@@ -365,60 +365,91 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
   const float ky = ws * one_m_a, kyt = wt * one_m_a;
 
   float cross = 0.f, sum_c = 0.f;
-  auto compute = [&](int vi, const float (&xs)[NV], const float (&xt)[NV], bool full) {
+  // Gradient of one element pair, without the label term.
+  auto elem = [&](float xs, float xt, float& g, float& gt, float& cx, float& c) {
+    g = fmaf(sgn, __builtin_amdgcn_exp2f(fmaf(xs, kLog2e, ca)), k0);
+    if (KL) {
+      const float b = __builtin_amdgcn_exp2f(fmaf(xs, it2, cb));
+      c = __builtin_amdgcn_exp2f(fmaf(xt, it2, cc));
+      g += b - c;
+      cx = c * (xt - xs);
+    }
+    if (TG) gt = __builtin_amdgcn_exp2f(fmaf(xt, kLog2e, cd)) + kt0;
+  };
+  auto compute = [&](int j0, const float (&xs)[NV], const float (&xt)[NV], bool full) {
     float g[NV], gt[NV];
-    const int64_t j0 = static_cast<int64_t>(vi) * NV;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const bool valid = full || j0 + i < v;
-      float gi = fmaf(sgn, __builtin_amdgcn_exp2f(fmaf(xs[i], kLog2e, ca)), k0);
+      float gi = 0.f, ti = 0.f, cx = 0.f, c = 0.f;
+      elem(xs[i], xt[i], gi, ti, cx, c);
       if (KL) {
-        const float b = __builtin_amdgcn_exp2f(fmaf(xs[i], it2, cb));
-        const float c = __builtin_amdgcn_exp2f(fmaf(xt[i], it2, cc));
-        gi += b - c;
-        const float cx = c * (xt[i] - xs[i]);
         cross += valid ? cx : 0.f;
         sum_c += valid ? c : 0.f;
       }
       g[i] = valid ? gi : 0.f;
-      if (TG) {
-        const float d = __builtin_amdgcn_exp2f(fmaf(xt[i], kLog2e, cd)) + kt0;
-        gt[i] = valid ? d : 0.f;
-      }
-    }
-    const int64_t yl = y - j0;
-    if (yl >= 0 && yl < NV) {
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        if (i == yl) {
-          g[i] -= ky;
-          if (TG) gt[i] -= kyt;
-        }
-      }
+      gt[i] = valid ? ti : 0.f;
     }
     store8(gsrow + j0, g);
     if (TG) store8(gtrow + j0, gt);
   };
-  int vi = tid;
-  for (; vi + kThreads < nfull; vi += 2 * kThreads) {
-    const int64_t j0 = static_cast<int64_t>(vi) * NV, j1 = j0 + kThreads * NV;
-    float s0[NV], s1[NV], t0[NV], t1[NV];
-    load8(srow + j0, s0);
-    load8(srow + j1, s1);
-    if (HT) {
-      load8(trow + j0, t0);
-      load8(trow + j1, t1);
-    }
-    compute(vi, s0, t0, true);
-    compute(vi + kThreads, s1, t1, true);
+  // The label column's logits, read by its owner before the row is
+  // overwritten (the gradient may go in place).
+  const bool owner = tid == (y / NV) % kThreads;
+  float xs_y = 0.f, xt_y = 0.f;
+  if (owner) {
+    xs_y = static_cast<float>(srow[y]);
+    if (HT) xt_y = static_cast<float>(trow[y]);
   }
-  for (; vi < nvec; vi += kThreads) {
-    const int64_t j0 = static_cast<int64_t>(vi) * NV;
+  // Offsets within a row fit 32 bits (V < 2^31). Every thread has at least
+  // nk full groups; those run software pipelined over two register buffers
+  // with a uniform trip count, so each group's loads are in flight while the
+  // previous group computes and every wait covers loads only.
+  constexpr int kStep = kThreads * NV;
+  const int jfull = nfull * NV;
+  const int nk = nfull / kThreads;
+  int j = tid * NV;
+  if (nk > 0) {
+    // Both buffers are loaded before the loop and each is refilled right
+    // after its group is stored, so every compute finds its loads issued
+    // one compute earlier on all paths into it.
+    float as[NV], at[NV], bs[NV], bt[NV];
+    const int jb0 = nk > 1 ? j + kStep : j;
+    load8(srow + j, as);
+    if (HT) load8(trow + j, at);
+    load8(srow + jb0, bs);
+    if (HT) load8(trow + jb0, bt);
+    int k = 0;
+    for (; k + 1 < nk; k += 2) {
+      compute(j, as, at, true);
+      const int ja = k + 2 < nk ? j + 2 * kStep : j;   // re-read when past the end
+      load8(srow + ja, as);
+      if (HT) load8(trow + ja, at);
+      compute(j + kStep, bs, bt, true);
+      const int jb = k + 3 < nk ? j + 3 * kStep : j;
+      load8(srow + jb, bs);
+      if (HT) load8(trow + jb, bt);
+      j += 2 * kStep;
+    }
+    if (k < nk) {
+      compute(j, as, at, true);
+      j += kStep;
+    }
+  }
+  for (; j < nvec * NV; j += kStep) {
     float s0[NV], t0[NV];
-    load8(srow + j0, s0);
-    if (HT) load8(trow + j0, t0);
-    if (vi < nfull) compute(vi, s0, t0, true);
-    else compute(vi, s0, t0, false);
+    load8(srow + j, s0);
+    if (HT) load8(trow + j, t0);
+    if (j < jfull) compute(j, s0, t0, true);
+    else compute(j, s0, t0, false);
+  }
+  // The label column: its owner (the thread that wrote it, so in program
+  // order) rewrites it with the −(1−α)·w term included.
+  if (owner) {
+    float gy = 0.f, ty = 0.f, cx = 0.f, c = 0.f;
+    elem(xs_y, xt_y, gy, ty, cx, c);
+    gsrow[y] = static_cast<GT>(gy - ky);
+    if (TG) gtrow[y] = static_cast<GT>(ty - kyt);
   }
 
   if (KL) {
