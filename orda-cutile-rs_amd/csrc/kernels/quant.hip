@@ -1,7 +1,8 @@
 // quant.hip — INT8 row-wise quantize/dequantize of grad_W on gfx950, and the
 // small element-wise helpers of the host orchestration.
 //
-// One workgroup per row (src/quant.rs:96-144, 157-202):
+// One workgroup per row (src/quant.rs:96-144, 157-202); rows that fit in
+// registers are read once (quant_vec_kernel), longer ones twice:
 //   s    = max(amax, 1e-12) / 127                (f32, IEEE division)
 //   code = clamp(RNE(x / s), -127, 127)           deterministic
 //   code = clamp(floor(x/s) + (frac > u), ...)    stochastic, u from SplitMix64
@@ -74,6 +75,73 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(QuantArgs a) {
   if (a.scales && threadIdx.x == 0) a.scales[r] = s;
 }
 
+// One code and its dequantized value (quant.rs:109-144, 186-199).
+__device__ __forceinline__ float quant_one(const QuantArgs& a, float x, float s, bool keep,
+                                           uint64_t e, int8_t& code) {
+  const float scaled = x / s;
+  if (a.stochastic) {
+    const float fl = floorf(scaled);
+    code = to_code(fl + ((scaled - fl) > uniform_at(a.seed, e) ? 1.0f : 0.0f));
+  } else {
+    code = to_code(rintf(scaled));
+  }
+  return (keep ? x : static_cast<float>(code) * s) * a.grad_output;
+}
+
+// Rows of at most kThreads·4·NV elements with 16-byte aligned rows: each row
+// is read once into registers (float4 per load), reduced to its scale and
+// written once. A kept row written in place with grad_output 1 is already
+// exact and is not written at all.
+template <int NV>
+__global__ __launch_bounds__(kThreads) void quant_vec_kernel(QuantArgs a) {
+  __shared__ float red[kThreads / 64];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int cols = static_cast<int>(a.cols);
+  const float* src = a.src + r * a.lds;
+  float4 x[NV];
+  float amax = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c = (tid + k * kThreads) * 4;
+    x[k] = c < cols ? *reinterpret_cast<const float4*>(src + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(x[k].x), fabsf(x[k].y)), fmaxf(fabsf(x[k].z), fabsf(x[k].w))));
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  amax = red[0];
+#pragma unroll
+  for (int w = 1; w < kThreads / 64; ++w) amax = fmaxf(amax, red[w]);
+  const float s = fmaxf(amax, 1e-12f) / 127.0f;             // quant.rs:54-57
+  const bool keep = a.keep_exact && a.keep_exact[r];
+  const bool write = !(keep && a.dst == a.src && a.ldd == a.lds && a.grad_output == 1.0f);
+  float* dst = a.dst + r * a.ldd;
+  int8_t* q = a.codes ? a.codes + r * a.ldq : nullptr;
+  const uint64_t ebase = static_cast<uint64_t>(r) * static_cast<uint64_t>(a.cols);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c = (tid + k * kThreads) * 4;
+    if (c >= cols) continue;
+    int8_t c0, c1, c2, c3;
+    float4 o;
+    o.x = quant_one(a, x[k].x, s, keep, ebase + c, c0);
+    o.y = quant_one(a, x[k].y, s, keep, ebase + c + 1, c1);
+    o.z = quant_one(a, x[k].z, s, keep, ebase + c + 2, c2);
+    o.w = quant_one(a, x[k].w, s, keep, ebase + c + 3, c3);
+    if (write) *reinterpret_cast<float4*>(dst + c) = o;
+    if (q) {
+      const uint32_t packed = static_cast<uint32_t>(static_cast<uint8_t>(c0)) |
+                              (static_cast<uint32_t>(static_cast<uint8_t>(c1)) << 8) |
+                              (static_cast<uint32_t>(static_cast<uint8_t>(c2)) << 16) |
+                              (static_cast<uint32_t>(static_cast<uint8_t>(c3)) << 24);
+      *reinterpret_cast<uint32_t*>(q + c) = packed;
+    }
+  }
+  if (a.scales && tid == 0) a.scales[r] = s;
+}
+
 __global__ void mark_targets_kernel(const int64_t* labels, int64_t n, int64_t ignore,
                                     uint8_t* keep, int64_t rows) {
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
@@ -105,7 +173,16 @@ unsigned grid_for(int64_t total) {
 
 hipError_t launch_quant(const QuantArgs& a, hipStream_t s) {
   if (a.rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(quant_kernel, dim3(static_cast<unsigned>(a.rows)), dim3(kThreads), 0, s, a);
+  const dim3 grid(static_cast<unsigned>(a.rows)), block(kThreads);
+  const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const bool vec = a.cols % 4 == 0 && a.lds % 4 == 0 && a.ldd % 4 == 0 && al16(a.src) &&
+                   al16(a.dst) && (a.codes == nullptr || (a.ldq % 4 == 0 && (reinterpret_cast<uintptr_t>(a.codes) & 3) == 0));
+  const int64_t per = kThreads * 4;   // elements per float4 of every thread
+  if (vec && a.cols <= per) hipLaunchKernelGGL(quant_vec_kernel<1>, grid, block, 0, s, a);
+  else if (vec && a.cols <= 2 * per) hipLaunchKernelGGL(quant_vec_kernel<2>, grid, block, 0, s, a);
+  else if (vec && a.cols <= 4 * per) hipLaunchKernelGGL(quant_vec_kernel<4>, grid, block, 0, s, a);
+  else if (vec && a.cols <= 8 * per) hipLaunchKernelGGL(quant_vec_kernel<8>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(quant_kernel, grid, block, 0, s, a);
   return hipGetLastError();
 }
 

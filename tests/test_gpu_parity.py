@@ -256,20 +256,29 @@ def test_all_labels_ignored(torch_dev):
 
 # ------------------------------------------------ entry points and host logic
 @pytest.mark.parametrize("stochastic", [False, True])
-def test_quant_entry_point_bit_exact(torch_dev, stochastic):
+@pytest.mark.parametrize("cols", [257, 256, 1000, 4096, 8192])
+def test_quant_entry_point_bit_exact(torch_dev, stochastic, cols):
     """orda_quant_rows_int8 on the same fp32 matrix as the oracle: codes,
-    scales and the dequantized matrix are identical (quant.rs:96-202)."""
+    scales and the dequantized matrix are identical (quant.rs:96-202). The
+    column counts cover the one-read register path (multiples of 4 up to
+    8192, one to eight float4 per thread, the last partly filled) and the
+    two-pass path (257)."""
+    rows = 300 if cols <= 1000 else 64
     rng = np.random.default_rng(9)
-    m = (rng.standard_normal((300, 257)) * rng.uniform(0.001, 3, (300, 1))).astype(np.float32)
+    m = (rng.standard_normal((rows, cols)) * rng.uniform(0.001, 3, (rows, 1))).astype(np.float32)
     m[5] = 0.0
     m[7, :10] = [0.5, 1.5, 2.5, -0.5, -1.5, 127, -127, 63.5, -63.5, 0.0]
-    targets = np.array([3, 3, 17, -100, 299, 0])
+    targets = np.array([3, 3, 17, -100, rows - 1, 0])
     out, q, s = H.quant_rows_int8(gpu(torch_dev, m), gpu(torch_dev, targets), -100, stochastic,
                                   seed=12345)
     rout, rq, rs = O.quant_dequant_grad_w(m, targets, -100, stochastic, 12345)
     np.testing.assert_array_equal(to_np(q), rq)
     np.testing.assert_array_equal(to_np(s), rs)
     np.testing.assert_array_equal(to_np(out), rout)
+    # in place: kept target rows are left as they are, the rest dequantized
+    g = gpu(torch_dev, m)
+    H.quant_rows_int8(g, gpu(torch_dev, targets), -100, stochastic, seed=12345, out=g)
+    np.testing.assert_array_equal(to_np(g), rout)
 
 
 def test_kl_ce_chunk_entry_point(torch_dev):
