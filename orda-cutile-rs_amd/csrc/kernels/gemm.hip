@@ -9,13 +9,17 @@
 // Workgroup tile 256x256, 4 waves each owning 128x128 as 8x8 fragments of
 // 16x16. K advances 64 bytes per stage (32 bf16 / 16 fp32) through a ring of
 // four 32 KB LDS stages. Operands travel global -> LDS by DMA
-// (global_load_lds_dwordx4, 16 bytes per lane, written lane-linearly) issued
-// four stages ahead; the fragments of stage s+1 are read into a second
-// register set while the 64 MFMAs of stage s run, so after each barrier the
-// MFMAs start at once and one barrier per stage suffices:
-//   * K-major tiles are stored [row][64 B] with the 16-byte chunks XOR-
-//     swizzled by row; the swizzle is applied by choosing which global chunk
-//     each lane fetches. Fragment reads are conflict-free ds_read_b128.
+// (global_load_lds_dwordx4, 16 bytes per lane, written lane-linearly). In
+// the bf16 loops the fragments of stage s+1 are read into a second register
+// set while the 64 MFMAs of stage s run, so the MFMAs start at once after a
+// barrier (one per stage). When both operands are K-major the bf16 loop
+// moves stages in pairs (128 bytes of K per row: 8 lanes fetch one full
+// cache line, half the L1 requests of single stages); otherwise it moves
+// single stages four ahead. The fp32 loop moves single stages three ahead:
+//   * K-major tiles are stored [row][64 B] (a pair: [row][128 B]) with the
+//     16-byte chunks XOR-swizzled by row; the swizzle is applied by choosing
+//     which global chunk each lane fetches. Fragment reads are conflict-free
+//     ds_read_b128.
 //   * MN-major tiles are stored [k][256 elements] (bf16: 512 B rows) with an
 //     8-byte-pair swizzle and read with ds_read_b64_tr_b16, the gfx950 LDS
 //     transpose read: lanes 4j..4j+3 of each 16-lane group name row j and
@@ -92,6 +96,7 @@ constexpr int kWaitAll = 0x0070;                              // vmcnt(0) lgkmcn
 constexpr int vm_wait(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
 constexpr int kWaitTwoStages = vm_wait(2 * 2 * kXfers);     // stage s+1 landed
 constexpr int kWaitThreeStages = vm_wait(3 * 2 * kXfers);   // stage 0 landed
+constexpr int kWaitLds = 0xC07F;                              // lgkmcnt(0) only
 
 // One DMA transfer: every active lane copies the 16 bytes at sbase + voff
 // into LDS at M0 + 16 * lane (global_load_lds_dwordx4, saddr form). Written as
@@ -221,6 +226,53 @@ struct Loader {
   }
 };
 
+// Per-thread description of one bf16 operand's DMA transfers for a stage
+// pair (64 elements of K) of the main loop; the pair lands in a double slot
+// of 32 KB:
+//   K-major:  [256 rows][8 chunks of 16 B], chunk q of row r stored at
+//             q ^ (r & 7), so 8 lanes fetch one full 128-byte line of a row;
+//   MN-major: [64 k-rows][32 chunks of 16 B] with the single-stage swizzle,
+//             i.e. two consecutive single-stage slots.
+// Rows/columns past the operand's edge are clamped as in Loader.
+template <bool KMAJOR>
+struct PairLoader {
+  static constexpr int kX = 2 * kXfers;   // transfers per thread per pair
+  const unsigned char* base;
+  int64_t step;                           // bytes from one pair to the next
+  uint32_t goff[kX];
+
+  __device__ __forceinline__ void init(const void* p, int64_t ld, int64_t ext, int origin, int wave,
+                                       int lane) {
+    const int64_t ldb = ld * 2;
+    if (KMAJOR) {
+      base = static_cast<const unsigned char*>(p) + static_cast<int64_t>(origin) * ldb;
+      step = 128;
+      const int rmax = static_cast<int>(ext - 1 - origin);
+#pragma unroll
+      for (int t = 0; t < kX; ++t) {
+        const int P = (t * 4 + wave) * 64 + lane;
+        const int r = P >> 3;
+        const int q = (P & 7) ^ (r & 7);
+        const int rr = r < rmax ? r : rmax;
+        goff[t] = static_cast<uint32_t>(rr * ldb + q * 16);
+      }
+    } else {
+      base = static_cast<const unsigned char*>(p) + static_cast<int64_t>(origin) * 2;
+      step = 64 * ldb;
+      const int cmax = static_cast<int>((ext - 1 - origin) / 8);
+#pragma unroll
+      for (int t = 0; t < kX; ++t) {
+        const int P = (t * 4 + wave) * 64 + lane;
+        const int r = P >> 5;
+        const int c = (P & 31) ^ mnb_swz(r);
+        const int cc = c < cmax ? c : cmax;
+        goff[t] = static_cast<uint32_t>(r * ldb + cc * 16);
+      }
+    }
+  }
+  __device__ __forceinline__ const unsigned char* src(int pair) const { return base + pair * step; }
+};
+
 // ---------------------------------------------------------------- fragments
 // Operand fragment of a stage (64 bytes of K) for 16 rows (or columns)
 // starting at r0 of the tile: lane (m = lane%16, g = lane/16) holds the K
@@ -260,27 +312,38 @@ __device__ __forceinline__ u32x4 read_frag(const unsigned char* tile, int r0, in
   }
 }
 
-// Fragment reader of one bf16 operand for the interleaved main loop. It keeps
-// each lane's LDS byte address of every read of ring slot 0; slot s lies
-// s * kOpBytes further, which the read takes as its immediate offset:
-//   K-major:  fragment i sits 1024*i bytes after fragment 0 (the row swizzle
-//             depends on the row's low bits only) — one ds_read_b128 each;
-//   MN-major: two transpose reads per fragment (h = 0, 1); fragment i of read
-//             h sits at off[h] ^ (i << 5), because i only moves chunk bits 1-3
-//             of the row, which are the bits the swizzle XORs.
+// Fragment reader of one bf16 operand for the interleaved main loops. Each
+// lane keeps its LDS byte addresses of the reads of ring stage 0 (and, for a
+// paired K-major tile, of stage 1); the rest is the read's immediate:
+//   K-major, single stages (slot s at s * kOpBytes): fragment i sits 1024*i
+//             bytes after fragment 0 (the row swizzle depends on the row's
+//             low bits only) — one ds_read_b128 each;
+//   K-major, paired (PairLoader's double slots; stage s is half s%2 of
+//             double slot s/2): fragment i sits 2048*i bytes after fragment
+//             0; the stage half selects chunk bit 2, which the swizzle XORs,
+//             hence one base address per half;
+//   MN-major (either ring; stage s at s * kOpBytes): two transpose reads per
+//             fragment (h = 0, 1); fragment i of read h sits at
+//             off[h] ^ (i << 5), because i only moves chunk bits 1-3 of the
+//             row, which are the bits the swizzle XORs.
 // read_op<SLOT>(o) issues LDS instruction o of a stage: fragment o (K-major)
 // or half o%2 of fragment o/2 (MN-major).
-template <bool KMAJOR>
+template <bool KMAJOR, bool PAIRED>
 struct FragReader {
   static constexpr int kOps = KMAJOR ? kFrag : 2 * kFrag;
-  uint32_t addr[KMAJOR ? 1 : 2 * kFrag];
+  uint32_t addr[KMAJOR ? 2 : 2 * kFrag];
 
-  // tile0: LDS byte address of this operand's tile in slot 0; w0: the wave
+  // tile0: LDS byte address of this operand's stage-0 slot; w0: the wave
   // strip's first row (K-major) or column (MN-major).
   __device__ __forceinline__ void init(uint32_t tile0, int w0, int lane) {
     const int m = lane & 15, g = lane >> 4;
-    if constexpr (KMAJOR) {
-      addr[0] = tile0 + static_cast<uint32_t>(kmaj_off(w0 + m, g));
+    if constexpr (KMAJOR && PAIRED) {
+      const int r = w0 + m;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        addr[h] = tile0 + static_cast<uint32_t>(r * 128 + (((4 * h + g) ^ (r & 7)) << 4));
+    } else if constexpr (KMAJOR) {
+      addr[0] = addr[1] = tile0 + static_cast<uint32_t>(kmaj_off(w0 + m, g));
     } else {
       const int col = w0 + 4 * (m & 3);
       const int c = col >> 3;
@@ -297,7 +360,10 @@ struct FragReader {
   }
   template <int SLOT>
   __device__ __forceinline__ void read_op(int o, u32x4 (&r)[kFrag]) const {
-    if constexpr (KMAJOR) {
+    if constexpr (KMAJOR && PAIRED) {
+      r[o] = *(const lds_u32x4*)(static_cast<uintptr_t>(addr[SLOT & 1] +
+                                                        (o * 2048 + (SLOT >> 1) * 2 * kOpBytes)));
+    } else if constexpr (KMAJOR) {
       r[o] = *(const lds_u32x4*)(static_cast<uintptr_t>(addr[0] + (o * 1024 + SLOT * kOpBytes)));
     } else {
       const u32x2 w = __builtin_bit_cast(
@@ -409,11 +475,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
   const TileCoord tc = map_tile(g);
   const GemmProblem& pr = g.prob[tc.p];
 
-  Loader<T, AK> la;
-  Loader<T, BK> lb;
-  la.init(pr.a, g.lda, g.M, g.K, tc.m0, wave, lane);
-  lb.init(pr.b, g.ldb, g.N, g.K, tc.n0, wave, lane);
-
   f32x4 acc[kFrag][kFrag];
 #pragma unroll
   for (int i = 0; i < kFrag; ++i)
@@ -424,25 +485,20 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
   // The logits epilogue wants each lane to own consecutive columns of a row.
   constexpr bool kSwapAB = EPI == GemmEpilogue::Logits;
 
-  // Full stages (nkf of them) run through the ring; a partial last stage
-  // (K % SK != 0) is handled after the loop. Every iteration issues the same
-  // number of DMA transfers (past the last full stage, an in-bounds dummy
-  // copy of stage 0 into a slot nobody reads again), so one constant vmcnt
-  // wait always means "stage s+1 has landed".
-  const int nkf = static_cast<int>(g.K / SK);
+  const int nkf = static_cast<int>(g.K / SK);   // full stages
   u32x4 ra[2][kFrag], rb[2][kFrag];
-  auto issue_stage = [&](int slot_idx, int st) {
-    const int src = st < nkf ? st : 0;
-    la.issue(tileA(slot_idx), src, wave, lane);
-    lb.issue(tileB(slot_idx), src, wave, lane);
-  };
   auto read_stage = [&](int slot_idx, u32x4 (&rA)[kFrag], u32x4 (&rB)[kFrag]) {
 #pragma unroll
     for (int i = 0; i < kFrag; ++i) rA[i] = read_frag<T, AK>(tileA(slot_idx), wm * 128 + i * 16, lane);
 #pragma unroll
     for (int j = 0; j < kFrag; ++j) rB[j] = read_frag<T, BK>(tileB(slot_idx), wn * 128 + j * 16, lane);
   };
+  int st_done = 0;   // stages consumed by the main loop
   if constexpr (Elem<T>::kSize == 2) {
+    // Stage pairs (128-byte K-major rows) when both operands are K-major;
+    // single stages otherwise, where the transpose reads of an MN-major
+    // operand need the whole iteration.
+    constexpr bool kPaired = AK && BK;
     // LDS byte address of the ring and of this wave's 1 KB DMA block.
     // The base is hidden from the optimiser: otherwise it folds the B tiles'
     // 64 KB offset into the per-read constant, which then no longer fits the
@@ -451,109 +507,268 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)smem))));
     asm volatile("" : "+s"(lds0));
     const uint32_t m0wave = lds0 + static_cast<uint32_t>(wave) * 1024;
-    FragReader<AK> fa;
-    FragReader<BK> fb;
+    FragReader<AK, kPaired> fa;
+    FragReader<BK, kPaired> fb;
     fa.init(lds0, wm * 128, lane);
     fb.init(lds0 + kRing * kOpBytes, wn * 128, lane);
     __builtin_amdgcn_sched_barrier(0);
     mfma_prime();
     __builtin_amdgcn_sched_barrier(0);
-    if (nkf > 0) {
-#pragma unroll
-      for (int t = 0; t < kRing; ++t) issue_stage(t, t);
-      __builtin_amdgcn_s_waitcnt(kWaitThreeStages);
-      __builtin_amdgcn_s_barrier();
-      read_stage(0, ra[0], rb[0]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // Iteration s (stage s sits in slot s%4 and register set s%2):
-    // (1) wait until stage s+1 has landed (stages s+2, s+3 may still be in
-    // flight) and every wave has finished reading stage s out of its slot;
-    // (2) read stage s+1's fragments into the other register set; (3) DMA
-    // stage s+4 into stage s's slot; (4) 64 MFMAs on stage s.
-    //
-    // With one wave per SIMD nothing else fills the matrix pipe, so (2) and
-    // (3) ride between the MFMAs: the 64 MFMAs go out as 32 pairs and side
-    // operation o (the stage's LDS reads first, then its eight DMA
-    // transfers) issues with pair (o * 32) / kSide, while the MFMAs before
-    // it execute. The reads finish early enough that the next iteration's
-    // wait does not stall. An iteration whose stage s+1 does not exist reads
-    // a slot whose contents are never used.
-    constexpr int kOpsA = FragReader<AK>::kOps, kOpsB = FragReader<BK>::kOps;
-    constexpr int kReads = kOpsA + kOpsB;
-    constexpr int kSide = kReads + 2 * kXfers;
-    constexpr int kPairDma = (kReads * 32) / kSide;   // first pair carrying a DMA
-    auto iter = [&](auto slot_c, int st, u32x4 (&rnA)[kFrag], u32x4 (&rnB)[kFrag],
-                    const u32x4 (&rcA)[kFrag], const u32x4 (&rcB)[kFrag]) {
-      constexpr int S = decltype(slot_c)::value;       // slot of stage s
-      constexpr int SN = (S + 1) % kRing;              // slot of stage s+1
-      constexpr int MA = S * kOpBytes;                 // DMA targets, from m0wave
-      constexpr int MB = (kRing + S) * kOpBytes;
-      __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(kWaitTwoStages);
-      __builtin_amdgcn_s_barrier();
-      __builtin_amdgcn_sched_barrier(0);
-      uint64_t sa = 0, sb = 0;
-#pragma unroll
-      for (int pr = 0; pr < 32; ++pr) {
-        if (pr == kPairDma - 2) {
-          // DMA sources of stage s+4, computed here so the scalar work
-          // overlaps MFMAs instead of delaying the first one.
-          const int nxt = st + kRing < nkf ? st + kRing : 0;
-          sa = uniform64(la.stage_src(nxt));
-          sb = uniform64(lb.stage_src(nxt));
+    if constexpr (kPaired) {
+      // The ring holds two stage pairs (64 elements of K each): pair p sits in
+      // double slot p%2, stage s in half s%2 of double slot (s/2)%2.
+      //
+      // Iteration s computes stage s from registers and reads stage s+1's
+      // fragments into the other register set. An even iteration s reads
+      // first; at its middle barrier every wave has finished reading stages s
+      // and s+1 (the latter just now, with an LDS wait before the barrier),
+      // so their double slot is free and the DMA of pair s/2 + 2 into it
+      // follows. An odd iteration s starts by waiting for its own DMAs of pair
+      // (s+1)/2 (the newer pair stays in flight) and a barrier, after which
+      // every wave's share of that pair has landed. Each pair thus has 2.5
+      // iterations to land and up to two pairs are in flight. Past the last
+      // pair the DMA re-reads the last pair into a double slot nobody reads
+      // again, so the wait counts stay exact.
+      //
+      // With one wave per SIMD nothing else fills the matrix pipe, so the side
+      // operations ride between the MFMAs (64 per stage, issued as 32 pairs).
+      PairLoader<AK> pa;
+      PairLoader<BK> pb;
+      pa.init(pr.a, g.lda, g.M, tc.m0, wave, lane);
+      pb.init(pr.b, g.ldb, g.N, tc.n0, wave, lane);
+      const int np = nkf / 2;
+      // Transfer x (0-7 A, 8-15 B) of a pair's DMA into double slot D, from
+      // the pair's sources sa, sb.
+      auto dma_op = [&](auto d_c, int x, uint64_t sa, uint64_t sb) {
+        constexpr int MA = decltype(d_c)::value * 2 * kOpBytes;
+        constexpr int MB = MA + kRing * kOpBytes;
+        switch (x) {   // 0-7: A transfers, 8-15: B transfers
+          case 0: dma16_at<MA + 0 * 4096>(sa, pa.goff[0], m0wave); break;
+          case 1: dma16_at<MA + 1 * 4096>(sa, pa.goff[1], m0wave); break;
+          case 2: dma16_at<MA + 2 * 4096>(sa, pa.goff[2], m0wave); break;
+          case 3: dma16_at<MA + 3 * 4096>(sa, pa.goff[3], m0wave); break;
+          case 4: dma16_at<MA + 4 * 4096>(sa, pa.goff[4], m0wave); break;
+          case 5: dma16_at<MA + 5 * 4096>(sa, pa.goff[5], m0wave); break;
+          case 6: dma16_at<MA + 6 * 4096>(sa, pa.goff[6], m0wave); break;
+          case 7: dma16_at<MA + 7 * 4096>(sa, pa.goff[7], m0wave); break;
+          case 8: dma16_at<MB + 0 * 4096>(sb, pb.goff[0], m0wave); break;
+          case 9: dma16_at<MB + 1 * 4096>(sb, pb.goff[1], m0wave); break;
+          case 10: dma16_at<MB + 2 * 4096>(sb, pb.goff[2], m0wave); break;
+          case 11: dma16_at<MB + 3 * 4096>(sb, pb.goff[3], m0wave); break;
+          case 12: dma16_at<MB + 4 * 4096>(sb, pb.goff[4], m0wave); break;
+          case 13: dma16_at<MB + 5 * 4096>(sb, pb.goff[5], m0wave); break;
+          case 14: dma16_at<MB + 6 * 4096>(sb, pb.goff[6], m0wave); break;
+          default: dma16_at<MB + 7 * 4096>(sb, pb.goff[7], m0wave); break;
         }
-#pragma unroll
-        for (int o = 0; o < kSide; ++o) {
-          if ((o * 32) / kSide != pr) continue;
-          if (o < kOpsA) {
-            fa.template read_op<SN>(o, rnA);
-          } else if (o < kReads) {
-            fb.template read_op<SN>(o - kOpsA, rnB);
-          } else {
-            switch (o - kReads) {   // 0-3: A transfers, 4-7: B transfers
-              case 0: dma16_at<MA + 0 * 4096>(sa, la.goff[0], m0wave); break;
-              case 1: dma16_at<MA + 1 * 4096>(sa, la.goff[1], m0wave); break;
-              case 2: dma16_at<MA + 2 * 4096>(sa, la.goff[2], m0wave); break;
-              case 3: dma16_at<MA + 3 * 4096>(sa, la.goff[3], m0wave); break;
-              case 4: dma16_at<MB + 0 * 4096>(sb, lb.goff[0], m0wave); break;
-              case 5: dma16_at<MB + 1 * 4096>(sb, lb.goff[1], m0wave); break;
-              case 6: dma16_at<MB + 2 * 4096>(sb, lb.goff[2], m0wave); break;
-              default: dma16_at<MB + 3 * 4096>(sb, lb.goff[3], m0wave); break;
-            }
-          }
+      };
+      if (np > 0) {
+        {
+          const uint64_t sa = uniform64(pa.src(0)), sb = uniform64(pb.src(0));
+  #pragma unroll
+          for (int x = 0; x < 16; ++x) dma_op(SlotC<0>{}, x, sa, sb);
         }
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const int mm = 2 * pr + q;
-          if constexpr (kSwapAB)
-            mfma_bf16(acc[mm >> 3][mm & 7], rcB[mm & 7], rcA[mm >> 3]);
-          else
-            mfma_bf16(acc[mm >> 3][mm & 7], rcA[mm >> 3], rcB[mm & 7]);
+        if (np > 1) {
+          const uint64_t sa = uniform64(pa.src(1)), sb = uniform64(pb.src(1));
+  #pragma unroll
+          for (int x = 0; x < 16; ++x) dma_op(SlotC<1>{}, x, sa, sb);
+          __builtin_amdgcn_s_waitcnt(vm_wait(16));   // pair 0 landed
+        } else {
+          __builtin_amdgcn_s_waitcnt(kWaitAll);
         }
+        __builtin_amdgcn_s_barrier();
+  #pragma unroll
+        for (int o = 0; o < FragReader<AK, kPaired>::kOps; ++o) fa.template read_op<0>(o, ra[0]);
+  #pragma unroll
+        for (int o = 0; o < FragReader<BK, kPaired>::kOps; ++o) fb.template read_op<0>(o, rb[0]);
         __builtin_amdgcn_sched_barrier(0);
       }
-    };
-    // Unrolled by the ring depth so each slot is a compile-time immediate;
-    // the register sets alternate.
-    int s0 = 0;
-    for (; s0 + 3 < nkf; s0 += 4) {
-      iter(SlotC<0>{}, s0, ra[1], rb[1], ra[0], rb[0]);
-      iter(SlotC<1>{}, s0 + 1, ra[0], rb[0], ra[1], rb[1]);
-      iter(SlotC<2>{}, s0 + 2, ra[1], rb[1], ra[0], rb[0]);
-      iter(SlotC<3>{}, s0 + 3, ra[0], rb[0], ra[1], rb[1]);
+      constexpr int kOpsA = FragReader<AK, kPaired>::kOps, kOpsB = FragReader<BK, kPaired>::kOps;
+      constexpr int kReads = kOpsA + kOpsB;
+      constexpr int kMid = 16;   // MFMA pair of an even iteration's barrier
+      auto iter = [&](auto slot_c, int st, u32x4 (&rnA)[kFrag], u32x4 (&rnB)[kFrag],
+                      const u32x4 (&rcA)[kFrag], const u32x4 (&rcB)[kFrag]) {
+        constexpr int S = decltype(slot_c)::value;   // stage s % 4
+        constexpr int SN = (S + 1) % kRing;          // stage s+1 % 4
+        constexpr bool kOdd = (S & 1) != 0;
+        // LDS reads spread over the pairs before the barrier (even) or over
+        // the whole iteration (odd); an even iteration's DMAs follow its barrier.
+        constexpr int kReadPairs = kOdd ? 32 : kMid - 2;
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (kOdd) {
+          __builtin_amdgcn_s_waitcnt(vm_wait(16));   // pair (s+1)/2 landed
+          __builtin_amdgcn_s_barrier();
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        uint64_t sa = 0, sb = 0;
+  #pragma unroll
+        for (int pr = 0; pr < 32; ++pr) {
+          if (!kOdd && pr == kMid - 4) {
+            // DMA sources of pair s/2 + 2, computed here so the scalar work
+            // overlaps MFMAs.
+            const int p = (st >> 1) + 2;
+            const int nxt = p < np ? p : np - 1;
+            sa = uniform64(pa.src(nxt));
+            sb = uniform64(pb.src(nxt));
+          }
+          if (!kOdd && pr == kMid) {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(kWaitLds);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+          }
+  #pragma unroll
+          for (int o = 0; o < kReads; ++o) {
+            if ((o * kReadPairs) / kReads != pr) continue;
+            if (o < kOpsA)
+              fa.template read_op<SN>(o, rnA);
+            else
+              fb.template read_op<SN>(o - kOpsA, rnB);
+          }
+          if constexpr (!kOdd) {
+            if (pr >= kMid) dma_op(SlotC<(S >> 1)>{}, pr - kMid, sa, sb);
+          }
+  #pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const int mm = 2 * pr + q;
+            if constexpr (kSwapAB)
+              mfma_bf16(acc[mm >> 3][mm & 7], rcB[mm & 7], rcA[mm >> 3]);
+            else
+              mfma_bf16(acc[mm >> 3][mm & 7], rcA[mm >> 3], rcB[mm & 7]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      // Unrolled by the ring depth so each slot is a compile-time immediate;
+      // the register sets alternate. 2*np is even, so the remainder is 0 or 2.
+      const int ns = 2 * np;
+      int s0 = 0;
+      for (; s0 + 3 < ns; s0 += 4) {
+        iter(SlotC<0>{}, s0, ra[1], rb[1], ra[0], rb[0]);
+        iter(SlotC<1>{}, s0 + 1, ra[0], rb[0], ra[1], rb[1]);
+        iter(SlotC<2>{}, s0 + 2, ra[1], rb[1], ra[0], rb[0]);
+        iter(SlotC<3>{}, s0 + 3, ra[0], rb[0], ra[1], rb[1]);
+      }
+      if (s0 < ns) {
+        iter(SlotC<0>{}, s0, ra[1], rb[1], ra[0], rb[0]);
+        iter(SlotC<1>{}, s0 + 1, ra[0], rb[0], ra[1], rb[1]);
+      }
+      st_done = ns;
+    } else {
+      // Single stages: iteration s (stage s in slot s%4 and register set
+      // s%2) (1) waits until stage s+1 has landed (stages s+2, s+3 may still
+      // be in flight) and every wave has finished reading stage s out of its
+      // slot; (2) reads stage s+1's fragments into the other register set;
+      // (3) DMAs stage s+4 into stage s's slot; (4) runs the 64 MFMAs of
+      // stage s, with side operation o (the stage's LDS reads first, then
+      // its eight DMA transfers) issued with MFMA pair (o * 32) / kSide.
+      // Every iteration issues the same number of DMA transfers (past the
+      // last full stage, an in-bounds dummy copy of stage 0 into a slot
+      // nobody reads again), so one constant vmcnt wait always means "stage
+      // s+1 has landed". An iteration whose stage s+1 does not exist reads a
+      // slot whose contents are never used.
+      Loader<T, AK> la;
+      Loader<T, BK> lb;
+      la.init(pr.a, g.lda, g.M, g.K, tc.m0, wave, lane);
+      lb.init(pr.b, g.ldb, g.N, g.K, tc.n0, wave, lane);
+      if (nkf > 0) {
+#pragma unroll
+        for (int t = 0; t < kRing; ++t) {
+          const int src = t < nkf ? t : 0;
+          la.issue(tileA(t), src, wave, lane);
+          lb.issue(tileB(t), src, wave, lane);
+        }
+        __builtin_amdgcn_s_waitcnt(kWaitThreeStages);
+        __builtin_amdgcn_s_barrier();
+        read_stage(0, ra[0], rb[0]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      constexpr int kOpsA = FragReader<AK, kPaired>::kOps, kOpsB = FragReader<BK, kPaired>::kOps;
+      constexpr int kReads = kOpsA + kOpsB;
+      constexpr int kSide = kReads + 2 * kXfers;
+      constexpr int kPairDma = (kReads * 32) / kSide;   // first pair carrying a DMA
+      auto iter = [&](auto slot_c, int st, u32x4 (&rnA)[kFrag], u32x4 (&rnB)[kFrag],
+                      const u32x4 (&rcA)[kFrag], const u32x4 (&rcB)[kFrag]) {
+        constexpr int S = decltype(slot_c)::value;       // slot of stage s
+        constexpr int SN = (S + 1) % kRing;              // slot of stage s+1
+        constexpr int MA = S * kOpBytes;                 // DMA targets, from m0wave
+        constexpr int MB = (kRing + S) * kOpBytes;
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(kWaitTwoStages);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        uint64_t sa = 0, sb = 0;
+#pragma unroll
+        for (int pr = 0; pr < 32; ++pr) {
+          if (pr == kPairDma - 2) {
+            // DMA sources of stage s+4, computed here so the scalar work
+            // overlaps MFMAs instead of delaying the first one.
+            const int nxt = st + kRing < nkf ? st + kRing : 0;
+            sa = uniform64(la.stage_src(nxt));
+            sb = uniform64(lb.stage_src(nxt));
+          }
+#pragma unroll
+          for (int o = 0; o < kSide; ++o) {
+            if ((o * 32) / kSide != pr) continue;
+            if (o < kOpsA) {
+              fa.template read_op<SN>(o, rnA);
+            } else if (o < kReads) {
+              fb.template read_op<SN>(o - kOpsA, rnB);
+            } else {
+              switch (o - kReads) {   // 0-3: A transfers, 4-7: B transfers
+                case 0: dma16_at<MA + 0 * 4096>(sa, la.goff[0], m0wave); break;
+                case 1: dma16_at<MA + 1 * 4096>(sa, la.goff[1], m0wave); break;
+                case 2: dma16_at<MA + 2 * 4096>(sa, la.goff[2], m0wave); break;
+                case 3: dma16_at<MA + 3 * 4096>(sa, la.goff[3], m0wave); break;
+                case 4: dma16_at<MB + 0 * 4096>(sb, lb.goff[0], m0wave); break;
+                case 5: dma16_at<MB + 1 * 4096>(sb, lb.goff[1], m0wave); break;
+                case 6: dma16_at<MB + 2 * 4096>(sb, lb.goff[2], m0wave); break;
+                default: dma16_at<MB + 3 * 4096>(sb, lb.goff[3], m0wave); break;
+              }
+            }
+          }
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const int mm = 2 * pr + q;
+            if constexpr (kSwapAB)
+              mfma_bf16(acc[mm >> 3][mm & 7], rcB[mm & 7], rcA[mm >> 3]);
+            else
+              mfma_bf16(acc[mm >> 3][mm & 7], rcA[mm >> 3], rcB[mm & 7]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      int s0 = 0;
+      for (; s0 + 3 < nkf; s0 += 4) {
+        iter(SlotC<0>{}, s0, ra[1], rb[1], ra[0], rb[0]);
+        iter(SlotC<1>{}, s0 + 1, ra[0], rb[0], ra[1], rb[1]);
+        iter(SlotC<2>{}, s0 + 2, ra[1], rb[1], ra[0], rb[0]);
+        iter(SlotC<3>{}, s0 + 3, ra[0], rb[0], ra[1], rb[1]);
+      }
+      const int rem = nkf - s0;
+      if (rem >= 1) iter(SlotC<0>{}, s0, ra[1], rb[1], ra[0], rb[0]);
+      if (rem >= 2) iter(SlotC<1>{}, s0 + 1, ra[0], rb[0], ra[1], rb[1]);
+      if (rem >= 3) iter(SlotC<2>{}, s0 + 2, ra[1], rb[1], ra[0], rb[0]);
+      st_done = nkf;
     }
-    const int rem = nkf - s0;
-    if (rem >= 1) iter(SlotC<0>{}, s0, ra[1], rb[1], ra[0], rb[0]);
-    if (rem >= 2) iter(SlotC<1>{}, s0 + 1, ra[0], rb[0], ra[1], rb[1]);
-    if (rem >= 3) iter(SlotC<2>{}, s0 + 2, ra[1], rb[1], ra[0], rb[0]);
     __builtin_amdgcn_sched_barrier(0);
     mfma_drain();
     __builtin_amdgcn_sched_barrier(0);
   } else {
     // fp32: an MFMA stage is long (256 v_mfma_f32_16x16x4_f32), so one
     // register set suffices: DMA three stages ahead into the slot read one
-    // stage ago, read this stage after the barrier, then compute.
+    // stage ago, read this stage after the barrier, then compute. Every
+    // iteration issues the same number of DMA transfers (past the last full
+    // stage, an in-bounds dummy copy of stage 0 into a slot nobody reads
+    // again), so one constant vmcnt wait always means "stage s has landed".
+    Loader<T, AK> la;
+    Loader<T, BK> lb;
+    la.init(pr.a, g.lda, g.M, g.K, tc.m0, wave, lane);
+    lb.init(pr.b, g.ldb, g.N, g.K, tc.n0, wave, lane);
+    auto issue_stage = [&](int slot_idx, int st) {
+      const int src = st < nkf ? st : 0;
+      la.issue(tileA(slot_idx), src, wave, lane);
+      lb.issue(tileB(slot_idx), src, wave, lane);
+    };
     if (nkf > 0)
       for (int t = 0; t < kRing - 1; ++t) issue_stage(t, t);
     for (int st = 0; st < nkf; ++st) {
@@ -566,23 +781,33 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       __builtin_amdgcn_sched_barrier(0);
       mfma_step<T, kSwapAB>(acc, ra[0], rb[0]);
     }
+    st_done = nkf;
   }
-  if (nkf * SK < g.K) {
-    // Partial last stage: DMA the valid part, zero the rest, then one step.
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(kWaitAll);
-    __builtin_amdgcn_s_barrier();
-    la.issue(tileA(0), nkf, wave, lane);
-    lb.issue(tileB(0), nkf, wave, lane);
-    __builtin_amdgcn_s_waitcnt(kWaitAll);
-    __builtin_amdgcn_s_barrier();
-    read_stage(0, ra[1], rb[1]);
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(kWaitAll);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma_step<T, kSwapAB>(acc, ra[1], rb[1]);
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (Elem<T>::kSize == 2) mfma_drain();
+  if (static_cast<int64_t>(st_done) * SK < g.K) {
+    // Stages the main loop left — after the bf16 pairs an odd full stage,
+    // and a partial last stage — one at a time through slot 0 in the
+    // single-stage layout: DMA the valid part, zero the rest.
+    Loader<T, AK> la;
+    Loader<T, BK> lb;
+    la.init(pr.a, g.lda, g.M, g.K, tc.m0, wave, lane);
+    lb.init(pr.b, g.ldb, g.N, g.K, tc.n0, wave, lane);
+    auto tail_stage = [&](int st) {
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(kWaitAll);
+      __builtin_amdgcn_s_barrier();
+      la.issue(tileA(0), st, wave, lane);
+      lb.issue(tileB(0), st, wave, lane);
+      __builtin_amdgcn_s_waitcnt(kWaitAll);
+      __builtin_amdgcn_s_barrier();
+      read_stage(0, ra[1], rb[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(kWaitAll);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_step<T, kSwapAB>(acc, ra[1], rb[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (Elem<T>::kSize == 2) mfma_drain();
+    };
+    for (int st = st_done; static_cast<int64_t>(st) * SK < g.K; ++st) tail_stage(st);
   }
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_waitcnt(kWaitAll);

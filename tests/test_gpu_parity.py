@@ -230,6 +230,21 @@ def test_tied_reduced_bf16_int8(torch_dev):
     check_grad("grad_weight (dequantized)", gw, rw, "bf16")
 
 
+@pytest.mark.parametrize("bt,h,v,chunk", [(300, 224, 1000, 200), (96, 112, 1064, 48)])
+def test_tied_bf16_k_tails(torch_dev, bt, h, v, chunk):
+    """bf16 GEMMs whose K (H for the logits, V for grad_hidden, chunk rows
+    for grad_W) is a whole number of 64-element stage pairs followed by an
+    odd 32-element stage and a ragged rest, with teacher CE so that every
+    product runs on both halves."""
+    s, th = normal((bt, h), 61), normal((bt, h), 62)
+    w = normal((v, h), 63, 0.03)
+    y = uniform_labels(bt, v, 65)
+    opts = LossOptions(kd_weight=0.4, temperature=1.5, label_smoothing=0.1,
+                       teacher_ce_weight=0.5, chunk_size=ChunkSize.Fixed(chunk))
+    got, ref = run_pair(torch_dev, s, w, y, Teacher.Tied(th), opts, dtype="bf16")
+    check_output(got, ref, kind="bf16")
+
+
 def test_ignored_labels_and_reductions(torch_dev):
     bt, h, v = 200, 64, 777
     s, th = normal((bt, h), 51), normal((bt, h), 52)
