@@ -394,6 +394,18 @@ __device__ __forceinline__ void mfma_bf16(f32x4& acc, const u32x4& a, const u32x
 // Wait states between the last MFMA and the first read of its result, and
 // between an accumulator write by a VALU and the first MFMA reading it.
 __device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"); }
+// Copy of an accumulator into VGPRs at this point of the program. Without
+// it the compiler moves every accumulator into VGPRs at the start of the
+// logits epilogue, which then no longer fits the register file.
+__device__ __forceinline__ f32x4 from_acc(const f32x4& a) {
+  float x, y, z, w;
+  asm volatile(
+      "v_accvgpr_read_b32 %0, %4\n\tv_accvgpr_read_b32 %1, %5\n\t"
+      "v_accvgpr_read_b32 %2, %6\n\tv_accvgpr_read_b32 %3, %7"
+      : "=v"(x), "=v"(y), "=v"(z), "=v"(w)
+      : "a"(a[0]), "a"(a[1]), "a"(a[2]), "a"(a[3]));
+  return f32x4{x, y, z, w};
+}
 __device__ __forceinline__ void mfma_prime() { asm volatile("s_nop 7"); }
 
 // One stage of MFMAs: acc[i][j] += A-fragment i x B-fragment j. With SWAP the
@@ -863,6 +875,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       constexpr bool kFull = decltype(full_c)::value;
 #pragma unroll
       for (int i = 0; i < kFrag; ++i) {
+        f32x4 av[kFrag];
+#pragma unroll
+        for (int j = 0; j < kFrag; ++j) av[j] = from_acc(acc[i][j]);
         const int rl = wm * 128 + i * 16 + lrow;           // row within tile
         const int64_t row = tc.m0 + rl;
         const int64_t yl64 = lab[rl] - colw;
@@ -872,7 +887,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         for (int j = 0; j < kFrag; ++j)
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (kFull || j * 16 + e < ncol) mx = fmaxf(mx, acc[i][j][e]);
+            if (kFull || j * 16 + e < ncol) mx = fmaxf(mx, av[j][e]);
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         float d1 = 0.f, dT = 0.f, sx = 0.f;
@@ -880,7 +895,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         for (int j = 0; j < kFrag; ++j) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float x = acc[i][j][e];
+            const float x = av[j][e];
             const float dx = x - mx;
             const float a1 = __builtin_amdgcn_exp2f(dx * kLog2e);
             const float aT = __builtin_amdgcn_exp2f(dx * it2);
@@ -898,10 +913,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         float xy = 0.f;
 #pragma unroll
         for (int j = 0; j < kFrag; ++j) {
-          float t = acc[i][j][0];
-          t = ey == 1 ? acc[i][j][1] : t;
-          t = ey == 2 ? acc[i][j][2] : t;
-          t = ey == 3 ? acc[i][j][3] : t;
+          float t = av[j][0];
+          t = ey == 1 ? av[j][1] : t;
+          t = ey == 2 ? av[j][2] : t;
+          t = ey == 3 ? av[j][3] : t;
           xy = jy == j ? t : xy;
         }
         d1 += __shfl_xor(d1, 16);
@@ -916,7 +931,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
           LT* crow = C + row * g.ldc + colw;
 #pragma unroll
           for (int j = 0; j < kFrag; ++j) {
-            const f32x4 v = acc[i][j];
+            const f32x4 v = av[j];
             if (kFull || j * 16 + 4 <= ncol) {
               if constexpr (Elem<LT>::kSize == 2) {
                 u32x2 w;
