@@ -357,6 +357,35 @@ char* at(const void* base, int64_t elems, DType t) {
   return static_cast<char*>(const_cast<void*>(base)) + elems * orda::dtype_size(t);
 }
 
+// Tied teacher with bf16 inputs: the logits GEMM runs over student and
+// teacher rows interleaved in blocks of 16, so that it forms the KL cross
+// term Σ p_t^T·(x_t − x_s) from its fp32 accumulators.
+bool paired_rows(const LossPlan& P, const Inputs& in) {
+  return P.need_teacher && P.mode == ORDA_TEACHER_TIED && in.th.ld == in.hs.ld &&
+         P.dt == orda::DType::BF16;
+}
+
+// Logits storage: bf16 for bf16 inputs wherever only the gradient reads the
+// stored logits (every loss term comes from the GEMM's fp32 statistics);
+// fp32 when the row pass must form the KL cross term from them.
+orda::DType logits_dtype(const LossPlan& P, bool paired) {
+  return P.dt == orda::DType::BF16 && (paired || P.kd <= 0.f) ? orda::DType::BF16
+                                                             : orda::DType::F32;
+}
+
+// Device bytes the loss stages per chunk row.
+int64_t staged_bytes_per_row(const LossPlan& P, const Inputs& in) {
+  const bool paired = paired_rows(P, in);
+  const orda::DType lt = logits_dtype(P, paired);
+  const int64_t blocks = P.need_teacher ? 2 : 1;
+  const int64_t nst = orda::gemm_stat_tiles(P.v);
+  int64_t b = blocks * logits_pitch(P.v) *
+              (orda::dtype_size(lt) + (lt == P.dt ? 0 : orda::dtype_size(P.dt)));
+  b += 2 * nst * 16 + 2 * 4;   // statistics, label logits
+  if (paired) b += nst * 4 + 2 * round8(P.h) * 2;   // cross partials, paired hidden rows
+  return b;
+}
+
 void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan plan, int64_t G,
               float* row3_out, float* scal_dev) {
   using namespace orda;
@@ -370,13 +399,15 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   const int blocks = P.need_teacher ? 2 : 1;
   const bool tied_tce = P.mode == ORDA_TEACHER_TIED && P.w_t > 0.f;
 
-  // Logits are kept in fp32 so that the loss terms (statistics, label logits,
-  // the KL cross term) use the same values as the reference. The gradient
-  // rows the backward GEMMs read are in the input dtype: in place for f32
-  // inputs, a separate bf16 buffer for bf16 inputs.
-  const DType lt = DType::F32;
-  void* L = ws(c, "logits", blocks * cap * ldl * 4);
-  void* Gb = dt == DType::F32 ? L : ws(c, "dlogits", blocks * cap * ldl * es);
+  // Every loss term comes from fp32 values: the GEMM's tile statistics and
+  // label logits, and the KL cross term either from the paired GEMM or from
+  // fp32 logits read back by the row pass (lt = F32). The gradient rows the
+  // backward GEMMs read are in the input dtype: in place when lt == dt,
+  // else a separate bf16 buffer.
+  const bool paired = paired_rows(P, in);
+  const DType lt = logits_dtype(P, paired);
+  void* L = ws(c, "logits", blocks * cap * ldl * dtype_size(lt));
+  void* Gb = dt == lt ? L : ws(c, "dlogits", blocks * cap * ldl * es);
   // Statistics and label logits of a whole group: student rows, then teacher
   // rows (the logits GEMM of problem p writes row p*M + r).
   float4* stats = static_cast<float4*>(ws(c, "stats", 2 * cap * nst * 16));
@@ -387,6 +418,9 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   float* rkl = row3_out + 2 * bt;
   const int64_t ldh_cat = round8(h);
   void* hcat = tied_tce ? ws(c, "hcat", 2 * cap * ldh_cat * es) : nullptr;
+  const int64_t cap16 = (cap + 15) / 16 * 16;
+  void* hpair = paired ? ws(c, "hpair", 2 * cap16 * ldh_cat * es) : nullptr;
+  float* cross = paired ? static_cast<float*>(ws(c, "cross", cap * nst * 4)) : nullptr;
   const float inv_t = 1.0f / P.T;
 
   for (int64_t g0 = 0; g0 < nc; g0 += G) {
@@ -430,7 +464,20 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
     f.nprob = 1;
     f.prob[0] = {at(in.hs.p, gs * in.hs.ld, dt), in.W.p, Ls};
     const bool fuse_t = P.need_teacher && P.mode == ORDA_TEACHER_TIED && in.th.ld == in.hs.ld;
-    if (fuse_t) {
+    if (paired) {
+      // One problem over the interleaved rows; C rows, statistics and label
+      // logits come out in the usual order (student rows, then teacher rows).
+      timed(c, ORDA_KERNEL_OTHER, [&] {
+        return launch_interleave_rows(hpair, ldh_cat, at(in.hs.p, gs * in.hs.ld, dt),
+                                      at(in.th.p, gs * in.th.ld, dt), in.hs.ld, btg, round8(h),
+                                      c->stream);
+      });
+      f.M = 2 * ((btg + 15) / 16 * 16);
+      f.lda = ldh_cat;
+      f.prob[0] = {hpair, in.W.p, L};
+      f.lg.pair_rows = btg;
+      f.lg.cross = cross;
+    } else if (fuse_t) {
       f.nprob = 2;
       f.prob[1] = {at(in.th.p, gs * in.th.ld, dt), in.W.p, Lt};
     }
@@ -487,6 +534,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       r.stats_tiles_t = P.mode == ORDA_TEACHER_PRECOMPUTED ? 1 : nst;
       r.xy_s = xy;
       r.xy_t = xy + btg;
+      r.cross = cross;
       r.labels = in.labels + gs;
       r.ignore_index = P.ignore;
       r.w_s = P.w_s;
@@ -739,10 +787,7 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
   // ---- chunk plan, staging group, OOM retry (resolver.rs:103-126)
   orda::ChunkPlan plan = plan0;
   const int64_t limit = o->config.has_max_chunks ? o->config.max_chunks : default_max_chunks_limit(bt);
-  const int64_t chunk_bytes =
-      plan.chunk_size * ((P.need_teacher ? 2 : 1) * logits_pitch(v) *
-                             (4 + (P.dt == DType::F32 ? 0 : dtype_size(P.dt))) +
-                         2 * gemm_stat_tiles(v) * 16);
+  const int64_t chunk_bytes = plan.chunk_size * staged_bytes_per_row(P, in);
   int64_t G = std::max<int64_t>(1, std::min<int64_t>(plan.num_chunks, c->staging_budget / std::max<int64_t>(chunk_bytes, 1)));
   for (;;) {
     try {
@@ -757,6 +802,8 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
       ws_release(c, "stats");
       ws_release(c, "xy");
       ws_release(c, "dlogits");
+      ws_release(c, "hpair");
+      ws_release(c, "cross");
       if (G > 1) {
         G /= 2;
         continue;

@@ -34,8 +34,11 @@
 // The Logits epilogue fuses the statistics the row pass needs: for every row
 // and every 256-column tile it writes {max, Σe^(x-max), Σe^((x-max)/T), Σx}
 // from the fp32 accumulators, plus the fp32 logit at the row's label, so the
-// row pass reads each logit exactly once. bf16 logits are staged through LDS
-// and leave as 16-byte row-contiguous stores.
+// row pass reads each logit exactly once. With paired rows (student and
+// teacher rows interleaved in blocks of 16) it also writes the tile's KL
+// cross term Σ e^((t-max_t)/T)·(t - s), so that every loss term comes from
+// fp32 accumulators and the stored logits (then bf16) only feed the
+// gradient. Each lane stores its 4 consecutive columns directly.
 #include <float.h>
 #include <math.h>
 
@@ -857,18 +860,82 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
     // transposed blocks (kSwapAB): acc[i][j][e] is row wm*128 + 16i + lrow,
     // column wn*128 + 16j + 4*lgrp + e, so a lane owns 8 rows x 32 columns
     // and each row's 128 columns of this wave sit in the 4 lanes lrow + 16g.
+    // With paired rows (pair_rows > 0) fragments 2q and 2q+1 hold a block of
+    // student rows and the same teacher rows, so a lane also holds both
+    // logits of every (row, column) it owns and forms the KL cross term.
     LT* C = static_cast<LT*>(pr.c);
     int64_t* lab = reinterpret_cast<int64_t*>(epi);                      // [256]
     float4* part = reinterpret_cast<float4*>(epi + 2048);                // [2][256]
+    float* xpart = reinterpret_cast<float*>(epi + 10240);                // [2][256]
+    const int64_t prs = g.lg.pair_rows;
+    // Tile row rl as (output row, teacher?, valid): stats / xy / C row index.
+    auto out_row = [&](int rl, bool& teacher, bool& valid) -> int64_t {
+      if (prs > 0) {
+        const int64_t R = static_cast<int64_t>(tc.m0) + rl;
+        const int64_t r = ((R >> 5) << 4) + (R & 15);
+        teacher = ((R >> 4) & 1) != 0;
+        valid = r < prs;
+        return teacher ? prs + r : r;
+      }
+      teacher = false;
+      valid = tc.m0 + rl < g.M;
+      return static_cast<int64_t>(tc.p) * g.M + tc.m0 + rl;
+    };
     {
-      const int64_t row = tc.m0 + tid;
-      lab[tid] = row < g.M ? g.lg.labels[row] : g.lg.ignore_index;
+      bool t, ok;
+      const int64_t o = out_row(tid, t, ok);
+      const int64_t r = prs > 0 ? (t ? o - prs : o) : tc.m0 + tid;
+      lab[tid] = ok ? g.lg.labels[r] : g.lg.ignore_index;
     }
     __syncthreads();
     const float it2 = g.lg.inv_t * kLog2e;
     const int64_t colw = static_cast<int64_t>(tc.n0) + wn * 128 + 4 * lgrp;   // (j, e) = (0, 0)
     const int64_t ncol64 = g.N - colw;                    // (j, e) valid iff 16j + e < ncol
     const int ncol = static_cast<int>(ncol64 < 128 ? (ncol64 < 0 ? 0 : ncol64) : 128);
+    // This lane's 32 logits of one row, from column colw on.
+    auto store_row = [&](auto full_c, LT* crow, const f32x4 (&v)[kFrag]) {
+      constexpr bool kFull = decltype(full_c)::value;
+#pragma unroll
+      for (int j = 0; j < kFrag; ++j) {
+        if (kFull || j * 16 + 4 <= ncol) {
+          if constexpr (Elem<LT>::kSize == 2) {
+            u32x2 w;
+            w[0] = pack_bf16(v[j][0], v[j][1]);
+            w[1] = pack_bf16(v[j][2], v[j][3]);
+            *reinterpret_cast<u32x2*>(crow + j * 16) = w;
+          } else {
+            *reinterpret_cast<f32x4*>(crow + j * 16) = v[j];
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (j * 16 + e < ncol) crow[j * 16 + e] = static_cast<LT>(v[j][e]);
+        }
+      }
+    };
+    // The label's logit, if this lane holds its column (16j + e == yl):
+    // select e, then j.
+    auto pick = [&](const f32x4 (&v)[kFrag], int yl) {
+      const int jy = yl >> 4, ey = yl & 3;
+      float xy = 0.f;
+#pragma unroll
+      for (int j = 0; j < kFrag; ++j) {
+        float t = v[j][0];
+        t = ey == 1 ? v[j][1] : t;
+        t = ey == 2 ? v[j][2] : t;
+        t = ey == 3 ? v[j][3] : t;
+        xy = jy == j ? t : xy;
+      }
+      return xy;
+    };
+    auto quad_max = [](float x) {
+      x = fmaxf(x, __shfl_xor(x, 16));
+      return fmaxf(x, __shfl_xor(x, 32));
+    };
+    auto quad_sum = [](float x) {
+      x += __shfl_xor(x, 16);
+      return x + __shfl_xor(x, 32);
+    };
     // Full tiles (all but the last column tile when N % 256 != 0) take a
     // path without per-column checks.
     auto rows = [&](auto full_c) {
@@ -888,8 +955,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
             if (kFull || j * 16 + e < ncol) mx = fmaxf(mx, av[j][e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = quad_max(mx);
         float d1 = 0.f, dT = 0.f, sx = 0.f;
 #pragma unroll
         for (int j = 0; j < kFrag; ++j) {
@@ -906,63 +972,108 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
             }
           }
         }
-        // The label's logit, if this lane holds its column (16j + e == yl):
-        // select e, then j.
         const bool hit = yl >= 0 && (yl & 12) == 0;
-        const int jy = yl >> 4, ey = yl & 3;
-        float xy = 0.f;
-#pragma unroll
-        for (int j = 0; j < kFrag; ++j) {
-          float t = av[j][0];
-          t = ey == 1 ? av[j][1] : t;
-          t = ey == 2 ? av[j][2] : t;
-          t = ey == 3 ? av[j][3] : t;
-          xy = jy == j ? t : xy;
-        }
-        d1 += __shfl_xor(d1, 16);
-        dT += __shfl_xor(dT, 16);
-        sx += __shfl_xor(sx, 16);
-        d1 += __shfl_xor(d1, 32);
-        dT += __shfl_xor(dT, 32);
-        sx += __shfl_xor(sx, 32);
+        const float xy = pick(av, yl);
+        d1 = quad_sum(d1);
+        dT = quad_sum(dT);
+        sx = quad_sum(sx);
         if (lgrp == 0) part[wn * 256 + rl] = make_float4(mx, d1, dT, sx);
         if (row < g.M) {
           if (hit) g.lg.xy[tc.p * g.M + row] = xy;
-          LT* crow = C + row * g.ldc + colw;
-#pragma unroll
-          for (int j = 0; j < kFrag; ++j) {
-            const f32x4 v = av[j];
-            if (kFull || j * 16 + 4 <= ncol) {
-              if constexpr (Elem<LT>::kSize == 2) {
-                u32x2 w;
-                w[0] = pack_bf16(v[0], v[1]);
-                w[1] = pack_bf16(v[2], v[3]);
-                *reinterpret_cast<u32x2*>(crow + j * 16) = w;
-              } else {
-                *reinterpret_cast<f32x4*>(crow + j * 16) = v;
-              }
-            } else {
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                if (j * 16 + e < ncol) crow[j * 16 + e] = static_cast<LT>(v[e]);
-            }
-          }
+          store_row(full_c, C + row * g.ldc + colw, av);
         }
       }
     };
-    if (tc.n0 + kTile <= g.N)
-      rows(SlotC<1>{});
-    else
-      rows(SlotC<0>{});
+    auto rows_pair = [&](auto full_c) {
+      constexpr bool kFull = decltype(full_c)::value;
+#pragma unroll
+      for (int q = 0; q < kFrag / 2; ++q) {
+        f32x4 as[kFrag], at[kFrag];
+#pragma unroll
+        for (int j = 0; j < kFrag; ++j) as[j] = from_acc(acc[2 * q][j]);
+#pragma unroll
+        for (int j = 0; j < kFrag; ++j) at[j] = from_acc(acc[2 * q + 1][j]);
+        const int rs = wm * 128 + q * 32 + lrow;                         // tile rows
+        const int rt = rs + 16;
+        const int64_t row = (tc.m0 >> 1) + wm * 64 + q * 16 + lrow;      // student row
+        const int64_t yl64 = lab[rs] - colw;
+        const int yl = (yl64 >= 0 && yl64 < 128) ? static_cast<int>(yl64) : -1;
+        float ms = -INFINITY, mt = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < kFrag; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (kFull || j * 16 + e < ncol) {
+              ms = fmaxf(ms, as[j][e]);
+              mt = fmaxf(mt, at[j][e]);
+            }
+        ms = quad_max(ms);
+        mt = quad_max(mt);
+        float d1s = 0.f, dTs = 0.f, sxs = 0.f, d1t = 0.f, dTt = 0.f, sxt = 0.f, cx = 0.f;
+#pragma unroll
+        for (int j = 0; j < kFrag; ++j) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float xs = as[j][e], xt = at[j][e];
+            const float dxs = xs - ms, dxt = xt - mt;
+            const float a1s = __builtin_amdgcn_exp2f(dxs * kLog2e);
+            const float aTs = __builtin_amdgcn_exp2f(dxs * it2);
+            const float a1t = __builtin_amdgcn_exp2f(dxt * kLog2e);
+            const float aTt = __builtin_amdgcn_exp2f(dxt * it2);
+            if (kFull || j * 16 + e < ncol) {
+              d1s += a1s;
+              dTs += aTs;
+              sxs += xs;
+              d1t += a1t;
+              dTt += aTt;
+              sxt += xt;
+              cx = fmaf(aTt, xt - xs, cx);
+            }
+          }
+        }
+        const bool hit = yl >= 0 && (yl & 12) == 0;
+        const float xys = pick(as, yl), xyt = pick(at, yl);
+        d1s = quad_sum(d1s);
+        dTs = quad_sum(dTs);
+        sxs = quad_sum(sxs);
+        d1t = quad_sum(d1t);
+        dTt = quad_sum(dTt);
+        sxt = quad_sum(sxt);
+        cx = quad_sum(cx);
+        if (lgrp == 0) {
+          part[wn * 256 + rs] = make_float4(ms, d1s, dTs, sxs);
+          part[wn * 256 + rt] = make_float4(mt, d1t, dTt, sxt);
+          xpart[wn * 256 + rt] = cx;
+        }
+        if (row < prs) {
+          if (hit) {
+            g.lg.xy[row] = xys;
+            g.lg.xy[prs + row] = xyt;
+          }
+          store_row(full_c, C + row * g.ldc + colw, as);
+          store_row(full_c, C + (prs + row) * g.ldc + colw, at);
+        }
+      }
+    };
+    const bool full = tc.n0 + kTile <= g.N;
+    if (prs > 0) {
+      if (full) rows_pair(SlotC<1>{});
+      else rows_pair(SlotC<0>{});
+    } else {
+      if (full) rows(SlotC<1>{});
+      else rows(SlotC<0>{});
+    }
     __syncthreads();
     {
-      const int64_t row = tc.m0 + tid;
-      if (row < g.M) {
+      bool teacher, ok;
+      const int64_t orow = out_row(tid, teacher, ok);
+      if (ok) {
         const float4 a = part[tid], b = part[256 + tid];
         const float m = fmaxf(a.x, b.x);
         float4 s;
         s.x = m;
         s.w = a.w + b.w;
+        float cx = 0.f;
         if (m == -INFINITY) {
           s.y = 0.f;
           s.z = 0.f;
@@ -973,12 +1084,15 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
           const float fb = __builtin_amdgcn_exp2f((b.x - m) * it2);
           s.y = a.y * ea + b.y * eb;
           s.z = a.z * fa + b.z * fb;
+          cx = xpart[tid] * fa + xpart[256 + tid] * fb;
         }
-        g.lg.stats[(static_cast<int64_t>(tc.p) * g.M + row) * g.lg.stats_ld + tc.ntile] = s;
+        g.lg.stats[orow * g.lg.stats_ld + tc.ntile] = s;
+        if (teacher) g.lg.cross[(orow - prs) * g.lg.stats_ld + tc.ntile] = cx;
       }
     }
   }
 }
+
 
 // One named entry point per variant, so that profiles and the build's ISA
 // check can tell them apart: gemm_<A layout><B layout>_<epilogue>_<input>
@@ -1030,6 +1144,9 @@ int64_t gemm_stat_tiles(int64_t n) { return (n + kTile - 1) / kTile; }
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
   if (g.nprob < 1 || g.nprob > 2) return hipErrorInvalidValue;
   if ((g.lda % 8) || (g.ldb % 8) || (g.ldc % 8 && g.epi == GemmEpilogue::Logits))
+    return hipErrorInvalidValue;
+  if (g.epi == GemmEpilogue::Logits && g.lg.pair_rows > 0 &&
+      (g.nprob != 1 || g.lg.cross == nullptr || g.M != 2 * ((g.lg.pair_rows + 15) / 16 * 16)))
     return hipErrorInvalidValue;
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
   const GemmKernel k = select_kernel(g);

@@ -10,7 +10,9 @@
 //   teacher grad = w_t·((p_t − α/V) − [j=y](1−α))   (api.rs:325-333)
 // overwriting both rows in place, and accumulates Σ p_t^T·(x_t − x_s) so that
 //   KL_row = Σ p_t^T (x_t − x_s)/T + (lse_s^T − lse_t^T)·Σ p_t^T
-// comes out of the same pass. The per-row NLL uses the fp32 label logit and
+// comes out of the same pass — unless a paired logits GEMM already formed
+// that sum per tile from its fp32 accumulators (the logits are then stored
+// in bf16 and only feed the gradient). The per-row NLL uses the fp32 label logit and
 // Σx from the GEMM epilogue and is formed in f64 like the reference.
 // Exponentials are exp2 with log2(e) folded into one FMA per element.
 #include <math.h>
@@ -345,6 +347,17 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
   const Stat ss = load_row_stats(a.stats_s + r * a.stats_ld, a.stats_tiles, it2, sstat);
   Stat st{-INFINITY, 0.f, 0.f, 0.f};
   if (HT || a.teacher_ce) st = load_row_stats(a.stats_t + r * a.stats_ld, a.stats_tiles_t, it2, sstat);
+  // KL cross term from a paired logits GEMM: Σ_tiles e^((m_tile - M_t)/T)·x_tile
+  // = Σ_j e^((t_j - M_t)/T)·(t_j - s_j), formed from the fp32 accumulators.
+  float xc = 0.f;
+  if (KL && a.cross != nullptr) {
+    const float4* srow_t = a.stats_t + r * a.stats_ld;
+    const float* crow = a.cross + r * a.stats_ld;
+    float part = 0.f;
+    for (int64_t t = tid; t < a.stats_tiles_t; t += kThreads)
+      part = fmaf(crow[t], __builtin_amdgcn_exp2f((srow_t[t].x - st.m) * it2), part);
+    xc = block_sum(part, ssum);
+  }
 
   const double alpha = static_cast<double>(a.label_smoothing);
   const float lse1_s = ss.m + logf(ss.d1);
@@ -459,7 +472,10 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
   if (tid == 0) {
     a.row_nll_s[r] = static_cast<float>(row_nll(ss, a.xy_s[r], alpha, v));
     float kl_row = 0.f;
-    if (KL) kl_row = ((cross / gsc) * inv_t + (lseT_s - lseT_t) * (sum_c / gsc)) * (T * T);
+    if (KL && a.cross != nullptr)
+      kl_row = ((xc / st.dT) * inv_t + (lseT_s - lseT_t)) * (T * T);
+    else if (KL)
+      kl_row = ((cross / gsc) * inv_t + (lseT_s - lseT_t) * (sum_c / gsc)) * (T * T);
     a.row_kl[r] = kl_row;
     a.row_nll_t[r] = a.teacher_ce ? static_cast<float>(row_nll(st, a.xy_t[r], alpha, v)) : 0.f;
   }
@@ -538,7 +554,32 @@ __global__ void zero_pad_kernel(T* base, int64_t ld, int64_t n_rows, int64_t v) 
     base[(i / w) * ld + v + i % w] = static_cast<T>(0.f);
 }
 
+// Paired-row staging (launch_interleave_rows); pitches and columns in
+// 16-byte chunks, one workgroup row per destination row.
+__global__ void interleave_rows_kernel(u32x4* dst, int64_t ldd, const u32x4* s0, const u32x4* s1,
+                                       int64_t lds, int64_t n_rows, int64_t chunks) {
+  const int64_t R = blockIdx.y;
+  const int64_t r = ((R >> 5) << 4) + (R & 15);
+  const u32x4* src = ((R >> 4) & 1) ? s1 : s0;
+  for (int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; c < chunks;
+       c += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    dst[R * ldd + c] = r < n_rows ? src[r * lds + c] : u32x4{0u, 0u, 0u, 0u};
+}
+
 }  // namespace
+
+hipError_t launch_interleave_rows(void* dst, int64_t ldd, const void* s0, const void* s1,
+                                  int64_t lds, int64_t n_rows, int64_t cols, hipStream_t s) {
+  if (n_rows <= 0) return hipSuccess;
+  if ((ldd % 8) || (lds % 8) || (cols % 8)) return hipErrorInvalidValue;
+  const int64_t rows = 2 * ((n_rows + 15) / 16 * 16);
+  const int64_t chunks = cols / 8;
+  dim3 grid(static_cast<unsigned>((chunks + 255) / 256), static_cast<unsigned>(rows));
+  hipLaunchKernelGGL(interleave_rows_kernel, grid, dim3(256), 0, s, static_cast<u32x4*>(dst),
+                     ldd / 8, static_cast<const u32x4*>(s0), static_cast<const u32x4*>(s1), lds / 8,
+                     n_rows, chunks);
+  return hipGetLastError();
+}
 
 hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
   if (a.n_rows <= 0) return hipSuccess;
