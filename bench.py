@@ -105,10 +105,13 @@ def work_per_step(wl, plan):
         dgrad = 2 * bt * v * h
         wgrad = dgrad
         t_rows_written = 0
-    # row pass: read student + teacher logits once (kept in fp32), write the
-    # gradient rows in the input dtype
-    rows_read = 2 * bt
-    rowpass = rows_read * v * 4 + (bt + t_rows_written) * v * es
+    # row pass: read the student and teacher logits once, write the gradient
+    # rows in the input dtype. Logits are stored in bf16 for bf16 inputs when
+    # every loss term comes from the GEMM's fp32 accumulators (tied teacher,
+    # or no KL term), else in fp32.
+    rows_read = 2 * bt if (kd > 0 or wt > 0) else bt
+    ls = 2 if dt == "bf16" and (teacher == "tied" or kd == 0) else 4
+    rowpass = rows_read * v * ls + (bt + t_rows_written) * v * es
     quant_b = v * h * 8 if quant else 0
     return {"gemm_logits": ("mfma", fwd), "gemm_grad_hidden": ("mfma", dgrad),
             "gemm_grad_weight": ("mfma", wgrad), "row_pass": ("hbm", rowpass),
@@ -166,12 +169,13 @@ KERNEL_CLASSES = (
     ("gemm_km_", "gemm_grad_hidden"),
     ("gemm_mm_", "gemm_grad_weight"),
     ("gemm_kk_", "gemm_nt"),
-    ("row_pass_kernel", "row_pass"),
+    ("row_pass_", "row_pass"),            # row_pass_fused_kernel, row_pass_kernel
     ("row_stats_kernel", "row_stats"),
     ("finalize_kernel", "finalize"),
-    ("quant_kernel", "quant"),
+    ("quant_", "quant"),                  # quant_vec_kernel, quant_kernel
     ("mark_targets", "mark_targets"),
     ("convert_rows", "convert_rows"),
+    ("interleave_rows", "interleave_rows"),
     ("zero_pad", "zero_pad"),
 )
 COPY_KERNEL = "copyBuffer"          # HIP runtime's device-to-device copy kernel
