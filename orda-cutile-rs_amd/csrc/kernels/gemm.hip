@@ -511,9 +511,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
   int st_done = 0;   // stages consumed by the main loop
   if constexpr (Elem<T>::kSize == 2) {
     // Stage pairs (128-byte K-major rows) when both operands are K-major;
-    // single stages otherwise, where the transpose reads of an MN-major
-    // operand need the whole iteration.
+    // when only A is, A moves in pairs inside the single-stage loop (the
+    // transpose reads of an MN-major operand need the whole iteration);
+    // single stages when neither is.
     constexpr bool kPaired = AK && BK;
+    constexpr bool kHybrid = AK && !BK;
     // LDS byte address of the ring and of this wave's 1 KB DMA block.
     // The base is hidden from the optimiser: otherwise it folds the B tiles'
     // 64 KB offset into the per-read constant, which then no longer fits the
@@ -522,7 +524,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)smem))));
     asm volatile("" : "+s"(lds0));
     const uint32_t m0wave = lds0 + static_cast<uint32_t>(wave) * 1024;
-    FragReader<AK, kPaired> fa;
+    FragReader<AK, AK> fa;
     FragReader<BK, kPaired> fb;
     fa.init(lds0, wm * 128, lane);
     fb.init(lds0 + kRing * kOpBytes, wn * 128, lane);
@@ -592,12 +594,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         }
         __builtin_amdgcn_s_barrier();
   #pragma unroll
-        for (int o = 0; o < FragReader<AK, kPaired>::kOps; ++o) fa.template read_op<0>(o, ra[0]);
+        for (int o = 0; o < FragReader<AK, AK>::kOps; ++o) fa.template read_op<0>(o, ra[0]);
   #pragma unroll
         for (int o = 0; o < FragReader<BK, kPaired>::kOps; ++o) fb.template read_op<0>(o, rb[0]);
         __builtin_amdgcn_sched_barrier(0);
       }
-      constexpr int kOpsA = FragReader<AK, kPaired>::kOps, kOpsB = FragReader<BK, kPaired>::kOps;
+      constexpr int kOpsA = FragReader<AK, AK>::kOps, kOpsB = FragReader<BK, kPaired>::kOps;
       constexpr int kReads = kOpsA + kOpsB;
       constexpr int kMid = 16;   // MFMA pair of an even iteration's barrier
       auto iter = [&](auto slot_c, int st, u32x4 (&rnA)[kFrag], u32x4 (&rnB)[kFrag],
@@ -668,6 +670,140 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         iter(SlotC<1>{}, s0 + 1, ra[0], rb[0], ra[1], rb[1]);
       }
       st_done = ns;
+    } else if constexpr (kHybrid) {
+      // K-major A in stage pairs, MN-major B in single stages, in the
+      // single-stage loop: one barrier at the top of every iteration, B's
+      // transpose reads spread over the whole iteration. Iteration s DMAs B
+      // stage s+4 into B slot s%4 and, when s = 2p+1 is odd, A pair p+2 into
+      // A's double slot p%2, whose stages 2p and 2p+1 were read in
+      // iterations 2p-1 and 2p. An iteration's transfers go out as B's 4,
+      // then A's 8, so at the top of iteration s the newest transfers that
+      // must have landed (B stage s+1, and the A pair holding stage s+1) are
+      // followed by exactly 16 (s even) or 4 (s odd) younger ones. Past the
+      // last pair the DMAs re-read stage 0 (B) or the last pair (A) into
+      // slots nobody reads again.
+      const int np = nkf / 2;
+      const int ns = 2 * np;
+      PairLoader<AK> pa;
+      pa.init(pr.a, g.lda, g.M, tc.m0, wave, lane);
+      Loader<T, BK> lb;
+      lb.init(pr.b, g.ldb, g.N, g.K, tc.n0, wave, lane);
+      // Transfer x (0-7) of an A pair into double slot D.
+      auto dma_a = [&](auto d_c, int x, uint64_t sa) {
+        constexpr int MA = decltype(d_c)::value * 2 * kOpBytes;
+        switch (x) {
+          case 0: dma16_at<MA + 0 * 4096>(sa, pa.goff[0], m0wave); break;
+          case 1: dma16_at<MA + 1 * 4096>(sa, pa.goff[1], m0wave); break;
+          case 2: dma16_at<MA + 2 * 4096>(sa, pa.goff[2], m0wave); break;
+          case 3: dma16_at<MA + 3 * 4096>(sa, pa.goff[3], m0wave); break;
+          case 4: dma16_at<MA + 4 * 4096>(sa, pa.goff[4], m0wave); break;
+          case 5: dma16_at<MA + 5 * 4096>(sa, pa.goff[5], m0wave); break;
+          case 6: dma16_at<MA + 6 * 4096>(sa, pa.goff[6], m0wave); break;
+          default: dma16_at<MA + 7 * 4096>(sa, pa.goff[7], m0wave); break;
+        }
+      };
+      // Transfer x (0-3) of a B stage into B slot S.
+      auto dma_b = [&](auto s_c, int x, uint64_t sb) {
+        constexpr int MB = (kRing + decltype(s_c)::value) * kOpBytes;
+        switch (x) {
+          case 0: dma16_at<MB + 0 * 4096>(sb, lb.goff[0], m0wave); break;
+          case 1: dma16_at<MB + 1 * 4096>(sb, lb.goff[1], m0wave); break;
+          case 2: dma16_at<MB + 2 * 4096>(sb, lb.goff[2], m0wave); break;
+          default: dma16_at<MB + 3 * 4096>(sb, lb.goff[3], m0wave); break;
+        }
+      };
+      if (np > 0) {
+        // A pair 0, B stages 0-3, A pair 1; then stage 0 is followed by 20
+        // younger transfers.
+        uint64_t sa = uniform64(pa.src(0));
+#pragma unroll
+        for (int x = 0; x < 8; ++x) dma_a(SlotC<0>{}, x, sa);
+        uint64_t sb = uniform64(lb.stage_src(0));
+#pragma unroll
+        for (int x = 0; x < 4; ++x) dma_b(SlotC<0>{}, x, sb);
+        sb = uniform64(lb.stage_src(1 < ns ? 1 : 0));
+#pragma unroll
+        for (int x = 0; x < 4; ++x) dma_b(SlotC<1>{}, x, sb);
+        sb = uniform64(lb.stage_src(2 < ns ? 2 : 0));
+#pragma unroll
+        for (int x = 0; x < 4; ++x) dma_b(SlotC<2>{}, x, sb);
+        sb = uniform64(lb.stage_src(3 < ns ? 3 : 0));
+#pragma unroll
+        for (int x = 0; x < 4; ++x) dma_b(SlotC<3>{}, x, sb);
+        sa = uniform64(pa.src(np > 1 ? 1 : 0));
+#pragma unroll
+        for (int x = 0; x < 8; ++x) dma_a(SlotC<1>{}, x, sa);
+        __builtin_amdgcn_s_waitcnt(vm_wait(20));
+        __builtin_amdgcn_s_barrier();
+#pragma unroll
+        for (int o = 0; o < FragReader<AK, AK>::kOps; ++o) fa.template read_op<0>(o, ra[0]);
+#pragma unroll
+        for (int o = 0; o < FragReader<BK, kPaired>::kOps; ++o) fb.template read_op<0>(o, rb[0]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      constexpr int kOpsA = FragReader<AK, AK>::kOps, kOpsB = FragReader<BK, kPaired>::kOps;
+      constexpr int kReads = kOpsA + kOpsB;
+      auto iter = [&](auto slot_c, int st, u32x4 (&rnA)[kFrag], u32x4 (&rnB)[kFrag],
+                      const u32x4 (&rcA)[kFrag], const u32x4 (&rcB)[kFrag]) {
+        constexpr int S = decltype(slot_c)::value;   // stage s % 4
+        constexpr int SN = (S + 1) % kRing;          // stage s+1 % 4
+        constexpr bool kOdd = (S & 1) != 0;
+        constexpr int kDma = kOdd ? 12 : 4;
+        constexpr int kSide = kReads + kDma;
+        constexpr int kPairDma = (kReads * 32) / kSide;   // first MFMA pair carrying a DMA
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(kOdd ? vm_wait(4) : vm_wait(16));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        uint64_t sa = 0, sb = 0;
+#pragma unroll
+        for (int pr = 0; pr < 32; ++pr) {
+          if (pr == kPairDma - 2) {
+            // DMA sources (B stage s+4, A pair s/2 + 2), computed here so the
+            // scalar work overlaps MFMAs.
+            const int nb = st + kRing < ns ? st + kRing : 0;
+            sb = uniform64(lb.stage_src(nb));
+            if constexpr (kOdd) {
+              const int p = (st >> 1) + 2;
+              sa = uniform64(pa.src(p < np ? p : np - 1));
+            }
+          }
+#pragma unroll
+          for (int o = 0; o < kSide; ++o) {
+            if ((o * 32) / kSide != pr) continue;
+            if (o < kOpsA) {
+              fa.template read_op<SN>(o, rnA);
+            } else if (o < kReads) {
+              fb.template read_op<SN>(o - kOpsA, rnB);
+            } else if (o < kReads + 4) {
+              dma_b(SlotC<S>{}, o - kReads, sb);
+            } else {
+              dma_a(SlotC<(S >> 1)>{}, o - kReads - 4, sa);
+            }
+          }
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const int mm = 2 * pr + q;
+            if constexpr (kSwapAB)
+              mfma_bf16(acc[mm >> 3][mm & 7], rcB[mm & 7], rcA[mm >> 3]);
+            else
+              mfma_bf16(acc[mm >> 3][mm & 7], rcA[mm >> 3], rcB[mm & 7]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      int s0 = 0;
+      for (; s0 + 3 < ns; s0 += 4) {
+        iter(SlotC<0>{}, s0, ra[1], rb[1], ra[0], rb[0]);
+        iter(SlotC<1>{}, s0 + 1, ra[0], rb[0], ra[1], rb[1]);
+        iter(SlotC<2>{}, s0 + 2, ra[1], rb[1], ra[0], rb[0]);
+        iter(SlotC<3>{}, s0 + 3, ra[0], rb[0], ra[1], rb[1]);
+      }
+      if (s0 < ns) {
+        iter(SlotC<0>{}, s0, ra[1], rb[1], ra[0], rb[0]);
+        iter(SlotC<1>{}, s0 + 1, ra[0], rb[0], ra[1], rb[1]);
+      }
+      st_done = ns;
     } else {
       // Single stages: iteration s (stage s in slot s%4 and register set
       // s%2) (1) waits until stage s+1 has landed (stages s+2, s+3 may still
@@ -697,7 +833,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         read_stage(0, ra[0], rb[0]);
         __builtin_amdgcn_sched_barrier(0);
       }
-      constexpr int kOpsA = FragReader<AK, kPaired>::kOps, kOpsB = FragReader<BK, kPaired>::kOps;
+      constexpr int kOpsA = FragReader<AK, AK>::kOps, kOpsB = FragReader<BK, kPaired>::kOps;
       constexpr int kReads = kOpsA + kOpsB;
       constexpr int kSide = kReads + 2 * kXfers;
       constexpr int kPairDma = (kReads * 32) / kSide;   // first pair carrying a DMA
