@@ -1,0 +1,69 @@
+"""The float64 torch-autograd restatement (tests/torch_reference.py) against
+the CPU oracle, on the reference's LCG inputs (tests/end_to_end.rs:14-36):
+loss, components and every gradient of all teacher modes. This pins the torch
+restatement that the GPU autograd-op tests compare with.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import labels, mat
+from orda_hip.types import LossOptions, Reduction, Teacher
+from torch_reference import loss_f64
+
+CASES = {
+    # name: (mode, bt, h, ht, v, options, ignore_every)
+    "tied_tce_smooth_mean": ("tied", 9, 6, 6, 11,
+                             dict(kd_weight=0.5, temperature=1.5, teacher_ce_weight=1.0,
+                                  label_smoothing=0.1), 4),
+    "tied_default_weight": ("tied", 7, 5, 5, 13, dict(kd_weight=0.4, temperature=2.0), None),
+    "tied_pure_student": ("tied", 6, 4, 4, 9, dict(teacher_ce_weight=0.0), 3),
+    "separate_tce_sum": ("separate", 8, 5, 7, 10,
+                         dict(kd_weight=0.5, temperature=2.0, teacher_ce_weight=1.0,
+                              reduction=Reduction.Sum), None),
+    "separate_default_weight": ("separate", 6, 4, 6, 9,
+                                dict(kd_weight=0.5, temperature=2.0, label_smoothing=0.1), 5),
+    "precomputed": ("precomputed", 7, 5, 5, 12, dict(kd_weight=0.7, temperature=1.0), 3),
+}
+
+
+def run_case(name):
+    mode, bt, h, ht, v, o, every = CASES[name]
+    s = mat(bt, h, 1, 0.5)
+    w = mat(v, h, 2, 0.4)
+    y = labels(bt, v, every)
+    th = tw = tl = None
+    if mode == "tied":
+        th = mat(bt, h, 3, 0.5)
+        teacher = Teacher.Tied(th)
+    elif mode == "separate":
+        th = mat(bt, ht, 3, 0.5)
+        tw = mat(v, ht, 4, 0.4)
+        teacher = Teacher.Separate(th, tw)
+    else:
+        tl = mat(bt, v, 5, 2.0)
+        teacher = Teacher.Precomputed(tl)
+    opts = LossOptions(**o)
+    ref = O.distillation_loss(s, w, y, teacher, opts)
+    tr = loss_f64(s, w, y, mode, th, tw, tl, w_s=opts.student_ce_weight,
+                  w_t=opts.teacher_ce_weight, kd=opts.kd_weight, T=opts.temperature,
+                  alpha=opts.label_smoothing, ignore=opts.ignore_index,
+                  mean=opts.reduction == Reduction.Mean)
+    return ref, tr
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_torch_reference_matches_oracle(name):
+    ref, tr = run_case(name)
+    for k in ("loss", "student_ce", "teacher_ce", "kl"):
+        r = getattr(ref, k)
+        assert abs(tr[k] - r) <= 1e-5 * max(abs(r), 1e-2), f"{k}: torch {tr[k]!r} oracle {r!r}"
+    for k in ("grad_student_hidden", "grad_weight", "grad_teacher_hidden", "grad_teacher_weight"):
+        r = getattr(ref, k)
+        t = tr[k]
+        assert (r is None) == (t is None), f"{k}: presence differs"
+        if r is None:
+            continue
+        r = np.asarray(r, np.float64)
+        err = np.linalg.norm(t - r) / max(np.linalg.norm(r), 1e-30)
+        assert err <= 1e-5, f"{k}: rel fro err {err:.3e}"
