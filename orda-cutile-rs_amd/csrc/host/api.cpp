@@ -382,7 +382,7 @@ int64_t staged_bytes_per_row(const LossPlan& P, const Inputs& in) {
   int64_t b = blocks * logits_pitch(P.v) *
               (orda::dtype_size(lt) + (lt == P.dt ? 0 : orda::dtype_size(P.dt)));
   b += 2 * nst * 16 + 2 * 4;   // statistics, label logits
-  if (paired) b += nst * 4 + 2 * round8(P.h) * 2;   // cross partials, paired hidden rows
+  if (paired) b += nst * 4 + 2 * round8(P.h) * 2 + 16;   // cross partials, paired rows, row constants
   return b;
 }
 
@@ -421,6 +421,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   const int64_t cap16 = (cap + 15) / 16 * 16;
   void* hpair = paired ? ws(c, "hpair", 2 * cap16 * ldh_cat * es) : nullptr;
   float* cross = paired ? static_cast<float*>(ws(c, "cross", cap * nst * 4)) : nullptr;
+  float4* rconst = paired ? static_cast<float4*>(ws(c, "rconst", cap * 16)) : nullptr;
   const float inv_t = 1.0f / P.T;
 
   for (int64_t g0 = 0; g0 < nc; g0 += G) {
@@ -535,6 +536,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       r.xy_s = xy;
       r.xy_t = xy + btg;
       r.cross = cross;
+      r.row_consts = rconst;
       r.labels = in.labels + gs;
       r.ignore_index = P.ignore;
       r.w_s = P.w_s;
@@ -804,6 +806,7 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
       ws_release(c, "dlogits");
       ws_release(c, "hpair");
       ws_release(c, "cross");
+      ws_release(c, "rconst");
       if (G > 1) {
         G /= 2;
         continue;

@@ -99,6 +99,9 @@ struct RowPassArgs {
   // (LogitStatsArgs::cross, same pitch as the stats), or null: then the
   // pass accumulates the cross term from the logits it reads.
   const float* cross;
+  // Scratch of n_rows float4 for the chunked pass over paired bf16 logits
+  // (used when cross is set and the gradient goes in place); may be null.
+  float4* row_consts;
   // Gradient rows: written at grad_s/grad_t + r*ld in gtype. Null grad_s
   // means in place (gtype == ltype).
   void* grad_s;

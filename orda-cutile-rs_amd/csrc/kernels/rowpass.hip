@@ -481,6 +481,146 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
   }
 }
 
+// ------------------------------------------------- chunked row pass (paired)
+// With the KL cross term from a paired logits GEMM nothing in the row pass
+// needs a reduction over a row: every loss term comes from the GEMM's tile
+// statistics. The pass then splits into a per-row kernel that merges the
+// statistics, writes the row's losses and four exponent constants, and an
+// elementwise gradient kernel over (row, 8192-column chunk) blocks, so that
+// consecutive workgroups stream consecutive memory (the row-per-workgroup
+// kernel keeps ~2000 rows 256 KB apart open at once).
+//   consts[r] = {ca, cb, cc, cd}: log2|w_s| - lse1_s·log2e,
+//   log2(kd·T) - lseT_s·log2e, log2(kd·T) - lseT_t·log2e, log2(w_t) - lse1_t·log2e.
+template <bool KL, bool TG>
+__global__ __launch_bounds__(kThreads) void row_consts_kernel(RowPassArgs a) {
+  __shared__ Stat sstat[kThreads / 64];
+  __shared__ float ssum[kThreads / 64];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t y = a.labels[r];
+  if (y == a.ignore_index) {   // cross_entropy.rs:59, kl.rs:92
+    if (tid == 0) {
+      a.row_nll_s[r] = 0.f;
+      a.row_nll_t[r] = 0.f;
+      a.row_kl[r] = 0.f;
+      a.row_consts[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    return;
+  }
+  const float T = a.temperature;
+  const float inv_t = 1.0f / T;
+  const float it2 = inv_t * kLog2e;
+  const Stat ss = load_row_stats(a.stats_s + r * a.stats_ld, a.stats_tiles, it2, sstat);
+  Stat st{-INFINITY, 0.f, 0.f, 0.f};
+  if (KL || TG || a.teacher_ce)
+    st = load_row_stats(a.stats_t + r * a.stats_ld, a.stats_tiles_t, it2, sstat);
+  float xc = 0.f;
+  if (KL) {
+    const float4* srow_t = a.stats_t + r * a.stats_ld;
+    const float* crow = a.cross + r * a.stats_ld;
+    float part = 0.f;
+    for (int64_t t = tid; t < a.stats_tiles_t; t += kThreads)
+      part = fmaf(crow[t], __builtin_amdgcn_exp2f((srow_t[t].x - st.m) * it2), part);
+    xc = block_sum(part, ssum);
+  }
+  if (tid == 0) {
+    const double alpha = static_cast<double>(a.label_smoothing);
+    const float lse1_s = ss.m + logf(ss.d1);
+    const float lseT_s = ss.m * inv_t + logf(ss.dT);
+    const float lse1_t = st.m + logf(st.d1);
+    const float lseT_t = st.m * inv_t + logf(st.dT);
+    const float gsc = a.kd * T;                              // kl.rs:85
+    float4 k;
+    k.x = log2f(fabsf(a.w_s)) - lse1_s * kLog2e;
+    k.y = KL ? log2f(gsc) - lseT_s * kLog2e : 0.f;
+    k.z = KL ? log2f(gsc) - lseT_t * kLog2e : 0.f;
+    k.w = TG ? log2f(a.w_t) - lse1_t * kLog2e : 0.f;
+    a.row_consts[r] = k;
+    a.row_nll_s[r] = static_cast<float>(row_nll(ss, a.xy_s[r], alpha, a.v));
+    a.row_kl[r] = KL ? ((xc / st.dT) * inv_t + (lseT_s - lseT_t)) * (T * T) : 0.f;
+    a.row_nll_t[r] = a.teacher_ce ? static_cast<float>(row_nll(st, a.xy_t[r], alpha, a.v)) : 0.f;
+  }
+}
+
+// Gradient of one (row, chunk) block, in place in bf16 (the paired layout):
+// student g = w_s·((p_s − α/V) − [j=y](1−α)) + kd·T·(p_s^T − p_t^T),
+// teacher g = w_t·((p_t − α/V) − [j=y](1−α)) (when TG).
+constexpr int kChunkVec = 4;                             // 8-element vectors per thread
+constexpr int kChunk = kThreads * 8 * kChunkVec;         // columns per workgroup
+template <bool KL, bool TG>
+__global__ __launch_bounds__(kThreads) void row_grad_kernel(RowPassArgs a, int64_t chunks) {
+  constexpr int NV = 8;
+  const int64_t r = blockIdx.x / chunks;
+  const int64_t c0 = (blockIdx.x - r * chunks) * kChunk;
+  const int tid = threadIdx.x;
+  const int64_t y = a.labels[r];
+  const int64_t v = a.v;
+  __bf16* srow = static_cast<__bf16*>(a.student) + r * a.ld;
+  __bf16* trow = (KL || TG) ? static_cast<__bf16*>(a.teacher) + r * a.ld : nullptr;
+  if (y == a.ignore_index) {   // zero gradient rows
+    const float z[NV] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < kChunkVec; ++q) {
+      const int64_t j = c0 + (static_cast<int64_t>(q) * kThreads + tid) * NV;
+      if (j < v) {
+        store8(srow + j, z);
+        if (TG) store8(trow + j, z);
+      }
+    }
+    return;
+  }
+  const float4 k = a.row_consts[r];
+  const float it2 = kLog2e / a.temperature;
+  const float eps = static_cast<float>(static_cast<double>(a.label_smoothing) / static_cast<double>(v));
+  const float one_m_a = 1.0f - a.label_smoothing;
+  const float sgn = a.w_s < 0.f ? -1.f : 1.f;
+  const float k0 = -a.w_s * eps, kt0 = -a.w_t * eps;
+  auto elem = [&](float xs, float xt, float& g, float& gt) {
+    g = fmaf(sgn, __builtin_amdgcn_exp2f(fmaf(xs, kLog2e, k.x)), k0);
+    if (KL) g += __builtin_amdgcn_exp2f(fmaf(xs, it2, k.y)) - __builtin_amdgcn_exp2f(fmaf(xt, it2, k.z));
+    if (TG) gt = __builtin_amdgcn_exp2f(fmaf(xt, kLog2e, k.w)) + kt0;
+  };
+  // The label column's logits, read by the thread that writes that column.
+  const int64_t yl = y - c0;
+  const bool owner = yl >= 0 && yl < kChunk && tid == (yl / NV) % kThreads;
+  float xs_y = 0.f, xt_y = 0.f;
+  if (owner) {
+    xs_y = static_cast<float>(srow[y]);
+    if (KL || TG) xt_y = static_cast<float>(trow[y]);
+  }
+  float xs[kChunkVec][NV], xt[kChunkVec][NV];
+#pragma unroll
+  for (int q = 0; q < kChunkVec; ++q) {
+    const int64_t j = c0 + (static_cast<int64_t>(q) * kThreads + tid) * NV;
+    if (j < v) {
+      load8(srow + j, xs[q]);
+      if (KL || TG) load8(trow + j, xt[q]);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < kChunkVec; ++q) {
+    const int64_t j = c0 + (static_cast<int64_t>(q) * kThreads + tid) * NV;
+    if (j >= v) continue;
+    float g[NV], gt[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      float gi = 0.f, ti = 0.f;
+      elem(xs[q][i], (KL || TG) ? xt[q][i] : 0.f, gi, ti);
+      const bool valid = j + i < v;
+      g[i] = valid ? gi : 0.f;
+      gt[i] = valid ? ti : 0.f;
+    }
+    store8(srow + j, g);
+    if (TG) store8(trow + j, gt);
+  }
+  if (owner) {   // the label term, after this thread's own store of that column
+    float gy = 0.f, ty = 0.f;
+    elem(xs_y, xt_y, gy, ty);
+    srow[y] = static_cast<__bf16>(gy - a.w_s * one_m_a);
+    if (TG) trow[y] = static_cast<__bf16>(ty - a.w_t * one_m_a);
+  }
+}
+
 // ------------------------------------------------------------------ row stats
 template <typename ST, typename DT>
 __global__ __launch_bounds__(kThreads) void row_stats_kernel(RowStatsArgs a) {
@@ -598,6 +738,32 @@ hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
   if ((a.teacher_ce || kl || tg) && a.stats_t == nullptr) return hipErrorInvalidValue;
   const DType gt = a.grad_s ? a.gtype : a.ltype;
   if (a.grad_s && (tg && a.grad_t == nullptr)) return hipErrorInvalidValue;
+  if (a.cross != nullptr && a.row_consts != nullptr && a.ltype == DType::BF16 &&
+      a.grad_s == nullptr && (!(kl || tg || a.teacher_ce) || has_t)) {
+    // Paired layout, bf16 in place: per-row constants, then the chunked
+    // elementwise gradient.
+    const int64_t chunks = (a.v + kChunk - 1) / kChunk;
+    const int64_t blocks = a.n_rows * chunks;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    if (kl && tg) {
+      hipLaunchKernelGGL((row_consts_kernel<true, true>), grid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((row_grad_kernel<true, true>), dim3(static_cast<unsigned>(blocks)),
+                         dim3(kThreads), 0, s, a, chunks);
+    } else if (kl) {
+      hipLaunchKernelGGL((row_consts_kernel<true, false>), grid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((row_grad_kernel<true, false>), dim3(static_cast<unsigned>(blocks)),
+                         dim3(kThreads), 0, s, a, chunks);
+    } else if (tg) {
+      hipLaunchKernelGGL((row_consts_kernel<false, true>), grid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((row_grad_kernel<false, true>), dim3(static_cast<unsigned>(blocks)),
+                         dim3(kThreads), 0, s, a, chunks);
+    } else {
+      hipLaunchKernelGGL((row_consts_kernel<false, false>), grid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((row_grad_kernel<false, false>), dim3(static_cast<unsigned>(blocks)),
+                         dim3(kThreads), 0, s, a, chunks);
+    }
+    return hipGetLastError();
+  }
 #define ORDA_ROWPASS(LT, GT)                                                                          \
   if (kl && tg) hipLaunchKernelGGL((row_pass_fused_kernel<LT, GT, true, true>), grid, dim3(kThreads), 0, s, a);   \
   else if (kl) hipLaunchKernelGGL((row_pass_fused_kernel<LT, GT, true, false>), grid, dim3(kThreads), 0, s, a);  \
