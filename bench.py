@@ -170,8 +170,8 @@ KERNEL_CLASSES = (
     ("gemm_mm_", "gemm_grad_weight"),
     ("gemm_kk_", "gemm_nt"),
     ("row_pass_", "row_pass"),            # row_pass_fused_kernel, row_pass_kernel
-    ("row_consts_", "row_pass"),          # the chunked row pass: per-row constants ...
-    ("row_grad_", "row_pass"),            # ... and the elementwise gradient
+    ("row_consts_", "row_consts"),        # the chunked row pass: per-row constants ...
+    ("row_grad_", "row_grad"),            # ... and the elementwise gradient
     ("row_stats_kernel", "row_stats"),
     ("finalize_kernel", "finalize"),
     ("quant_", "quant"),                  # quant_vec_kernel, quant_kernel
