@@ -386,6 +386,19 @@ int64_t staged_bytes_per_row(const LossPlan& P, const Inputs& in) {
   return b;
 }
 
+// The split-K workspace a backward GEMM asks for, if any (one buffer shared
+// by the GEMMs of a call: they run in order on one stream).
+void attach_split_ws(orda_ctx* c, orda::GemmArgs& g) {
+  const int64_t b = orda::gemm_split_bytes(g);
+  if (b <= 0) return;
+  const orda_ctx::Buf& cur = c->bufs["splitk"];
+  // Growing the buffer frees the old one, which launches already queued on
+  // the stream may still use.
+  if (cur.p && cur.bytes < b) hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  g.split_ws = static_cast<float*>(ws(c, "splitk", b));
+  g.split_ws_bytes = b;
+}
+
 void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan plan, int64_t G,
               float* row3_out, float* scal_dev) {
   using namespace orda;
@@ -576,6 +589,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
         d.nprob = 2;
         d.prob[1] = {Gt, in.W.p, in.ght.p + gs * in.ght.ld};
       }
+      attach_split_ws(c, d);
       timed(c, ORDA_KERNEL_GEMM_GRAD_HIDDEN, [&] { return launch_gemm(d, c->stream); });
       if (P.has_ght && !fuse) {
         GemmArgs t = d;
@@ -585,6 +599,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
         t.ldb = sep ? in.tw.ld : in.W.ld;
         t.ldc = in.ght.ld;
         t.prob[0] = {Gt, sep ? in.tw.p : in.W.p, in.ght.p + gs * in.ght.ld};
+        attach_split_ws(c, t);
         timed(c, ORDA_KERNEL_GEMM_GRAD_HIDDEN, [&] { return launch_gemm(t, c->stream); });
       }
     }
@@ -620,6 +635,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
         w.ldb = in.hs.ld;
         w.prob[0] = {Gs, at(in.hs.p, gs * in.hs.ld, dt), in.gw.p};
       }
+      attach_split_ws(c, w);
       timed(c, ORDA_KERNEL_GEMM_GRAD_WEIGHT, [&] { return launch_gemm(w, c->stream); });
       if (P.has_gwt) {
         GemmArgs t = w;
@@ -628,6 +644,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
         t.ldb = in.th.ld;
         t.ldc = in.gwt.ld;
         t.prob[0] = {Gt, at(in.th.p, gs * in.th.ld, dt), in.gwt.p};
+        attach_split_ws(c, t);
         timed(c, ORDA_KERNEL_GEMM_GRAD_WEIGHT, [&] { return launch_gemm(t, c->stream); });
       }
     }
@@ -807,6 +824,7 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
       ws_release(c, "hpair");
       ws_release(c, "cross");
       ws_release(c, "rconst");
+      ws_release(c, "splitk");
       if (G > 1) {
         G /= 2;
         continue;

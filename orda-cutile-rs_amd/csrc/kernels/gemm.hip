@@ -442,12 +442,11 @@ struct TileCoord {
   int p, m0, n0, ntile;
 };
 
-__device__ __forceinline__ TileCoord map_tile(const GemmArgs& g) {
+__device__ __forceinline__ TileCoord map_tile(const GemmArgs& g, int64_t t) {
   const int64_t Mt = (g.M + kTile - 1) / kTile;
   const int64_t Nt = (g.N + kTile - 1) / kTile;
   const int64_t Mv = Mt * g.nprob;
   const int64_t T = Mv * Nt;
-  int64_t t = blockIdx.x;
   // Consecutive workgroups land on consecutive XCDs; give each XCD a
   // contiguous range of the raster so tiles sharing operands share an L2.
   const int64_t per = T / 8;
@@ -487,8 +486,25 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: M0 of the DMA
   const int wm = wave >> 1, wn = wave & 1;
-  const TileCoord tc = map_tile(g);
-  const GemmProblem& pr = g.prob[tc.p];
+  // Split K: workgroup s*T + t computes tile t over K range
+  // [s*split_len, (s+1)*split_len) into split s's partial buffer.
+  const int64_t tiles = ((g.M + kTile - 1) / kTile) * ((g.N + kTile - 1) / kTile) * g.nprob;
+  int64_t lin = blockIdx.x, kbeg = 0, Kl = g.K;
+  int split = 0;
+  if (g.split_k > 1) {
+    split = static_cast<int>(lin / tiles);
+    lin -= static_cast<int64_t>(split) * tiles;
+    kbeg = static_cast<int64_t>(split) * g.split_len;
+    Kl = g.K - kbeg < g.split_len ? g.K - kbeg : g.split_len;
+  }
+  const TileCoord tc = map_tile(g, lin);
+  GemmProblem pr = g.prob[tc.p];
+  if (g.split_k > 1) {
+    constexpr int ES = Elem<T>::kSize;
+    pr.a = static_cast<const unsigned char*>(pr.a) + kbeg * (AK ? 1 : g.lda) * ES;
+    pr.b = static_cast<const unsigned char*>(pr.b) + kbeg * (BK ? 1 : g.ldb) * ES;
+    pr.c = static_cast<float*>(pr.c) + static_cast<int64_t>(split) * g.split_stride;
+  }
 
   f32x4 acc[kFrag][kFrag];
 #pragma unroll
@@ -500,7 +516,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
   // The logits epilogue wants each lane to own consecutive columns of a row.
   constexpr bool kSwapAB = EPI == GemmEpilogue::Logits;
 
-  const int nkf = static_cast<int>(g.K / SK);   // full stages
+  const int nkf = static_cast<int>(Kl / SK);   // full stages
   u32x4 ra[2][kFrag], rb[2][kFrag];
   auto read_stage = [&](int slot_idx, u32x4 (&rA)[kFrag], u32x4 (&rB)[kFrag]) {
 #pragma unroll
@@ -687,7 +703,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       PairLoader<AK> pa;
       pa.init(pr.a, g.lda, g.M, tc.m0, wave, lane);
       Loader<T, BK> lb;
-      lb.init(pr.b, g.ldb, g.N, g.K, tc.n0, wave, lane);
+      lb.init(pr.b, g.ldb, g.N, Kl, tc.n0, wave, lane);
       // Transfer x (0-7) of an A pair into double slot D.
       auto dma_a = [&](auto d_c, int x, uint64_t sa) {
         constexpr int MA = decltype(d_c)::value * 2 * kOpBytes;
@@ -819,8 +835,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       // slot whose contents are never used.
       Loader<T, AK> la;
       Loader<T, BK> lb;
-      la.init(pr.a, g.lda, g.M, g.K, tc.m0, wave, lane);
-      lb.init(pr.b, g.ldb, g.N, g.K, tc.n0, wave, lane);
+      la.init(pr.a, g.lda, g.M, Kl, tc.m0, wave, lane);
+      lb.init(pr.b, g.ldb, g.N, Kl, tc.n0, wave, lane);
       if (nkf > 0) {
 #pragma unroll
         for (int t = 0; t < kRing; ++t) {
@@ -913,8 +929,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
     // again), so one constant vmcnt wait always means "stage s has landed".
     Loader<T, AK> la;
     Loader<T, BK> lb;
-    la.init(pr.a, g.lda, g.M, g.K, tc.m0, wave, lane);
-    lb.init(pr.b, g.ldb, g.N, g.K, tc.n0, wave, lane);
+    la.init(pr.a, g.lda, g.M, Kl, tc.m0, wave, lane);
+    lb.init(pr.b, g.ldb, g.N, Kl, tc.n0, wave, lane);
     auto issue_stage = [&](int slot_idx, int st) {
       const int src = st < nkf ? st : 0;
       la.issue(tileA(slot_idx), src, wave, lane);
@@ -934,14 +950,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
     }
     st_done = nkf;
   }
-  if (static_cast<int64_t>(st_done) * SK < g.K) {
+  if (static_cast<int64_t>(st_done) * SK < Kl) {
     // Stages the main loop left — after the bf16 pairs an odd full stage,
     // and a partial last stage — one at a time through slot 0 in the
     // single-stage layout: DMA the valid part, zero the rest.
     Loader<T, AK> la;
     Loader<T, BK> lb;
-    la.init(pr.a, g.lda, g.M, g.K, tc.m0, wave, lane);
-    lb.init(pr.b, g.ldb, g.N, g.K, tc.n0, wave, lane);
+    la.init(pr.a, g.lda, g.M, Kl, tc.m0, wave, lane);
+    lb.init(pr.b, g.ldb, g.N, Kl, tc.n0, wave, lane);
     auto tail_stage = [&](int st) {
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_waitcnt(kWaitAll);
@@ -958,7 +974,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (Elem<T>::kSize == 2) mfma_drain();
     };
-    for (int st = st_done; static_cast<int64_t>(st) * SK < g.K; ++st) tail_stage(st);
+    for (int st = st_done; static_cast<int64_t>(st) * SK < Kl; ++st) tail_stage(st);
   }
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_waitcnt(kWaitAll);
@@ -1273,9 +1289,65 @@ GemmKernel select_kernel(const GemmArgs& g) {
   return nullptr;
 }
 
+// Split-K reduction: C = alpha * (Σ_s partial_s) (+ alpha * C when
+// accumulating), the partials summed in split order.
+__global__ void splitk_reduce_kernel(const float* ws, int64_t stride, int splits, int64_t M,
+                                     int64_t N, int64_t ldp, float* c0, float* c1, int64_t ldc,
+                                     float alpha, bool accum) {
+  const int64_t per = M * N;
+  const int64_t total = per * (c1 ? 2 : 1);
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int p = i >= per ? 1 : 0;
+    const int64_t e = i - p * per;
+    const int64_t m = e / N, n = e - m * N;
+    const float* src = ws + p * M * ldp + m * ldp + n;
+    float v = 0.f;
+    for (int s = 0; s < splits; ++s) v += src[s * stride];
+    float* dst = (p ? c1 : c0) + m * ldc + n;
+    *dst = accum ? alpha * (*dst + v) : alpha * v;
+  }
+}
+
+struct SplitPlan {
+  int splits;
+  int64_t len, ldp, stride, bytes;
+};
+
+// Split K when the tiles cannot fill the CUs: about 256 workgroups in all,
+// each split at least 512 elements of K (a multiple of 64), at most 64
+// splits and 256 MB of partials.
+SplitPlan plan_split(const GemmArgs& g) {
+  SplitPlan sp{1, g.K, 0, 0, 0};
+  if (g.epi == GemmEpilogue::Logits || g.M <= 0 || g.N <= 0 || g.K <= 0) return sp;
+  const int64_t tiles = ((g.M + kTile - 1) / kTile) * ((g.N + kTile - 1) / kTile) * g.nprob;
+  if (tiles >= 192) return sp;
+  int64_t s = (256 + tiles - 1) / tiles;
+  const int64_t by_k = g.K / 512;
+  if (s > by_k) s = by_k;
+  if (s > 64) s = 64;
+  const int64_t per_split = g.nprob * g.M * ((g.N + 3) / 4 * 4) * 4;
+  if (s > (int64_t{256} << 20) / per_split) s = (int64_t{256} << 20) / per_split;
+  if (s <= 1) return sp;
+  const int64_t len = ((g.K + s - 1) / s + 63) / 64 * 64;
+  s = (g.K + len - 1) / len;
+  if (s <= 1) return sp;
+  sp.splits = static_cast<int>(s);
+  sp.len = len;
+  sp.ldp = (g.N + 3) / 4 * 4;
+  sp.stride = g.nprob * g.M * sp.ldp;
+  sp.bytes = s * sp.stride * 4;
+  return sp;
+}
+
 }  // namespace
 
 int64_t gemm_stat_tiles(int64_t n) { return (n + kTile - 1) / kTile; }
+
+int64_t gemm_split_bytes(const GemmArgs& g) {
+  const SplitPlan sp = plan_split(g);
+  return sp.splits > 1 ? sp.bytes : 0;
+}
 
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
   if (g.nprob < 1 || g.nprob > 2) return hipErrorInvalidValue;
@@ -1285,10 +1357,36 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
       (g.nprob != 1 || g.lg.cross == nullptr || g.M != 2 * ((g.lg.pair_rows + 15) / 16 * 16)))
     return hipErrorInvalidValue;
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
-  const GemmKernel k = select_kernel(g);
-  if (k == nullptr) return hipErrorInvalidValue;
   const int64_t tiles = ((g.M + kTile - 1) / kTile) * ((g.N + kTile - 1) / kTile) * g.nprob;
-  hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, stream, g);
+  const SplitPlan sp = plan_split(g);
+  if (sp.splits > 1 && g.split_ws != nullptr && g.split_ws_bytes >= sp.bytes) {
+    // Partials of every split with the Store epilogue (alpha 1), then one
+    // reduction applying the requested epilogue.
+    GemmArgs s = g;
+    s.epi = GemmEpilogue::StoreF32;
+    s.alpha = 1.f;
+    s.ldc = sp.ldp;
+    s.split_k = sp.splits;
+    s.split_len = sp.len;
+    s.split_stride = sp.stride;
+    for (int p = 0; p < g.nprob; ++p) s.prob[p].c = g.split_ws + p * g.M * sp.ldp;
+    const GemmKernel k = select_kernel(s);
+    if (k == nullptr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(tiles * sp.splits)), dim3(kThreads), 0,
+                       stream, s);
+    const int64_t total = g.M * g.N * g.nprob;
+    const unsigned blocks = static_cast<unsigned>((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, g.split_ws,
+                       sp.stride, sp.splits, g.M, g.N, sp.ldp, static_cast<float*>(g.prob[0].c),
+                       g.nprob > 1 ? static_cast<float*>(g.prob[1].c) : nullptr, g.ldc, g.alpha,
+                       g.epi == GemmEpilogue::AccumF32);
+    return hipGetLastError();
+  }
+  GemmArgs one = g;
+  one.split_k = 1;
+  const GemmKernel k = select_kernel(one);
+  if (k == nullptr) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, stream, one);
   return hipGetLastError();
 }
 

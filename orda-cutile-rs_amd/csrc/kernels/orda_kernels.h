@@ -64,9 +64,20 @@ struct GemmArgs {
   float alpha;
   int group_m;            // M-tiles per raster group (L2 reuse of B)
   LogitStatsArgs lg;
+  // Split-K workspace for Store/Accum GEMMs with fewer tiles than CUs: when
+  // given (gemm_split_bytes(g) bytes), launch_gemm splits K over several
+  // workgroups per tile and sums their fp32 partials in a fixed order.
+  float* split_ws;
+  int64_t split_ws_bytes;
+  // Set by launch_gemm for the split launch: K range s*split_len.. of the
+  // workgroups of split s, partials of split s at split_ws + s*split_stride.
+  int split_k;
+  int64_t split_len, split_stride;
 };
 
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);
+// Workspace bytes launch_gemm uses to split K for this GEMM (0: no split).
+int64_t gemm_split_bytes(const GemmArgs& g);
 int64_t gemm_stat_tiles(int64_t n);   // ceil(n/256)
 
 // ---------------------------------------------------------------- row pass
