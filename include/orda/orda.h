@@ -158,6 +158,12 @@ int32_t orda_ctx_set_stream(orda_ctx *ctx, void *hip_stream);
  * and staging). 0 = no bound. Allocations past it fail like a device OOM,
  * which drives the chunk-doubling retry (resolver.rs:107-126). */
 int32_t orda_ctx_set_memory_limit(orda_ctx *ctx, int64_t bytes);
+/* Bytes of logits staging the context may use per group of chunks
+ * (default 16 GiB). Consecutive chunks up to this size share one logits
+ * GEMM, row pass and backward GEMMs; a smaller budget runs more groups, each
+ * accumulating into grad_W. No counterpart in the reference, which runs one
+ * chunk at a time (src/api.rs:263-378). */
+int32_t orda_ctx_set_staging_budget(orda_ctx *ctx, int64_t bytes);
 /* Release the cached workspace. */
 int32_t orda_ctx_trim(orda_ctx *ctx);
 /* Per-kernel timing with HIP events on the context's stream. */

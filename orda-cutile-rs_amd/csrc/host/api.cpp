@@ -10,15 +10,19 @@
 // the optional INT8 round trip and the f64 loss assembly.
 //
 // Device-first layout: the logits of consecutive chunks are kept side by
-// side in one fp32 staging buffer (student block, then teacher block, each
-// [rows, round_up(V, 8)]); each chunk's logits_chunk is a slice of it. The
-// logits GEMM and the row pass run once per group of chunks, and so do the
-// backward GEMMs, which read the gradient rows (in place for f32 inputs, a
-// bf16 copy for bf16 inputs); grad_W is therefore written once per group
-// instead of read-modified-written per chunk. The group size is bounded by
-// the context's staging budget (16 GiB by default); an out-of-memory
-// failure first halves the group, then walks the reference's
-// chunk-doubling schedule (resolver.rs:107-126).
+// side in one staging buffer (student block, then teacher block, each
+// [rows, pitch]); each chunk's logits_chunk is a slice of it. Every loss
+// term comes from fp32 values (GEMM statistics, label logits, the KL cross
+// term), so the logits are stored in bf16 for bf16 inputs wherever the row
+// pass need not form the KL cross term from them: a Tied teacher (the GEMM
+// runs over interleaved student/teacher rows and forms it) or no KL term;
+// otherwise fp32. The logits GEMM and the row pass run once per group of
+// chunks, and so do the backward GEMMs, which read the gradient rows (in
+// place when the logits have the input dtype, else a bf16 copy); grad_W is
+// therefore written once per group instead of read-modified-written per
+// chunk. The group size is bounded by the context's staging budget (16 GiB
+// by default); an out-of-memory failure first halves the group, then walks
+// the reference's chunk-doubling schedule (resolver.rs:107-126).
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -1029,6 +1033,12 @@ int32_t orda_ctx_set_stream(orda_ctx* c, void* s) {
 int32_t orda_ctx_set_memory_limit(orda_ctx* c, int64_t bytes) {
   if (!c || bytes < 0) return ORDA_ERR_INVALID;
   c->mem_limit = bytes;
+  return ORDA_OK;
+}
+
+int32_t orda_ctx_set_staging_budget(orda_ctx* c, int64_t bytes) {
+  if (!c || bytes <= 0) return ORDA_ERR_INVALID;
+  c->staging_budget = bytes;
   return ORDA_OK;
 }
 

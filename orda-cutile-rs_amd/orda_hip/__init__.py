@@ -193,6 +193,11 @@ class Context:
     def set_memory_limit(self, nbytes: int):
         self._lib.orda_ctx_set_memory_limit(self.handle, int(nbytes))
 
+    def set_staging_budget(self, nbytes: int):
+        """Bytes of logits staging per group of chunks (default 16 GiB)."""
+        if self._lib.orda_ctx_set_staging_budget(self.handle, int(nbytes)) != L.ORDA_OK:
+            raise OrdaError("staging budget must be positive")
+
     def trim(self):
         self._lib.orda_ctx_trim(self.handle)
 

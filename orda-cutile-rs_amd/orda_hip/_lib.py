@@ -88,6 +88,7 @@ SIGNATURES = [
     ("orda_ctx_destroy", None, [C.c_void_p]),
     ("orda_ctx_set_stream", C.c_int32, [C.c_void_p, C.c_void_p]),
     ("orda_ctx_set_memory_limit", C.c_int32, [C.c_void_p, C.c_int64]),
+    ("orda_ctx_set_staging_budget", C.c_int32, [C.c_void_p, C.c_int64]),
     ("orda_ctx_trim", C.c_int32, [C.c_void_p]),
     ("orda_ctx_set_timing", C.c_int32, [C.c_void_p, C.c_int32]),
     ("orda_ctx_get_kernel_time", C.c_int32,

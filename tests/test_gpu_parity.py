@@ -245,6 +245,31 @@ def test_tied_bf16_k_tails(torch_dev, bt, h, v, chunk):
     check_output(got, ref, kind="bf16")
 
 
+@pytest.mark.parametrize("dtype", [None, "bf16"])
+def test_multi_group_split_k(torch_dev, dtype):
+    """A staging budget of one chunk runs four groups, so grad_W accumulates
+    across groups; with V=2000 and H=64 both backward GEMMs have fewer tiles
+    than CUs and split K (grad_W over 2048 rows in 4 splits, then the
+    accumulating reduction)."""
+    bt, h, v = 4096, 64, 2000
+    s, th = normal((bt, h), 71), normal((bt, h), 72)
+    w = normal((v, h), 73, 0.05)
+    y = uniform_labels(bt, v, 74)
+    y[::11] = -100
+    opts = LossOptions(kd_weight=0.4, temperature=1.5, label_smoothing=0.1,
+                       chunk_size=ChunkSize.Fixed(1024))
+    if dtype == "bf16":
+        s, th, w = bf16_round(s), bf16_round(th), bf16_round(w)
+    ctx = H.Context(0)
+    ctx.set_staging_budget(1)   # one chunk per group
+    got = H.distillation_loss(gpu(torch_dev, s, dtype), gpu(torch_dev, w, dtype),
+                              gpu(torch_dev, y), Teacher.Tied(gpu(torch_dev, th, dtype)), opts,
+                              ctx=ctx)
+    ref = O.distillation_loss(s, w, y, Teacher.Tied(th), opts)
+    check_output(got, ref, kind="bf16" if dtype else "f32")
+    ctx.close()
+
+
 def test_ignored_labels_and_reductions(torch_dev):
     bt, h, v = 200, 64, 777
     s, th = normal((bt, h), 51), normal((bt, h), 52)
