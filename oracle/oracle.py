@@ -1,8 +1,8 @@
 """ctypes/numpy front end of the CPU oracle (liborda_oracle.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()`` and
-the ``cpu_baseline`` leg of bench.py, always as the checker. The product
-never imports it.
+the ``cpu_baseline`` leg of bench.py, always as the reference side of a
+comparison or as the timed CPU baseline. The product never imports it.
 
 The functions mirror the reference crate's Rust API (file:line cited on each
 C entry point in orda_oracle.c). Teacher/option objects are duck-typed: any
