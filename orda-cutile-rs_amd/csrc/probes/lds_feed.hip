@@ -6,7 +6,8 @@
 // stage (64 = a K-major stage, 128 = a K-major stage pair, 512 = an MN-major
 // row of 256 bf16), row pitch 262272 bytes (the padded pitch of a 131072-wide
 // bf16 logits row). `groups` distinct row blocks are read: 32 gives 4 blocks
-// per XCD (8 workgroups share each), 8 gives one block per XCD. Build with
+// per XCD (8 workgroups share each), 8 gives one block per XCD. A last set
+// of runs reads every stage as one contiguous block instead. Build with
 // `make -C orda-cutile-rs_amd probes`; prints TB/s per configuration.
 #include <hip/hip_runtime.h>
 #include <stdio.h>
@@ -27,12 +28,14 @@ __global__ __launch_bounds__(256, 1) void feed(const unsigned char* src, int64_t
   uint32_t goff[XF];
   for (int t = 0; t < XF; ++t) {
     const int P = (t * 4 + wave) * 64 + lane;
-    goff[t] = (P / cpr) * pitch + (P % cpr) * 16;
+    goff[t] = (P / cpr) * (mn == 2 ? rowb : pitch) + (P % cpr) * 16;
   }
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
   auto issue = [&](int st, int slot) {
-    const unsigned char* s = mn ? src + (int64_t)(blockIdx.x % groups) * 512 + (int64_t)st * rows_per_stage * pitch
-                                : base + (int64_t)st * rowb;
+    // mn 1: MN-major rows; mn 2: blocked, each stage one contiguous block
+    const unsigned char* s = mn == 1 ? src + (int64_t)(blockIdx.x % groups) * 512 + (int64_t)st * rows_per_stage * pitch
+                           : mn == 2 ? src + ((int64_t)(blockIdx.x % groups) * stages + st) * (XF * 4096)
+                                     : base + (int64_t)st * rowb;
     uint64_t p = (uint64_t)s;
     uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p), hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
     uint64_t ps = ((uint64_t)hi << 32) | lo;
@@ -95,6 +98,18 @@ int main() {
              (long long)pitch, rowb, groups, tot8 / t44 / 1e9, tot4 / t84 / 1e9);
       fflush(stdout);
     }
+  }
+  // blocked: group g's stages are consecutive contiguous blocks of the stage size
+  for (int groups : {32, 8}) {
+    const int rowb = 128;
+    const int nst8 = (int)(bytes / ((size_t)groups * 32768)) < 2048 ? (int)(bytes / ((size_t)groups * 32768)) : 2048;
+    const int nst4 = nst8;
+    const double tot8 = (double)nwg * nst8 * 32768.0, tot4 = (double)nwg * nst4 * 16384.0;
+    float t44 = run<4, 8>(src, pitch, rowb, nst8, groups, nwg, sink, 2);
+    float t84 = run<8, 4>(src, pitch, rowb, nst4, groups, nwg, sink, 2);
+    printf("blocked 32KB/16KB stages   groups %3d: ring 4x32KB %.1f TB/s | ring 8x16KB %.1f TB/s\n",
+           groups, tot8 / t44 / 1e9, tot4 / t84 / 1e9);
+    fflush(stdout);
   }
   CHECK(hipFree(src)); CHECK(hipFree(sink));
   }
