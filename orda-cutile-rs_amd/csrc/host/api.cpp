@@ -377,11 +377,20 @@ orda::DType logits_dtype(const LossPlan& P, bool paired) {
                                                              : orda::DType::F32;
 }
 
+// Precomputed teacher logits already in the logits dtype, with a pitch of a
+// multiple of 8 elements and a 16-byte aligned base (the row pass reads
+// 16-byte vectors): the row pass reads them where they are instead of from a
+// copy in the staging buffer.
+bool teacher_logits_direct(const LossPlan& P, const Inputs& in) {
+  return P.need_teacher && P.mode == ORDA_TEACHER_PRECOMPUTED && in.tl.t == logits_dtype(P, false) &&
+         in.tl.ld % 8 == 0 && reinterpret_cast<uintptr_t>(in.tl.p) % 16 == 0;
+}
+
 // Device bytes the loss stages per chunk row.
 int64_t staged_bytes_per_row(const LossPlan& P, const Inputs& in) {
   const bool paired = paired_rows(P, in);
   const orda::DType lt = logits_dtype(P, paired);
-  const int64_t blocks = P.need_teacher ? 2 : 1;
+  const int64_t blocks = P.need_teacher && !teacher_logits_direct(P, in) ? 2 : 1;
   const int64_t nst = orda::gemm_stat_tiles(P.v);
   int64_t b = blocks * logits_pitch(P.v) *
               (orda::dtype_size(lt) + (lt == P.dt ? 0 : orda::dtype_size(P.dt)));
@@ -413,7 +422,8 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   const int64_t ldl = logits_pitch(v);
   const int64_t nst = gemm_stat_tiles(v);
   const int64_t cap = std::min(bt, G * cs);
-  const int blocks = P.need_teacher ? 2 : 1;
+  const bool tl_direct = teacher_logits_direct(P, in);
+  const int blocks = P.need_teacher && !tl_direct ? 2 : 1;
   const bool tied_tce = P.mode == ORDA_TEACHER_TIED && P.w_t > 0.f;
 
   // Every loss term comes from fp32 values: the GEMM's tile statistics and
@@ -508,7 +518,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
         r.src = at(in.tl.p, gs * in.tl.ld, in.tl.t);
         r.lds = in.tl.ld;
         r.dst_type = lt;
-        r.dst = Lt;
+        r.dst = tl_direct ? nullptr : Lt;
         r.ldd = ldl;
         r.n_rows = btg;
         r.v = v;
@@ -538,7 +548,8 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       RowPassArgs r{};
       r.ltype = lt;
       r.student = Ls;
-      r.teacher = P.need_teacher ? Lt : nullptr;
+      r.teacher = !P.need_teacher ? nullptr : tl_direct ? at(in.tl.p, gs * in.tl.ld, in.tl.t) : Lt;
+      r.ld_t = tl_direct ? in.tl.ld : 0;
       r.grad_s = dt == lt ? nullptr : Gs;
       r.grad_t = dt == lt ? nullptr : Gt;
       r.gtype = dt;

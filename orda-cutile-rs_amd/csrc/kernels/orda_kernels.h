@@ -88,6 +88,8 @@ struct RowPassArgs {
   void* student;           // row r of the student block at student + r*ld
   void* teacher;           // row r of the teacher block (may be null)
   int64_t ld;              // pitch (elements) of both blocks, multiple of 8
+  int64_t ld_t;            // teacher pitch when it differs (read-only teacher
+                           // rows, e.g. Precomputed logits in place); 0: ld
   int64_t n_rows;          // row pairs
   int64_t v;               // vocabulary
   const float4* stats_s;   // per-row partial stats of student rows

@@ -323,7 +323,7 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
   const int nvec = static_cast<int>((v + NV - 1) / NV);
   const int nfull = static_cast<int>(v / NV);
   const LT* srow = static_cast<const LT*>(a.student) + r * a.ld;
-  const LT* trow = HT ? static_cast<const LT*>(a.teacher) + r * a.ld : nullptr;
+  const LT* trow = HT ? static_cast<const LT*>(a.teacher) + r * (a.ld_t ? a.ld_t : a.ld) : nullptr;
   GT* gsrow = static_cast<GT*>(a.grad_s ? a.grad_s : a.student) + r * a.ld;
   GT* gtrow = TG ? static_cast<GT*>(a.grad_s ? a.grad_t : a.teacher) + r * a.ld : nullptr;
 
@@ -738,8 +738,9 @@ hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
   if ((a.teacher_ce || kl || tg) && a.stats_t == nullptr) return hipErrorInvalidValue;
   const DType gt = a.grad_s ? a.gtype : a.ltype;
   if (a.grad_s && (tg && a.grad_t == nullptr)) return hipErrorInvalidValue;
+  if (a.ld_t && ((a.ld_t % 8) || (tg && a.grad_s == nullptr))) return hipErrorInvalidValue;
   if (a.cross != nullptr && a.row_consts != nullptr && a.ltype == DType::BF16 &&
-      a.grad_s == nullptr && (!(kl || tg || a.teacher_ce) || has_t)) {
+      a.grad_s == nullptr && a.ld_t == 0 && (!(kl || tg || a.teacher_ce) || has_t)) {
     // Paired layout, bf16 in place: per-row constants, then the chunked
     // elementwise gradient.
     const int64_t chunks = (a.v + kChunk - 1) / kChunk;
