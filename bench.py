@@ -211,7 +211,7 @@ def read_traffic(workload, kind):
     return None if rec is None else rec["bytes_per_launch"]
 
 
-def summarize(dirs, copy_bytes):
+def summarize(dirs, copy_bytes, timed_steps=0):
     """Markdown summary of rocprofv3 output directories: kernel-trace stats
     (per kernel kind) and, where present, FETCH_SIZE / WRITE_SIZE counter
     collections turned into HBM bytes per launch with the copy-kernel factor
@@ -221,7 +221,14 @@ def summarize(dirs, copy_bytes):
     from collections import defaultdict
     stats = defaultdict(lambda: [0, 0.0])           # kind -> [calls, total ns]
     counters = defaultdict(lambda: defaultdict(list))   # counter -> kind -> [KiB per dispatch]
+    trace = defaultdict(list)                       # kind -> [(start ns, duration ns)]
     for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                k = kernel_kind(r["Kernel_Name"])
+                if k:
+                    t0, t1 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+                    trace[k].append((t0, t1 - t0))
         for f in glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True):
             for r in csv.DictReader(open(f)):
                 k = kernel_kind(r["Name"])
@@ -235,10 +242,23 @@ def summarize(dirs, copy_bytes):
                     counters[r["Counter_Name"]][k].append(float(r["Counter_Value"]))
     out = []
     if stats:
-        out.append("| kernel | calls | avg duration (ms) | total (ms) |")
-        out.append("|---|---|---|---|")
+        # Steps are counted by the logits GEMM (one launch per group and step);
+        # the timed-steps column averages each kind over its launches in the
+        # last `timed_steps` steps, the steps bench.py times.
+        steps = len(trace.get("gemm_logits", [])) or None
+        hdr = "| kernel | calls | avg duration (ms) | total (ms) |"
+        if timed_steps and steps:
+            hdr += f" avg over the last {timed_steps} steps (ms) |"
+        out.append(hdr)
+        out.append("|---|---|---|---|" + ("---|" if timed_steps and steps else ""))
         for k, (n, ns) in sorted(stats.items(), key=lambda x: -x[1][1]):
-            out.append(f"| {k} | {n} | {ns / n / 1e6:.4f} | {ns / 1e6:.3f} |")
+            line = f"| {k} | {n} | {ns / n / 1e6:.4f} | {ns / 1e6:.3f} |"
+            if timed_steps and steps:
+                durs = [dt for _, dt in sorted(trace.get(k, []))]
+                per_step = max(len(durs) // steps, 1)
+                last = durs[-timed_steps * per_step:] if durs else []
+                line += f" {sum(last) / len(last) / 1e6:.4f} |" if last else " - |"
+            out.append(line)
     traffic = {}
     if counters:
         factors = {}
@@ -283,9 +303,11 @@ def main():
                          "(reference kernel for HBM counter calibration)")
     ap.add_argument("--summarize", nargs="+", metavar="DIR",
                     help="print a markdown summary of rocprofv3 output directories and exit")
+    ap.add_argument("--timed-steps", type=int, default=0, metavar="K",
+                    help="with --summarize: also average each kernel over the last K steps")
     args = ap.parse_args()
     if args.summarize:
-        print(summarize(args.summarize, args.copy_calibration))
+        print(summarize(args.summarize, args.copy_calibration, args.timed_steps))
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
