@@ -1065,6 +1065,32 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         }
       }
     };
+    // bf16 rows of full tiles leave as 16-byte stores: for each fragment pair
+    // (j, j+1), one v_permlane16_swap per dword gives the lanes of 16-lane
+    // row g (g = lane/16) eight consecutive columns, 16*(j + g%2) + 8*(g/2)
+    // onward, so a store instruction writes 64 contiguous bytes of each of 16
+    // rows instead of 32. Done by every lane (the swap pairs lanes 16 apart,
+    // which hold the same row); the stores follow under the row's test.
+    auto swap_rows = [&](const f32x4 (&v)[kFrag], u32x4 (&w)[kFrag / 2]) {
+#pragma unroll
+      for (int jp = 0; jp < kFrag; jp += 2) {
+        const auto a = __builtin_amdgcn_permlane16_swap(pack_bf16(v[jp][0], v[jp][1]),
+                                                        pack_bf16(v[jp + 1][0], v[jp + 1][1]),
+                                                        false, false);
+        const auto b = __builtin_amdgcn_permlane16_swap(pack_bf16(v[jp][2], v[jp][3]),
+                                                        pack_bf16(v[jp + 1][2], v[jp + 1][3]),
+                                                        false, false);
+        w[jp / 2] = u32x4{a[0], b[0], a[1], b[1]};
+      }
+    };
+    // rowbase: the row's element at column tc.n0 + wn*128.
+    auto store_swapped = [&](LT* rowbase, const u32x4 (&w)[kFrag / 2]) {
+      const int c0 = 16 * (lgrp & 1) + 8 * (lgrp >> 1);
+#pragma unroll
+      for (int jp = 0; jp < kFrag; jp += 2)
+        *reinterpret_cast<u32x4*>(rowbase + 16 * jp + c0) = w[jp / 2];
+    };
+    constexpr bool kSwapStore = Elem<LT>::kSize == 2;
     // The label's logit, if this lane holds its column (16j + e == yl):
     // select e, then j.
     auto pick = [&](const f32x4 (&v)[kFrag], int yl) {
@@ -1130,9 +1156,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         dT = quad_sum(dT);
         sx = quad_sum(sx);
         if (lgrp == 0) part[wn * 256 + rl] = make_float4(mx, d1, dT, sx);
+        u32x4 aw[kFrag / 2];
+        if constexpr (kSwapStore && kFull) swap_rows(av, aw);
         if (row < g.M) {
           if (hit) g.lg.xy[tc.p * g.M + row] = xy;
-          store_row(full_c, C + row * g.ldc + colw, av);
+          if constexpr (kSwapStore && kFull)
+            store_swapped(C + row * g.ldc + (colw - 4 * lgrp), aw);
+          else
+            store_row(full_c, C + row * g.ldc + colw, av);
         }
       }
     };
@@ -1197,13 +1228,23 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
           part[wn * 256 + rt] = make_float4(mt, d1t, dTt, sxt);
           xpart[wn * 256 + rt] = cx;
         }
+        u32x4 sw[kFrag / 2], tw[kFrag / 2];
+        if constexpr (kSwapStore && kFull) {
+          swap_rows(as, sw);
+          swap_rows(at, tw);
+        }
         if (row < prs) {
           if (hit) {
             g.lg.xy[row] = xys;
             g.lg.xy[prs + row] = xyt;
           }
-          store_row(full_c, C + row * g.ldc + colw, as);
-          store_row(full_c, C + (prs + row) * g.ldc + colw, at);
+          if constexpr (kSwapStore && kFull) {
+            store_swapped(C + row * g.ldc + (colw - 4 * lgrp), sw);
+            store_swapped(C + (prs + row) * g.ldc + (colw - 4 * lgrp), tw);
+          } else {
+            store_row(full_c, C + row * g.ldc + colw, as);
+            store_row(full_c, C + (prs + row) * g.ldc + colw, at);
+          }
         }
       }
     };
