@@ -513,8 +513,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
     for (int j = 0; j < kFrag; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   constexpr int SK = kSlab / Elem<T>::kSize;
-  // The logits epilogue wants each lane to own consecutive columns of a row.
-  constexpr bool kSwapAB = EPI == GemmEpilogue::Logits;
+  // The logits epilogue, and the store epilogue of grad_W (A M-major),
+  // take swapped MFMA operands, so that each lane owns 4 consecutive columns
+  // of a row (the grad_hidden loop measured faster unswapped).
+  constexpr bool kSwapAB = EPI == GemmEpilogue::Logits || !AK;
 
   const int nkf = static_cast<int>(Kl / SK);   // full stages
   u32x4 ra[2][kFrag], rb[2][kFrag];
@@ -983,25 +985,61 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
   // ------------------------------------------------------------ epilogue
   const int lrow = lane & 15;
   const int lgrp = lane >> 4;
-  const int row_w = tc.m0 + wm * 128;          // first row of this wave
-  const int col_l = tc.n0 + wn * 128 + lrow;   // this lane's column of fragment j=0
   if constexpr (EPI == GemmEpilogue::StoreF32 || EPI == GemmEpilogue::AccumF32) {
     float* C = static_cast<float*>(pr.c);
+    if constexpr (!kSwapAB) {
+      // acc[i][j][e] is row wm*128 + 16i + 4*lgrp + e, column wn*128 + 16j + lrow.
+      const int row_w = tc.m0 + wm * 128;
+      const int col_l = tc.n0 + wn * 128 + lrow;
+#pragma unroll
+      for (int i = 0; i < kFrag; ++i) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t row = row_w + i * 16 + lgrp * 4 + e;
+          if (row >= g.M) continue;
+          float* crow = C + row * g.ldc;
+#pragma unroll
+          for (int j = 0; j < kFrag; ++j) {
+            const int64_t col = col_l + j * 16;
+            if (col < g.N) {
+              float v = acc[i][j][e];
+              if constexpr (EPI == GemmEpilogue::AccumF32) v = g.alpha * (crow[col] + v);
+              else v = g.alpha * v;
+              crow[col] = v;
+            }
+          }
+        }
+      }
+      return;
+    }
+    // acc[i][j][e] is row wm*128 + 16i + lrow, column wn*128 + 16j + 4*lgrp + e
+    // (swapped operands): each lane writes 4 consecutive columns of a row as
+    // one 16-byte store where the pitch and base allow.
+    const bool vec = (g.ldc % 4) == 0 && (reinterpret_cast<uintptr_t>(C) % 16) == 0;
+    const int64_t col0 = static_cast<int64_t>(tc.n0) + wn * 128 + 4 * lgrp;
 #pragma unroll
     for (int i = 0; i < kFrag; ++i) {
+      const int64_t row = static_cast<int64_t>(tc.m0) + wm * 128 + i * 16 + lrow;
+      if (row >= g.M) continue;
+      float* crow = C + row * g.ldc + col0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t row = row_w + i * 16 + lgrp * 4 + e;
-        if (row >= g.M) continue;
-        float* crow = C + row * g.ldc;
+      for (int j = 0; j < kFrag; ++j) {
+        const int64_t col = col0 + j * 16;
+        f32x4 v = acc[i][j];
+        if (vec && col + 4 <= g.N) {
+          f32x4* dst = reinterpret_cast<f32x4*>(crow + j * 16);
+          if constexpr (EPI == GemmEpilogue::AccumF32) v = g.alpha * (*dst + v);
+          else v = g.alpha * v;
+          *dst = v;
+        } else {
 #pragma unroll
-        for (int j = 0; j < kFrag; ++j) {
-          const int64_t col = col_l + j * 16;
-          if (col < g.N) {
-            float v = acc[i][j][e];
-            if constexpr (EPI == GemmEpilogue::AccumF32) v = g.alpha * (crow[col] + v);
-            else v = g.alpha * v;
-            crow[col] = v;
+          for (int e = 0; e < 4; ++e) {
+            if (col + e < g.N) {
+              float x = v[e];
+              if constexpr (EPI == GemmEpilogue::AccumF32) x = g.alpha * (crow[j * 16 + e] + x);
+              else x = g.alpha * x;
+              crow[j * 16 + e] = x;
+            }
           }
         }
       }
