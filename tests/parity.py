@@ -47,6 +47,26 @@ def check_grad(name, got, ref, kind="f32"):
     return ndiff / max(nref, 1e-30)
 
 
+def check_quantized_grad_weight(got, ref, y, ignore=-100):
+    """Dequantized grad_W of an fp32 run: target rows carry the exact
+    gradient (fp32 tolerance); other rows are code*scale with codes within
+    ±1 of the oracle's (grad_W itself differs in its last bits, so a code may
+    flip at a rounding boundary) and scales within 1e-3 relative."""
+    gw, rw = to_np(got.grad_weight), ref.grad_weight
+    gq, rq = to_np(got.quant_codes).astype(np.int32), ref.quant_codes.astype(np.int32)
+    gs, rs = to_np(got.quant_scales).reshape(-1), ref.quant_scales
+    tgt = sorted({int(t) for t in y if t != ignore})
+    assert np.all(np.abs(gq - rq) <= 1)
+    assert np.mean(gq != rq) < 0.01
+    np.testing.assert_allclose(gs, rs, rtol=1e-3, atol=1e-30)
+    mask = np.zeros(rw.shape[0], bool)
+    mask[tgt] = True
+    if tgt:
+        check_grad("grad_weight[target rows]", gw[mask], rw[mask])
+    # non-target rows are exactly code * scale
+    np.testing.assert_array_equal(gw[~mask], (gq[~mask] * gs[~mask, None]).astype(np.float32))
+
+
 def check_output(got, ref, kind="f32", skip_grad_weight=False):
     for k in ("loss", "student_ce", "teacher_ce", "kl"):
         check_scalar(k, getattr(got, k), getattr(ref, k))

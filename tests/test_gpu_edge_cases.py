@@ -1,0 +1,177 @@
+"""GPU parity on the edges of the bf16 and staging paths, against the CPU
+oracle on identical seeded inputs (bf16 runs feed the oracle the same
+bf16-rounded values; tolerances as in tests/parity.py):
+
+* Separate teacher in bf16 with a teacher width that is not a multiple of 8
+  (staged into a padded copy) and Hs != Ht;
+* Precomputed teacher logits next to bf16 hidden states: fp32 logits used in
+  place, fp32 logits with an odd vocabulary (converted), bf16 logits
+  (converted), and a strided device view;
+* hidden widths that are not a multiple of 8 (padded staging of bf16);
+* strided device views of the inputs, 16-byte aligned (used in place) and
+  not (staged);
+* paired student/teacher rows at a row count that is not a multiple of 16;
+* temperatures far from 1 and full label smoothing (alpha = 1);
+* stochastic INT8 rounding of grad_W through the whole path.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import bf16_round, normal, uniform_labels
+from parity import check_grad, check_output, check_quantized_grad_weight, to_np
+
+import orda_hip as H
+from orda_hip import ChunkSize, KernelConfig, LossOptions, Teacher
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a visible GPU"
+    assert H.is_available(), "liborda_hip.so does not see a gfx950 device"
+    return torch, torch.device("cuda:0")
+
+
+def dev(torch_dev, a, dtype=None):
+    torch, d = torch_dev
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(d)
+    return t.to(torch.bfloat16) if dtype == "bf16" else t
+
+
+def strided(torch_dev, a, offset, pad, dtype=None):
+    """Device view of `a` inside a wider buffer: columns [offset, offset+cols)
+    of rows `pad` elements longer than `a`'s, so the view has a row pitch of
+    cols + pad and a base `offset` elements into the allocation."""
+    torch, d = torch_dev
+    rows, cols = a.shape
+    big = np.full((rows, cols + pad), np.nan, np.float32)
+    big[:, offset:offset + cols] = a
+    t = dev(torch_dev, big, dtype)
+    v = t[:, offset:offset + cols]
+    assert v.stride(0) == cols + pad and v.stride(1) == 1
+    return v
+
+
+def tied_inputs(bt, h, v, seed, wstd=0.03):
+    s = bf16_round(normal((bt, h), seed))
+    th = bf16_round(normal((bt, h), seed + 1))
+    w = bf16_round(normal((v, h), seed + 2, wstd))
+    y = uniform_labels(bt, v, seed + 3)
+    return s, th, w, y
+
+
+def test_separate_bf16_unaligned_teacher_width(torch_dev):
+    bt, hs, ht, v = 192, 96, 100, 1500
+    s, ws = bf16_round(normal((bt, hs), 81)), bf16_round(normal((v, hs), 82, 0.03))
+    th, wt = bf16_round(normal((bt, ht), 83)), bf16_round(normal((v, ht), 84, 0.03))
+    y = uniform_labels(bt, v, 85)
+    y[::9] = -100
+    opts = LossOptions(kd_weight=0.5, temperature=2.0, label_smoothing=0.1,
+                       teacher_ce_weight=1.0, chunk_size=ChunkSize.Fixed(64))
+    got = H.distillation_loss(dev(torch_dev, s, "bf16"), dev(torch_dev, ws, "bf16"),
+                              dev(torch_dev, y),
+                              Teacher.Separate(dev(torch_dev, th, "bf16"),
+                                               dev(torch_dev, wt, "bf16")), opts)
+    ref = O.distillation_loss(s, ws, y, Teacher.Separate(th, wt), opts)
+    check_output(got, ref, kind="bf16")
+
+
+@pytest.mark.parametrize("tl_dtype,v,view", [(None, 1024, False), (None, 1001, False),
+                                             ("bf16", 1024, False), (None, 1024, True)])
+def test_precomputed_logits_with_bf16_hidden(torch_dev, tl_dtype, v, view):
+    bt, h = 160, 64
+    s, w = bf16_round(normal((bt, h), 91)), bf16_round(normal((v, h), 92, 0.03))
+    y = uniform_labels(bt, v, 93)
+    tl = normal((bt, v), 94, 2.0)
+    tl[np.arange(bt), y] += 6.0
+    if tl_dtype == "bf16":
+        tl = bf16_round(tl)
+    tl_dev = strided(torch_dev, tl, 8, 16, tl_dtype) if view else dev(torch_dev, tl, tl_dtype)
+    opts = LossOptions(kd_weight=0.7, temperature=1.0, chunk_size=ChunkSize.Fixed(48))
+    got = H.distillation_loss(dev(torch_dev, s, "bf16"), dev(torch_dev, w, "bf16"),
+                              dev(torch_dev, y), Teacher.Precomputed(tl_dev), opts)
+    ref = O.distillation_loss(s, w, y, Teacher.Precomputed(tl), opts)
+    assert got.grad_teacher_hidden is None
+    check_output(got, ref, kind="bf16")
+
+
+@pytest.mark.parametrize("h", [100, 13])
+def test_tied_bf16_hidden_width_not_multiple_of_8(torch_dev, h):
+    bt, v = 144, 999
+    s, th, w, y = tied_inputs(bt, h, v, 101)
+    opts = LossOptions(kd_weight=0.4, temperature=1.5, label_smoothing=0.1,
+                       teacher_ce_weight=1.0, chunk_size=ChunkSize.Fixed(64))
+    got = H.distillation_loss(dev(torch_dev, s, "bf16"), dev(torch_dev, w, "bf16"),
+                              dev(torch_dev, y), Teacher.Tied(dev(torch_dev, th, "bf16")), opts)
+    ref = O.distillation_loss(s, w, y, Teacher.Tied(th), opts)
+    check_output(got, ref, kind="bf16")
+
+
+@pytest.mark.parametrize("dtype", [None, "bf16"])
+@pytest.mark.parametrize("offset", [8, 3])
+def test_strided_device_views(torch_dev, dtype, offset):
+    """offset 8 keeps every row 16-byte aligned (inputs used in place),
+    offset 3 does not (inputs staged into packed copies)."""
+    bt, h, v = 128, 64, 1200
+    s, th, w, y = tied_inputs(bt, h, v, 111)
+    opts = LossOptions(kd_weight=0.4, temperature=1.5, teacher_ce_weight=1.0,
+                       chunk_size=ChunkSize.Fixed(32))
+    got = H.distillation_loss(strided(torch_dev, s, offset, 16, dtype),
+                              strided(torch_dev, w, offset, 16, dtype), dev(torch_dev, y),
+                              Teacher.Tied(strided(torch_dev, th, offset, 16, dtype)), opts)
+    ref = O.distillation_loss(s, w, y, Teacher.Tied(th), opts)
+    check_output(got, ref, kind="bf16" if dtype else "f32")
+
+
+@pytest.mark.parametrize("bt,chunk", [(37, None), (203, 70)])
+def test_paired_rows_not_multiple_of_16(torch_dev, bt, chunk):
+    h, v = 64, 500
+    s, th, w, y = tied_inputs(bt, h, v, 121)
+    y[::5] = -100
+    cs = ChunkSize.Fixed(chunk) if chunk else ChunkSize.Auto
+    opts = LossOptions(kd_weight=0.4, temperature=1.5, label_smoothing=0.1, chunk_size=cs)
+    got = H.distillation_loss(dev(torch_dev, s, "bf16"), dev(torch_dev, w, "bf16"),
+                              dev(torch_dev, y), Teacher.Tied(dev(torch_dev, th, "bf16")), opts)
+    ref = O.distillation_loss(s, w, y, Teacher.Tied(th), opts)
+    check_output(got, ref, kind="bf16")
+
+
+@pytest.mark.parametrize("dtype", [None, "bf16"])
+@pytest.mark.parametrize("temperature,alpha", [(0.25, 0.1), (8.0, 0.1), (1.5, 1.0)])
+def test_temperature_and_smoothing_extremes(torch_dev, dtype, temperature, alpha):
+    bt, h, v = 192, 64, 2000
+    s, th, w, y = tied_inputs(bt, h, v, 131, wstd=0.1)
+    opts = LossOptions(kd_weight=0.6, temperature=temperature, label_smoothing=alpha,
+                       teacher_ce_weight=1.0, chunk_size=ChunkSize.Fixed(64))
+    got = H.distillation_loss(dev(torch_dev, s, dtype), dev(torch_dev, w, dtype),
+                              dev(torch_dev, y), Teacher.Tied(dev(torch_dev, th, dtype)), opts)
+    ref = O.distillation_loss(s, w, y, Teacher.Tied(th), opts)
+    check_output(got, ref, kind="bf16" if dtype else "f32")
+
+
+@pytest.mark.parametrize("dtype", [None, "bf16"])
+def test_stochastic_int8_through_the_path(torch_dev, dtype):
+    """Stochastic rounding draws one SplitMix64 number per grad_W element in
+    row-major order (src/quant.rs:120-144). fp32: codes within ±1 of the
+    oracle's and target rows exact; bf16: the dequantized grad_W within the
+    bf16 gradient tolerance (its codes follow bf16-rounded gradients)."""
+    bt, h, v = 256, 64, 1500
+    s, th, w, y = tied_inputs(bt, h, v, 141)
+    if dtype is None:
+        s, th, w = normal((bt, h), 141), normal((bt, h), 142), normal((v, h), 143, 0.03)
+    cfg = KernelConfig(quantize_grad_weight=True, stochastic_rounding=True, stochastic_seed=987)
+    opts = LossOptions(kd_weight=0.4, temperature=1.5, label_smoothing=0.1, config=cfg,
+                       chunk_size=ChunkSize.Fixed(64))
+    got = H.distillation_loss(dev(torch_dev, s, dtype), dev(torch_dev, w, dtype),
+                              dev(torch_dev, y), Teacher.Tied(dev(torch_dev, th, dtype)), opts,
+                              quant_codes=True)
+    ref = O.distillation_loss(s, w, y, Teacher.Tied(th), opts)
+    if dtype is None:
+        check_output(got, ref, skip_grad_weight=True)
+        check_quantized_grad_weight(got, ref, y)
+    else:
+        check_output(got, ref, kind="bf16", skip_grad_weight=True)
+        check_grad("grad_weight (dequantized)", to_np(got.grad_weight), ref.grad_weight, "bf16")

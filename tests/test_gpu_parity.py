@@ -11,7 +11,7 @@ import pytest
 
 import oracle as O
 from helpers import bf16_round, labels, mat, normal, uniform_labels
-from parity import check_grad, check_output, check_scalar, to_np
+from parity import check_grad, check_output, check_quantized_grad_weight, check_scalar, to_np
 
 import orda_hip as H
 from orda_hip import (ChunkSize, KernelConfig, LossOptions, OrdaError, Reduction, Teacher)
@@ -126,26 +126,6 @@ def test_int8_small(torch_dev):
                                   config=KernelConfig(quantize_grad_weight=True)))
     check_output(got, ref, skip_grad_weight=True)
     check_quantized_grad_weight(got, ref, labels(bt, v, None))
-
-
-def check_quantized_grad_weight(got, ref, y, ignore=-100):
-    """Dequantized grad_W: target rows carry the exact gradient (fp32 path
-    tolerance); other rows are code*scale with codes within ±1 of the
-    oracle's (grad_W itself differs in its last bits, so a code may flip at a
-    rounding boundary) and scales within 1e-3 relative."""
-    gw, rw = to_np(got.grad_weight), ref.grad_weight
-    gq, rq = to_np(got.quant_codes).astype(np.int32), ref.quant_codes.astype(np.int32)
-    gs, rs = to_np(got.quant_scales).reshape(-1), ref.quant_scales
-    tgt = sorted({int(t) for t in y if t != ignore})
-    assert np.all(np.abs(gq - rq) <= 1)
-    assert np.mean(gq != rq) < 0.01
-    np.testing.assert_allclose(gs, rs, rtol=1e-3, atol=1e-30)
-    mask = np.zeros(rw.shape[0], bool)
-    mask[tgt] = True
-    if tgt:
-        check_grad("grad_weight[target rows]", gw[mask], rw[mask])
-    # non-target rows are exactly code * scale
-    np.testing.assert_array_equal(gw[~mask], (gq[~mask] * gs[~mask, None]).astype(np.float32))
 
 
 # ------------------------------------------------ benchmark-shape cases
