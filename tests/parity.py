@@ -47,6 +47,30 @@ def check_grad(name, got, ref, kind="f32"):
     return ndiff / max(nref, 1e-30)
 
 
+def check_grad_device(name, got, ref, kind="f32", block=8192):
+    """check_grad's criteria evaluated with torch on the tensors' device, a
+    block of rows at a time in float64, for gradients too large to copy to
+    the host."""
+    import torch
+    assert tuple(got.shape) == tuple(ref.shape), f"{name}: shape {tuple(got.shape)} vs {tuple(ref.shape)}"
+    rtol = GRAD_RTOL[kind]
+    sref = sdiff = 0.0
+    amax = emax = 0.0
+    for r0 in range(0, got.shape[0], block):
+        g = got[r0:r0 + block].double()
+        r = ref[r0:r0 + block].double()
+        assert bool(torch.isfinite(g).all()), f"{name}: non-finite values"
+        d = g - r
+        sref += float((r * r).sum())
+        sdiff += float((d * d).sum())
+        amax = max(amax, float(r.abs().max()))
+        emax = max(emax, float(d.abs().max()))
+    nref, ndiff = sref ** 0.5, sdiff ** 0.5
+    assert ndiff <= rtol * nref + 1e-12, f"{name}: rel fro err {ndiff / max(nref, 1e-30):.3e}"
+    assert emax <= rtol * amax + 1e-7, f"{name}: max elem err {emax:.3e} vs max|ref| {amax:.3e}"
+    return ndiff / max(nref, 1e-30)
+
+
 def check_quantized_grad_weight(got, ref, y, ignore=-100):
     """Dequantized grad_W of an fp32 run: target rows carry the exact
     gradient (fp32 tolerance); other rows are code*scale with codes within

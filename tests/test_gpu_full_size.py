@@ -1,0 +1,63 @@
+"""Parity at the full benchmark shape: Tied teacher, BT=8192, H=4096,
+V=131072, bf16 inputs, kd 0.4, T 1.5, label smoothing 0.1, INT8 grad_W
+(Auto plan: 16 chunks x 512 rows), every 13th label ignored.
+
+The CPU oracle cannot run this shape in test time, so the reference is the
+row-chunked float32/float64 torch restatement (tests/torch_reference.py,
+pinned to the oracle at small sizes on the CPU) run on the same GPU.
+Tolerances as in tests/parity.py (loss terms 1e-4, bf16 gradients 2e-2).
+Size-independent properties of the INT8 result are checked besides: codes
+within ±127, every non-target row reaching ±127 at its largest element, and
+non-target rows of the returned grad_W equal to code x scale exactly.
+"""
+import pytest
+
+from parity import check_grad_device, check_scalar
+from torch_reference import loss_tied_chunked
+
+import orda_hip as H
+from orda_hip import KernelConfig, LossOptions, Teacher
+
+pytestmark = pytest.mark.gpu
+
+
+def test_tied_bf16_int8_full_benchmark_shape():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a visible GPU"
+    assert H.is_available(), "liborda_hip.so does not see a gfx950 device"
+    torch.backends.cuda.matmul.allow_tf32 = False
+    dev = torch.device("cuda:0")
+    bt, h, v = 8192, 4096, 131072
+    g = torch.Generator(device=dev)
+    g.manual_seed(20261201)
+    hs = torch.randn(bt, h, generator=g, device=dev).to(torch.bfloat16)
+    ht = torch.randn(bt, h, generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn(v, h, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    y = torch.randint(0, v, (bt,), generator=g, device=dev)
+    y[::13] = -100
+    opts = LossOptions(kd_weight=0.4, temperature=1.5, label_smoothing=0.1,
+                       config=KernelConfig(quantize_grad_weight=True))
+    got = H.distillation_loss(hs, w, y, Teacher.Tied(ht), opts, quant_codes=True)
+    assert (got.chunk_plan.chunk_size, got.chunk_plan.num_chunks) == (512, 16)
+
+    ref = loss_tied_chunked(hs, ht, w, y, kd=0.4, T=1.5, alpha=0.1)
+    rel = {}
+    for k in ("loss", "student_ce", "teacher_ce", "kl"):
+        check_scalar(k, getattr(got, k), ref[k])
+        rel[k] = abs(getattr(got, k) - ref[k]) / abs(ref[k])
+    rel["grad_student_hidden"] = check_grad_device(
+        "grad_student_hidden", got.grad_student_hidden, ref["grad_student_hidden"], "bf16")
+    rel["grad_teacher_hidden"] = check_grad_device(
+        "grad_teacher_hidden", got.grad_teacher_hidden, ref["grad_teacher_hidden"], "bf16")
+    rel["grad_weight"] = check_grad_device("grad_weight (dequantized)", got.grad_weight,
+                                           ref["grad_weight"], "bf16")
+    print("relative errors:", {k: f"{e:.2e}" for k, e in rel.items()})
+    del ref
+
+    codes, scales = got.quant_codes, got.quant_scales.reshape(-1)
+    target = torch.zeros(v, dtype=torch.bool, device=dev)
+    target[y[y != -100]] = True
+    other = ~target
+    assert int(codes.abs().max()) <= 127
+    assert bool((codes[other].abs().amax(1) == 127).all())
+    assert torch.equal(got.grad_weight[other], codes[other].float() * scales[other, None])

@@ -9,7 +9,7 @@ import pytest
 import oracle as O
 from helpers import labels, mat
 from orda_hip.types import LossOptions, Reduction, Teacher
-from torch_reference import loss_f64
+from torch_reference import loss_f64, loss_tied_chunked
 
 CASES = {
     # name: (mode, bt, h, ht, v, options, ignore_every)
@@ -64,6 +64,41 @@ def test_torch_reference_matches_oracle(name):
         assert (r is None) == (t is None), f"{k}: presence differs"
         if r is None:
             continue
+        r = np.asarray(r, np.float64)
+        err = np.linalg.norm(t - r) / max(np.linalg.norm(r), 1e-30)
+        assert err <= 1e-5, f"{k}: rel fro err {err:.3e}"
+
+
+@pytest.mark.parametrize("opts,rows", [
+    (dict(kd_weight=0.4, temperature=1.5, label_smoothing=0.1, teacher_ce_weight=1.0), 8),
+    (dict(kd_weight=0.4, temperature=1.5, label_smoothing=0.1, teacher_ce_weight=1.0), 1024),
+    (dict(kd_weight=0.7, temperature=0.5, teacher_ce_weight=0.5, reduction=Reduction.Sum), 5),
+    (dict(teacher_ce_weight=0.0), 16),
+])
+def test_chunked_tied_reference_matches_oracle(opts, rows):
+    """The row-chunked float32/float64 restatement used at the full benchmark
+    shape, against the oracle: loss terms to 1e-6, gradients to 1e-5
+    (float32 GEMMs in a different summation order)."""
+    import torch
+    bt, h, v = 37, 24, 300
+    s, th, w = mat(bt, h, 1, 0.5), mat(bt, h, 3, 0.5), mat(v, h, 2, 0.4)
+    y = labels(bt, v, 6)
+    o = LossOptions(**opts)
+    ref = O.distillation_loss(s, w, y, Teacher.Tied(th), o)
+    got = loss_tied_chunked(torch.from_numpy(s), torch.from_numpy(th), torch.from_numpy(w),
+                            torch.from_numpy(y), kd=o.kd_weight, T=o.temperature,
+                            alpha=o.label_smoothing, w_s=o.student_ce_weight,
+                            w_t=o.teacher_ce_weight if o.teacher_ce_weight is not None else 1.0,
+                            ignore=o.ignore_index, mean=o.reduction == Reduction.Mean, rows=rows)
+    for k in ("loss", "student_ce", "teacher_ce", "kl"):
+        r = getattr(ref, k)
+        assert abs(got[k] - r) <= 1e-6 * max(abs(r), 1e-2), f"{k}: chunked {got[k]!r} oracle {r!r}"
+    for k in ("grad_student_hidden", "grad_weight", "grad_teacher_hidden"):
+        r = getattr(ref, k)
+        assert (r is None) == (got[k] is None), f"{k}: presence differs"
+        if r is None:
+            continue
+        t = got[k].numpy().astype(np.float64)
         r = np.asarray(r, np.float64)
         err = np.linalg.norm(t - r) / max(np.linalg.norm(r), 1e-30)
         assert err <= 1e-5, f"{k}: rel fro err {err:.3e}"

@@ -7,6 +7,11 @@ teacher-detached forward KL at temperature T times T², src/reference/kl.rs:83-1
 weights and deferred mean, src/api.rs:211-230, 401-405) and the gradients come
 from torch autograd. Used to pin the torch autograd op: the CPU tests check it
 against the oracle, the GPU tests check the op's .grad values against it.
+
+`loss_tied_chunked` states the same Tied-teacher loss row-chunked with explicit
+gradients (float32 GEMMs, float64 row arithmetic), on any device: the
+full-size GPU test runs it on the GPU beside the library; the CPU tests pin it
+to the oracle at small sizes.
 """
 import numpy as np
 import torch
@@ -66,3 +71,79 @@ def loss_f64(hs, w, labels, mode, th=None, tw=None, tl=None, *, w_s=1.0, w_t=Non
         "grad_teacher_hidden": g(th_t, has_t),
         "grad_teacher_weight": g(tw_t, has_t and mode == "separate"),
     }
+
+
+def loss_tied_chunked(hs, ht, w, labels, *, kd, T, alpha, w_s=1.0, w_t=1.0, ignore=-100,
+                      mean=True, rows=1024):
+    """Tied teacher at any size, on the tensors' own device, `rows` rows at a
+    time: logits hs·Wᵀ and ht·Wᵀ as float32 GEMMs; log-sum-exp, losses and
+    dlogits in float64 (label-smoothed CE per row, src/reference/
+    cross_entropy.rs:27-73; teacher-detached KL at T, gradient kd·T·(p_s − p_t),
+    src/reference/kl.rs:83-124; KL merged into the student rows, src/api.rs:
+    336-344); the deferred mean as the float32 1/max(n_valid, 1) applied to
+    every gradient (src/api.rs:225-230, 381-388); backward GEMMs dlogits·W and
+    dlogitsᵀ·h in float32 (src/api.rs:346-361). Explicit gradients, no
+    autograd, so the full benchmark shape fits. Returns the loss terms as
+    floats and float32 gradient tensors."""
+    dev = hs.device
+    wf = w.float()
+    n, h = hs.shape
+    V = w.shape[0]
+    y = labels.to(dev)
+    valid = y != ignore
+    nv = int(valid.sum())
+    scale = float(np.float32(1.0) / np.float32(max(nv, 1))) if mean else 1.0
+    f32 = torch.float32
+    gs = torch.empty(n, h, dtype=f32, device=dev)
+    gt = torch.empty(n, h, dtype=f32, device=dev) if w_t > 0 else None
+    gw = torch.zeros(V, h, dtype=f32, device=dev)
+    sums = {"s": 0.0, "t": 0.0, "kl": 0.0}
+
+    def ce(x, vm, ys, idx):
+        xd = x.double()
+        lse = torch.logsumexp(xd, 1)
+        nll = lse - xd[idx, ys]
+        if alpha > 0:
+            nll = lse - (1 - alpha) * xd[idx, ys] - (alpha / V) * xd.sum(1)
+        g = torch.exp(xd - lse[:, None])
+        if alpha > 0:
+            g -= alpha / V
+        g[idx, ys] -= 1 - alpha
+        g[~vm] = 0
+        return float(torch.where(vm, nll, torch.zeros_like(nll)).sum()), g
+
+    for r0 in range(0, n, rows):
+        r1 = min(r0 + rows, n)
+        hs_c, ht_c = hs[r0:r1].float(), ht[r0:r1].float()
+        vm = valid[r0:r1]
+        ys = torch.where(vm, y[r0:r1], torch.zeros_like(y[r0:r1]))
+        idx = torch.arange(r1 - r0, device=dev)
+        ls, lt = hs_c @ wf.T, ht_c @ wf.T
+        nll, ds = ce(ls, vm, ys, idx)
+        sums["s"] += nll
+        ds *= w_s
+        if kd > 0:
+            lps = torch.log_softmax(ls.double() / T, 1)
+            lpt = torch.log_softmax(lt.double() / T, 1)
+            pt = lpt.exp()
+            kl = (pt * (lpt - lps)).sum(1) * (T * T)
+            sums["kl"] += float(torch.where(vm, kl, torch.zeros_like(kl)).sum())
+            gk = kd * T * (lps.exp() - pt)
+            gk[~vm] = 0
+            ds += gk
+            del lps, lpt, pt, gk
+        dsf = (ds * scale).to(f32)
+        del ds
+        gs[r0:r1] = dsf @ wf
+        gw += dsf.T @ hs_c
+        if w_t > 0:
+            nll, dt = ce(lt, vm, ys, idx)
+            sums["t"] += nll
+            dtf = (dt * (w_t * scale)).to(f32)
+            del dt
+            gt[r0:r1] = dtf @ wf
+            gw += dtf.T @ ht_c
+    loss = (w_s * sums["s"] + w_t * sums["t"] + kd * sums["kl"]) * scale
+    return {"loss": loss, "student_ce": sums["s"] * scale, "teacher_ce": sums["t"] * scale,
+            "kl": sums["kl"] * scale, "grad_student_hidden": gs, "grad_weight": gw,
+            "grad_teacher_hidden": gt}
