@@ -19,6 +19,7 @@ namespace orda {
 namespace {
 
 constexpr int kThreads = 256;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr uint64_t kGamma = 0x9E3779B97F4A7C15ull;
 
 __device__ __forceinline__ uint64_t splitmix_mix(uint64_t z) {
@@ -104,7 +105,13 @@ __global__ __launch_bounds__(kThreads) void quant_vec_kernel(QuantArgs a) {
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int c = (tid + k * kThreads) * 4;
-    x[k] = c < cols ? *reinterpret_cast<const float4*>(src + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    // grad_W streams through once: non-temporal loads and stores
+    if (c < cols) {
+      const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + c));
+      x[k] = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      x[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     amax = fmaxf(amax, fmaxf(fmaxf(fabsf(x[k].x), fabsf(x[k].y)), fmaxf(fabsf(x[k].z), fabsf(x[k].w))));
   }
 #pragma unroll
@@ -130,13 +137,13 @@ __global__ __launch_bounds__(kThreads) void quant_vec_kernel(QuantArgs a) {
     o.y = quant_one(a, x[k].y, s, keep, ebase + c + 1, c1);
     o.z = quant_one(a, x[k].z, s, keep, ebase + c + 2, c2);
     o.w = quant_one(a, x[k].w, s, keep, ebase + c + 3, c3);
-    if (write) *reinterpret_cast<float4*>(dst + c) = o;
+    if (write) __builtin_nontemporal_store(f32x4{o.x, o.y, o.z, o.w}, reinterpret_cast<f32x4*>(dst + c));
     if (q) {
       const uint32_t packed = static_cast<uint32_t>(static_cast<uint8_t>(c0)) |
                               (static_cast<uint32_t>(static_cast<uint8_t>(c1)) << 8) |
                               (static_cast<uint32_t>(static_cast<uint8_t>(c2)) << 16) |
                               (static_cast<uint32_t>(static_cast<uint8_t>(c3)) << 24);
-      *reinterpret_cast<uint32_t*>(q + c) = packed;
+      __builtin_nontemporal_store(packed, reinterpret_cast<uint32_t*>(q + c));
     }
   }
   if (a.scales && tid == 0) a.scales[r] = s;

@@ -294,6 +294,13 @@ template <>
 __device__ __forceinline__ void store8(__bf16* p, const float (&g)[8]) {
   *reinterpret_cast<u32x4*>(p) = Vec<__bf16>::pack(g);
 }
+// Streaming forms for data touched once (non-temporal hint on the access).
+__device__ __forceinline__ void load8_nt(const __bf16* p, float (&x)[8]) {
+  Vec<__bf16>::unpack(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)), x);
+}
+__device__ __forceinline__ void store8_nt(__bf16* p, const float (&g)[8]) {
+  __builtin_nontemporal_store(Vec<__bf16>::pack(g), reinterpret_cast<u32x4*>(p));
+}
 
 // The row pass of distillation_loss, specialised on the logits type LT, the
 // gradient type GT and whether the KL term (KL) and the teacher CE gradient
@@ -563,8 +570,8 @@ __global__ __launch_bounds__(kThreads) void row_grad_kernel(RowPassArgs a, int64
     for (int q = 0; q < kChunkVec; ++q) {
       const int64_t j = c0 + (static_cast<int64_t>(q) * kThreads + tid) * NV;
       if (j < v) {
-        store8(srow + j, z);
-        if (TG) store8(trow + j, z);
+        store8_nt(srow + j, z);
+        if (TG) store8_nt(trow + j, z);
       }
     }
     return;
@@ -593,8 +600,8 @@ __global__ __launch_bounds__(kThreads) void row_grad_kernel(RowPassArgs a, int64
   for (int q = 0; q < kChunkVec; ++q) {
     const int64_t j = c0 + (static_cast<int64_t>(q) * kThreads + tid) * NV;
     if (j < v) {
-      load8(srow + j, xs[q]);
-      if (KL || TG) load8(trow + j, xt[q]);
+      load8_nt(srow + j, xs[q]);
+      if (KL || TG) load8_nt(trow + j, xt[q]);
     }
   }
 #pragma unroll
@@ -610,8 +617,8 @@ __global__ __launch_bounds__(kThreads) void row_grad_kernel(RowPassArgs a, int64
       g[i] = valid ? gi : 0.f;
       gt[i] = valid ? ti : 0.f;
     }
-    store8(srow + j, g);
-    if (TG) store8(trow + j, gt);
+    store8_nt(srow + j, g);
+    if (TG) store8_nt(trow + j, gt);
   }
   if (owner) {   // the label term, after this thread's own store of that column
     float gy = 0.f, ty = 0.f;
