@@ -152,7 +152,8 @@ int64_t orda_chunk_doubling_schedule(int64_t bt, int64_t start, int64_t limit, i
 /* ---- context -------------------------------------------------------------- */
 int32_t orda_ctx_create(int32_t device, orda_ctx **out, char *err, size_t err_len);
 void orda_ctx_destroy(orda_ctx *ctx);
-/* Run on a caller-owned hipStream_t (NULL: the context's own stream). */
+/* Run on a caller-owned hipStream_t (NULL: the context's own stream, a
+ * blocking stream, so it is ordered after work queued on the null stream). */
 int32_t orda_ctx_set_stream(orda_ctx *ctx, void *hip_stream);
 /* Upper bound, in bytes, on device memory the context may hold (workspace
  * and staging). 0 = no bound. Allocations past it fail like a device OOM,

@@ -1011,7 +1011,10 @@ int32_t orda_ctx_create(int32_t device, orda_ctx** out, char* err, size_t err_le
     std::unique_ptr<orda_ctx> c(new orda_ctx());
     c->device = device;
     hip_check(hipSetDevice(device), "hipSetDevice");
-    hip_check(hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking), "hipStreamCreate");
+    // A blocking stream: it waits for work the caller queued on the legacy
+    // null stream (torch's default stream, whose handle is NULL) before it
+    // reads the inputs, and the null stream waits for it in turn.
+    hip_check(hipStreamCreateWithFlags(&c->own, hipStreamDefault), "hipStreamCreate");
     c->stream = c->own;
     *out = c.release();
     return ORDA_OK;

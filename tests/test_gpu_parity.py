@@ -274,6 +274,31 @@ def test_all_labels_ignored(torch_dev):
     assert got.loss == 0.0 and np.all(to_np(got.grad_weight) == 0.0)
 
 
+def test_inputs_from_pending_default_stream_work(torch_dev):
+    """Inputs whose producing kernels are still queued on torch's default
+    stream (the null stream, handle NULL) when the call starts. The call runs
+    on the context's own stream, which must be ordered after them: the labels
+    are read back for validation and every input is read by the kernels."""
+    torch, dev = torch_dev
+    assert torch.cuda.current_stream(dev).cuda_stream == 0
+    bt, h, v = 256, 64, 1000
+    s, th = normal((bt, h), 151), normal((bt, h), 152)
+    w = normal((v, h), 153, 0.05)
+    y = uniform_labels(bt, v, 154)
+    y[::9] = -100
+    # ~60 ms of queued work ending in an exact zero that every input depends on
+    a = torch.full((4096, 4096), 1e-3, device=dev)
+    for _ in range(40):
+        a = torch.tanh(a @ a)
+    zf = a[0, 0] * 0.0
+    zi = zf.to(torch.int64)
+    opts = base_opts(teacher_ce_weight=1.0, label_smoothing=0.1, chunk_size=ChunkSize.Fixed(64))
+    got = H.distillation_loss(gpu(torch_dev, s) + zf, gpu(torch_dev, w) + zf,
+                              gpu(torch_dev, y) + zi, Teacher.Tied(gpu(torch_dev, th) + zf), opts)
+    ref = O.distillation_loss(s, w, y, Teacher.Tied(th), opts)
+    check_output(got, ref)
+
+
 # ------------------------------------------------ entry points and host logic
 @pytest.mark.parametrize("stochastic", [False, True])
 @pytest.mark.parametrize("cols", [257, 256, 1000, 4096, 8192])
