@@ -11,6 +11,7 @@ include/orda/orda.h; torch tensors (or numpy arrays) carry the memory.
 from __future__ import annotations
 
 import ctypes as C
+import threading
 from typing import Any, Optional
 
 import numpy as np
@@ -215,13 +216,20 @@ class Context:
         return ms.value, n.value
 
 
-_default_ctx = {}
+_default_ctx = threading.local()
 
 
 def default_context(device: int = 0) -> Context:
-    if device not in _default_ctx:
-        _default_ctx[device] = Context(device)
-    return _default_ctx[device]
+    """The calling thread's context for `device`. A context's workspace
+    and stream serve one call at a time, and ctypes releases the GIL during
+    the call, so every thread gets its own (the C ABI's one context per
+    caller thread)."""
+    per_thread = getattr(_default_ctx, "by_device", None)
+    if per_thread is None:
+        per_thread = _default_ctx.by_device = {}
+    if device not in per_thread:
+        per_thread[device] = Context(device)
+    return per_thread[device]
 
 
 def _options_c(o: LossOptions) -> LossOptionsC:

@@ -299,6 +299,47 @@ def test_inputs_from_pending_default_stream_work(torch_dev):
     check_output(got, ref)
 
 
+def test_concurrent_calls_from_two_threads(torch_dev):
+    """Two Python threads in the library at once (ctypes releases the GIL
+    for the call): each thread's default context has its own stream and
+    workspace, and every result matches the oracle."""
+    import threading
+    torch, dev = torch_dev
+    cases = []
+    for k in range(2):
+        bt, h, v = 192 + 64 * k, 64, 1500 + 500 * k
+        cases.append((normal((bt, h), 160 + k), normal((bt, h), 170 + k),
+                      normal((v, h), 180 + k, 0.05), uniform_labels(bt, v, 190 + k)))
+    opts = base_opts(teacher_ce_weight=1.0, label_smoothing=0.1, chunk_size=ChunkSize.Fixed(64))
+    got, errors = [None, None], []
+    start = threading.Barrier(2)
+
+    def run(k):
+        try:
+            s, th, w, y = cases[k]
+            args = (gpu(torch_dev, s), gpu(torch_dev, w), gpu(torch_dev, y),
+                    Teacher.Tied(gpu(torch_dev, th)))
+            torch.cuda.synchronize()
+            start.wait()
+            outs = [H.distillation_loss(*args, opts) for _ in range(5)]
+            got[k] = (outs, H.default_context(0))
+        except BaseException as e:   # reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(k,)) for k in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    assert got[0][1] is not got[1][1] and got[0][1] is not H.default_context(0)
+    for k in range(2):
+        s, th, w, y = cases[k]
+        ref = O.distillation_loss(s, w, y, Teacher.Tied(th), opts)
+        for out in got[k][0]:
+            check_output(out, ref)
+
+
 # ------------------------------------------------ entry points and host logic
 @pytest.mark.parametrize("stochastic", [False, True])
 @pytest.mark.parametrize("cols", [257, 256, 1000, 4096, 8192])
