@@ -220,7 +220,8 @@ def summarize(dirs, copy_bytes, timed_steps=0):
     import glob
     from collections import defaultdict
     stats = defaultdict(lambda: [0, 0.0])           # kind -> [calls, total ns]
-    counters = defaultdict(lambda: defaultdict(list))   # counter -> kind -> [KiB per dispatch]
+    counters = defaultdict(lambda: defaultdict(list))   # counter -> kind -> [value per dispatch]
+    spans = defaultdict(dict)                       # kind -> {dispatch id: duration ns}
     trace = defaultdict(list)                       # kind -> [(start ns, duration ns)]
     for d in dirs:
         for f in glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True):
@@ -240,6 +241,7 @@ def summarize(dirs, copy_bytes, timed_steps=0):
                 k = kernel_kind(r["Kernel_Name"])
                 if k:
                     counters[r["Counter_Name"]][k].append(float(r["Counter_Value"]))
+                    spans[k][r["Dispatch_Id"]] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
     out = []
     if stats:
         # Steps are counted by the logits GEMM (one launch per group and step);
@@ -259,8 +261,26 @@ def summarize(dirs, copy_bytes, timed_steps=0):
                 last = durs[-timed_steps * per_step:] if durs else []
                 line += f" {sum(last) / len(last) / 1e6:.4f} |" if last else " - |"
             out.append(line)
+    if "GRBM_GUI_ACTIVE" in counters and "SQ_VALU_MFMA_BUSY_CYCLES" in counters:
+        # MI355X: 8 XCDs (GRBM_GUI_ACTIVE is summed over them) and 256 CUs x 4
+        # SIMDs (the MFMA busy cycles are summed over the 1024 SIMDs).
+        out.append("")
+        out.append("| kernel | dispatches | duration (ms) | cycles per XCD | shader clock (GHz) | "
+                   "MFMA busy cycles per SIMD | MFMA busy / elapsed cycles |")
+        out.append("|---|---|---|---|---|---|---|")
+        for k in sorted(counters["SQ_VALU_MFMA_BUSY_CYCLES"]):
+            busy = counters["SQ_VALU_MFMA_BUSY_CYCLES"][k]
+            grbm = counters["GRBM_GUI_ACTIVE"].get(k, [])
+            if not grbm or max(busy) <= 0:
+                continue
+            n = len(grbm)
+            cyc = sum(grbm) / n / 8
+            dur = sum(spans[k].values()) / max(len(spans[k]), 1)
+            simd = sum(busy) / len(busy) / 1024
+            out.append(f"| {k} | {n} | {dur / 1e6:.3f} | {cyc:.4g} | {cyc / dur:.3f} | "
+                       f"{simd:.4g} | {simd / cyc:.3f} |")
     traffic = {}
-    if counters:
+    if "FETCH_SIZE" in counters or "WRITE_SIZE" in counters:
         factors = {}
         for c in ("FETCH_SIZE", "WRITE_SIZE"):
             cp = counters.get(c, {}).get("copy")

@@ -767,8 +767,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         constexpr int SN = (S + 1) % kRing;          // stage s+1 % 4
         constexpr bool kOdd = (S & 1) != 0;
         constexpr int kDma = kOdd ? 12 : 4;
-        constexpr int kSide = kReads + kDma;
-        constexpr int kPairDma = (kReads * 32) / kSide;   // first MFMA pair carrying a DMA
+        constexpr int kSide = kReads + kDma;   // reads keep the slots of a kSide spread
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(kOdd ? vm_wait(4) : vm_wait(16));
         __builtin_amdgcn_s_barrier();
@@ -776,28 +775,22 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         uint64_t sa = 0, sb = 0;
 #pragma unroll
         for (int pr = 0; pr < 32; ++pr) {
-          if (pr == kPairDma - 2) {
-            // DMA sources (B stage s+4, A pair s/2 + 2), computed here so the
-            // scalar work overlaps MFMAs.
-            const int nb = st + kRing < ns ? st + kRing : 0;
-            sb = uniform64(lb.stage_src(nb));
-            if constexpr (kOdd) {
-              const int p = (st >> 1) + 2;
-              sa = uniform64(pa.src(p < np ? p : np - 1));
-            }
-          }
+          // The slots the DMAs fill were freed by the barrier above. B's
+          // transfers go out with MFMA pairs 1-4 and A's with pairs 14-21
+          // (the order B then A keeps the vmcnt counts above). Measured
+          // against the earlier placement after all reads (pairs 21-31):
+          // A from pair 14 or 15 runs 3.5-4.5 % faster; A from pairs 5-12
+          // runs up to 9 % slower.
+          constexpr int kB0 = 1, kA0 = 14;   // first MFMA pair of B's / A's transfers
+          if (pr >= kB0 && pr < kB0 + 4) dma_b(SlotC<S>{}, pr - kB0, sb);
+          if (kOdd && pr >= kA0 && pr < kA0 + 8) dma_a(SlotC<(S >> 1)>{}, pr - kA0, sa);
 #pragma unroll
-          for (int o = 0; o < kSide; ++o) {
+          for (int o = 0; o < kReads; ++o) {
             if ((o * 32) / kSide != pr) continue;
-            if (o < kOpsA) {
+            if (o < kOpsA)
               fa.template read_op<SN>(o, rnA);
-            } else if (o < kReads) {
+            else
               fb.template read_op<SN>(o - kOpsA, rnB);
-            } else if (o < kReads + 4) {
-              dma_b(SlotC<S>{}, o - kReads, sb);
-            } else {
-              dma_a(SlotC<(S >> 1)>{}, o - kReads - 4, sa);
-            }
           }
 #pragma unroll
           for (int q = 0; q < 2; ++q) {
@@ -806,6 +799,16 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
               mfma_bf16(acc[mm >> 3][mm & 7], rcB[mm & 7], rcA[mm >> 3]);
             else
               mfma_bf16(acc[mm >> 3][mm & 7], rcA[mm >> 3], rcB[mm & 7]);
+          }
+          if (pr == 0) {
+            // DMA sources (B stage s+4, A pair s/2 + 2), computed behind the
+            // first MFMAs.
+            const int nb = st + kRing < ns ? st + kRing : 0;
+            sb = uniform64(lb.stage_src(nb));
+            if constexpr (kOdd) {
+              const int p = (st >> 1) + 2;
+              sa = uniform64(pa.src(p < np ? p : np - 1));
+            }
           }
           __builtin_amdgcn_sched_barrier(0);
         }
