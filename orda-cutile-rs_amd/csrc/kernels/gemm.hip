@@ -555,15 +555,16 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       //
       // Iteration s computes stage s from registers and reads stage s+1's
       // fragments into the other register set. An even iteration s reads
-      // first; at its middle barrier every wave has finished reading stages s
-      // and s+1 (the latter just now, with an LDS wait before the barrier),
-      // so their double slot is free and the DMA of pair s/2 + 2 into it
-      // follows. An odd iteration s starts by waiting for its own DMAs of pair
-      // (s+1)/2 (the newer pair stays in flight) and a barrier, after which
-      // every wave's share of that pair has landed. Each pair thus has 2.5
-      // iterations to land and up to two pairs are in flight. Past the last
-      // pair the DMA re-reads the last pair into a double slot nobody reads
-      // again, so the wait counts stay exact.
+      // first, all in its first MFMA pairs; at its barrier (MFMA pair kMid)
+      // every wave has finished reading stages s and s+1 (the latter just
+      // now, with an LDS wait before the barrier), so their double slot is
+      // free and the DMA of pair s/2 + 2 into it follows, spread over the
+      // rest of the iteration. An odd iteration s starts by waiting for its
+      // own DMAs of pair (s+1)/2 (the newer pair stays in flight) and a
+      // barrier, after which every wave's share of that pair has landed. Each
+      // pair thus has nearly three iterations to land and up to two pairs are
+      // in flight. Past the last pair the DMA re-reads the last pair into a
+      // double slot nobody reads again, so the wait counts stay exact.
       //
       // With one wave per SIMD nothing else fills the matrix pipe, so the side
       // operations ride between the MFMAs (64 per stage, issued as 32 pairs).
@@ -619,7 +620,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       }
       constexpr int kOpsA = FragReader<AK, AK>::kOps, kOpsB = FragReader<BK, kPaired>::kOps;
       constexpr int kReads = kOpsA + kOpsB;
-      constexpr int kMid = 16;   // MFMA pair of an even iteration's barrier
+      // MFMA pair of an even iteration's barrier. The earlier the barrier,
+      // the longer the next pair has to land: measured 13.4 ms at pair 22,
+      // 13.1 ms at 16, 12.8 ms at 10, 12.7 ms at 6 and 12.8 ms at 4.
+      constexpr int kMid = 6;
       auto iter = [&](auto slot_c, int st, u32x4 (&rnA)[kFrag], u32x4 (&rnB)[kFrag],
                       const u32x4 (&rcA)[kFrag], const u32x4 (&rcB)[kFrag]) {
         constexpr int S = decltype(slot_c)::value;   // stage s % 4
@@ -660,7 +664,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
               fb.template read_op<SN>(o - kOpsA, rnB);
           }
           if constexpr (!kOdd) {
-            if (pr >= kMid) dma_op(SlotC<(S >> 1)>{}, pr - kMid, sa, sb);
+            // the pair's 16 transfers, spread over the pairs after the barrier
+#pragma unroll
+            for (int x = 0; x < 16; ++x)
+              if (kMid + (x * (32 - kMid)) / 16 == pr) dma_op(SlotC<(S >> 1)>{}, x, sa, sb);
           }
   #pragma unroll
           for (int q = 0; q < 2; ++q) {
