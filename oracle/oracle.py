@@ -19,7 +19,9 @@ from types import SimpleNamespace
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liborda_oracle.so")
+# ORDA_ORACLE_LIB selects another build of the same source (the Makefile's
+# `asan` target builds one with AddressSanitizer).
+_LIB_PATH = os.environ.get("ORDA_ORACLE_LIB", os.path.join(_HERE, "liborda_oracle.so"))
 
 _f32p = C.POINTER(C.c_float)
 _f64p = C.POINTER(C.c_double)
