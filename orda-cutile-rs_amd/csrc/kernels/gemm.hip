@@ -624,6 +624,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       // the longer the next pair has to land: measured 13.4 ms at pair 22,
       // 13.1 ms at 16, 12.8 ms at 10, 12.7 ms at 6 and 12.8 ms at 4.
       constexpr int kMid = 6;
+      // MFMA pairs the pair's 16 transfers spread over: all the rest of the
+      // iteration (over 16 pairs measured 4 % slower, over 8 pairs 8 %).
+      constexpr int kSpan = 32 - kMid;
       auto iter = [&](auto slot_c, int st, u32x4 (&rnA)[kFrag], u32x4 (&rnB)[kFrag],
                       const u32x4 (&rcA)[kFrag], const u32x4 (&rcB)[kFrag]) {
         constexpr int S = decltype(slot_c)::value;   // stage s % 4
@@ -667,7 +670,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
             // the pair's 16 transfers, spread over the pairs after the barrier
 #pragma unroll
             for (int x = 0; x < 16; ++x)
-              if (kMid + (x * (32 - kMid)) / 16 == pr) dma_op(SlotC<(S >> 1)>{}, x, sa, sb);
+              if (kMid + (x * kSpan) / 16 == pr) dma_op(SlotC<(S >> 1)>{}, x, sa, sb);
           }
   #pragma unroll
           for (int q = 0; q < 2; ++q) {
@@ -783,14 +786,17 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
 #pragma unroll
         for (int pr = 0; pr < 32; ++pr) {
           // The slots the DMAs fill were freed by the barrier above. B's
-          // transfers go out with MFMA pairs 1-4 and A's with pairs 14-21
-          // (the order B then A keeps the vmcnt counts above). Measured
-          // against the earlier placement after all reads (pairs 21-31):
-          // A from pair 14 or 15 runs 3.5-4.5 % faster; A from pairs 5-12
-          // runs up to 9 % slower.
+          // transfers go out with MFMA pairs 1-4 and A's with every other
+          // pair from 14 to 28 (the order B then A keeps the vmcnt counts
+          // above). Measured against the earlier placement after all reads
+          // (pairs 21-31): A from pair 14 or 15 runs 3.5-4.5 % faster, and
+          // every other pair a further 0.7 %; A from pairs 5-12 runs up to
+          // 9 % slower.
           constexpr int kB0 = 1, kA0 = 14;   // first MFMA pair of B's / A's transfers
+          constexpr int kAS = 2;             // MFMA pairs between A's transfers
           if (pr >= kB0 && pr < kB0 + 4) dma_b(SlotC<S>{}, pr - kB0, sb);
-          if (kOdd && pr >= kA0 && pr < kA0 + 8) dma_a(SlotC<(S >> 1)>{}, pr - kA0, sa);
+          if (kOdd && pr >= kA0 && pr < kA0 + 8 * kAS && (pr - kA0) % kAS == 0)
+            dma_a(SlotC<(S >> 1)>{}, (pr - kA0) / kAS, sa);
 #pragma unroll
           for (int o = 0; o < kReads; ++o) {
             if ((o * 32) / kSide != pr) continue;
