@@ -506,6 +506,20 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
     pr.c = static_cast<float*>(pr.c) + static_cast<int64_t>(split) * g.split_stride;
   }
 
+  // Logits: this thread's tile-row label, loaded now so that it has long
+  // landed when the epilogue needs it (tile row -> student row as in the
+  // epilogue's out_row). A global (not flat) load: a flat load would also
+  // count in lgkmcnt and turn the main loop's LDS waits into lgkmcnt(0).
+  int64_t lab_pre = 0;
+  if constexpr (EPI == GemmEpilogue::Logits) {
+    typedef __attribute__((address_space(1))) const int64_t global_i64;
+    const int64_t R = static_cast<int64_t>(tc.m0) + tid;
+    const int64_t prs = g.lg.pair_rows;
+    const int64_t r = prs > 0 ? ((R >> 5) << 4) + (R & 15) : R;
+    const bool ok = prs > 0 ? r < prs : R < g.M;
+    lab_pre = ok ? *(global_i64*)(reinterpret_cast<uintptr_t>(g.lg.labels + r)) : g.lg.ignore_index;
+  }
+
   f32x4 acc[kFrag][kFrag];
 #pragma unroll
   for (int i = 0; i < kFrag; ++i)
@@ -1087,12 +1101,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       valid = tc.m0 + rl < g.M;
       return static_cast<int64_t>(tc.p) * g.M + tc.m0 + rl;
     };
-    {
-      bool t, ok;
-      const int64_t o = out_row(tid, t, ok);
-      const int64_t r = prs > 0 ? (t ? o - prs : o) : tc.m0 + tid;
-      lab[tid] = ok ? g.lg.labels[r] : g.lg.ignore_index;
-    }
+    lab[tid] = lab_pre;
     __syncthreads();
     const float it2 = g.lg.inv_t * kLog2e;
     const int64_t colw = static_cast<int64_t>(tc.n0) + wn * 128 + 4 * lgrp;   // (j, e) = (0, 0)
