@@ -410,6 +410,21 @@ __device__ __forceinline__ f32x4 from_acc(const f32x4& a) {
   return f32x4{x, y, z, w};
 }
 __device__ __forceinline__ void mfma_prime() { asm volatile("s_nop 7"); }
+// max(a, b, c) in one instruction. fmaxf on values that come out of inline
+// asm (from_acc) first canonicalises each operand, one more op per value.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// Maximum of a lane's 32 values of one row (all columns valid): 16 v_max3.
+__device__ __forceinline__ float row_max32(const f32x4 (&v)[8]) {
+  float m = max3f(v[0][0], v[0][1], v[0][2]);
+  m = max3f(m, v[0][3], v[1][0]);
+#pragma unroll
+  for (int k = 5; k < 31; k += 2) m = max3f(m, v[k >> 2][k & 3], v[(k + 1) >> 2][(k + 1) & 3]);
+  return max3f(m, v[7][3], v[7][3]);
+}
 
 // One stage of MFMAs: acc[i][j] += A-fragment i x B-fragment j. With SWAP the
 // operands enter the MFMA the other way round, so acc[i][j] holds the
@@ -1191,21 +1206,26 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         const int64_t yl64 = lab[rl] - colw;
         const int yl = (yl64 >= 0 && yl64 < 128) ? static_cast<int>(yl64) : -1;
         float mx = -INFINITY;
+        if constexpr (kFull) {
+          mx = row_max32(av);
+        } else {
 #pragma unroll
-        for (int j = 0; j < kFrag; ++j)
+          for (int j = 0; j < kFrag; ++j)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (kFull || j * 16 + e < ncol) mx = fmaxf(mx, av[j][e]);
+            for (int e = 0; e < 4; ++e)
+              if (j * 16 + e < ncol) mx = fmaxf(mx, av[j][e]);
+        }
         mx = quad_max(mx);
+        // exp((x - mx)) and exp((x - mx)/T) as exp2 of one fma each.
+        const float o1 = -mx * kLog2e, oT = -mx * it2;
         float d1 = 0.f, dT = 0.f, sx = 0.f;
 #pragma unroll
         for (int j = 0; j < kFrag; ++j) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float x = av[j][e];
-            const float dx = x - mx;
-            const float a1 = __builtin_amdgcn_exp2f(dx * kLog2e);
-            const float aT = __builtin_amdgcn_exp2f(dx * it2);
+            const float a1 = __builtin_amdgcn_exp2f(fmaf(x, kLog2e, o1));
+            const float aT = __builtin_amdgcn_exp2f(fmaf(x, it2, oT));
             if (kFull || j * 16 + e < ncol) {
               d1 += a1;
               dT += aT;
@@ -1214,7 +1234,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
           }
         }
         const bool hit = yl >= 0 && (yl & 12) == 0;
-        const float xy = pick(av, yl);
         d1 = quad_sum(d1);
         dT = quad_sum(dT);
         sx = quad_sum(sx);
@@ -1222,7 +1241,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         u32x4 aw[kFrag / 2];
         if constexpr (kSwapStore && kFull) swap_rows(av, aw);
         if (row < g.M) {
-          if (hit) g.lg.xy[tc.p * g.M + row] = xy;
+          if (hit) g.lg.xy[tc.p * g.M + row] = pick(av, yl);
           if constexpr (kSwapStore && kFull)
             store_swapped(C + row * g.ldc + (colw - 4 * lgrp), aw);
           else
@@ -1245,27 +1264,33 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         const int64_t yl64 = lab[rs] - colw;
         const int yl = (yl64 >= 0 && yl64 < 128) ? static_cast<int>(yl64) : -1;
         float ms = -INFINITY, mt = -INFINITY;
+        if constexpr (kFull) {
+          ms = row_max32(as);
+          mt = row_max32(at);
+        } else {
 #pragma unroll
-        for (int j = 0; j < kFrag; ++j)
+          for (int j = 0; j < kFrag; ++j)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (kFull || j * 16 + e < ncol) {
-              ms = fmaxf(ms, as[j][e]);
-              mt = fmaxf(mt, at[j][e]);
-            }
+            for (int e = 0; e < 4; ++e)
+              if (j * 16 + e < ncol) {
+                ms = fmaxf(ms, as[j][e]);
+                mt = fmaxf(mt, at[j][e]);
+              }
+        }
         ms = quad_max(ms);
         mt = quad_max(mt);
+        const float o1s = -ms * kLog2e, oTs = -ms * it2;
+        const float o1t = -mt * kLog2e, oTt = -mt * it2;
         float d1s = 0.f, dTs = 0.f, sxs = 0.f, d1t = 0.f, dTt = 0.f, sxt = 0.f, cx = 0.f;
 #pragma unroll
         for (int j = 0; j < kFrag; ++j) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float xs = as[j][e], xt = at[j][e];
-            const float dxs = xs - ms, dxt = xt - mt;
-            const float a1s = __builtin_amdgcn_exp2f(dxs * kLog2e);
-            const float aTs = __builtin_amdgcn_exp2f(dxs * it2);
-            const float a1t = __builtin_amdgcn_exp2f(dxt * kLog2e);
-            const float aTt = __builtin_amdgcn_exp2f(dxt * it2);
+            const float a1s = __builtin_amdgcn_exp2f(fmaf(xs, kLog2e, o1s));
+            const float aTs = __builtin_amdgcn_exp2f(fmaf(xs, it2, oTs));
+            const float a1t = __builtin_amdgcn_exp2f(fmaf(xt, kLog2e, o1t));
+            const float aTt = __builtin_amdgcn_exp2f(fmaf(xt, it2, oTt));
             if (kFull || j * 16 + e < ncol) {
               d1s += a1s;
               dTs += aTs;
@@ -1278,7 +1303,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
           }
         }
         const bool hit = yl >= 0 && (yl & 12) == 0;
-        const float xys = pick(as, yl), xyt = pick(at, yl);
         d1s = quad_sum(d1s);
         dTs = quad_sum(dTs);
         sxs = quad_sum(sxs);
@@ -1297,9 +1321,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
           swap_rows(at, tw);
         }
         if (row < prs) {
-          if (hit) {
-            g.lg.xy[row] = xys;
-            g.lg.xy[prs + row] = xyt;
+          if (hit) {   // one lane of a row at most, for one column tile
+            g.lg.xy[row] = pick(as, yl);
+            g.lg.xy[prs + row] = pick(at, yl);
           }
           if constexpr (kSwapStore && kFull) {
             store_swapped(C + row * g.ldc + (colw - 4 * lgrp), sw);
