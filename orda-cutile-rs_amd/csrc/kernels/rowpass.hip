@@ -663,13 +663,16 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(FinalizeArgs a) {
     t_nll += static_cast<double>(a.row_nll_t[i]);
   }
   // KL is accumulated per chunk and rounded to f32 (api.rs:304-314 with
-  // kl.rs:126).
+  // kl.rs:126): one wave per chunk, lane partials summed across the wave.
   const int64_t nc = (a.bt + a.chunk_size - 1) / a.chunk_size;
-  for (int64_t c = threadIdx.x; c < nc; c += kThreads) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t c = threadIdx.x >> 6; c < nc; c += kThreads / 64) {
     const int64_t e = (c + 1) * a.chunk_size < a.bt ? (c + 1) * a.chunk_size : a.bt;
     double k = 0.0;
-    for (int64_t i = c * a.chunk_size; i < e; ++i) k += static_cast<double>(a.row_kl[i]);
-    kl += static_cast<double>(static_cast<float>(k));
+    for (int64_t i = c * a.chunk_size + lane; i < e; i += 64) k += static_cast<double>(a.row_kl[i]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) k += __shfl_xor(k, o);
+    if (lane == 0) kl += static_cast<double>(static_cast<float>(k));
   }
   red[0][threadIdx.x] = s_nll;
   red[1][threadIdx.x] = t_nll;
