@@ -395,7 +395,7 @@ int64_t staged_bytes_per_row(const LossPlan& P, const Inputs& in) {
   int64_t b = blocks * logits_pitch(P.v) *
               (orda::dtype_size(lt) + (lt == P.dt ? 0 : orda::dtype_size(P.dt)));
   b += 2 * nst * 16 + 2 * 4;   // statistics, label logits
-  if (paired) b += nst * 4 + 2 * round8(P.h) * 2 + 16;   // cross partials, paired rows, row constants
+  if (paired) b += nst * 4 + 16;   // cross partials, row constants
   return b;
 }
 
@@ -445,8 +445,6 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   float* rkl = row3_out + 2 * bt;
   const int64_t ldh_cat = round8(h);
   void* hcat = tied_tce ? ws(c, "hcat", 2 * cap * ldh_cat * es) : nullptr;
-  const int64_t cap16 = (cap + 15) / 16 * 16;
-  void* hpair = paired ? ws(c, "hpair", 2 * cap16 * ldh_cat * es) : nullptr;
   float* cross = paired ? static_cast<float*>(ws(c, "cross", cap * nst * 4)) : nullptr;
   float4* rconst = paired ? static_cast<float4*>(ws(c, "rconst", cap * 16)) : nullptr;
   const float inv_t = 1.0f / P.T;
@@ -493,16 +491,12 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
     f.prob[0] = {at(in.hs.p, gs * in.hs.ld, dt), in.W.p, Ls};
     const bool fuse_t = P.need_teacher && P.mode == ORDA_TEACHER_TIED && in.th.ld == in.hs.ld;
     if (paired) {
-      // One problem over the interleaved rows; C rows, statistics and label
+      // One problem over student and teacher rows in blocks of 16, read in
+      // place from both tensors (one pitch); C rows, statistics and label
       // logits come out in the usual order (student rows, then teacher rows).
-      timed(c, ORDA_KERNEL_OTHER, [&] {
-        return launch_interleave_rows(hpair, ldh_cat, at(in.hs.p, gs * in.hs.ld, dt),
-                                      at(in.th.p, gs * in.th.ld, dt), in.hs.ld, btg, round8(h),
-                                      c->stream);
-      });
+      f.prob[0] = {at(in.hs.p, gs * in.hs.ld, dt), in.W.p, L};
+      f.lg.pair_teacher = at(in.th.p, gs * in.th.ld, dt);
       f.M = 2 * ((btg + 15) / 16 * 16);
-      f.lda = ldh_cat;
-      f.prob[0] = {hpair, in.W.p, L};
       f.lg.pair_rows = btg;
       f.lg.cross = cross;
     } else if (fuse_t) {
@@ -836,7 +830,6 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
       ws_release(c, "stats");
       ws_release(c, "xy");
       ws_release(c, "dlogits");
-      ws_release(c, "hpair");
       ws_release(c, "cross");
       ws_release(c, "rconst");
       ws_release(c, "splitk");

@@ -199,7 +199,32 @@ struct Loader {
     }
   }
 
-  // Source of a full stage kt (all SK elements of K exist).
+  // K-major paired rows read in place (LogitStatsArgs::pair_teacher), as
+  // PairLoader::init_paired for the single-stage layout: transfer i of wave
+  // w covers tile rows 16(4i + w) .. +15, so odd waves move teacher rows
+  // only. Used for the K left after the stage pairs.
+  __device__ __forceinline__ void init_paired(const void* ps, const void* pt, int64_t ld,
+                                              int64_t rows, int64_t k, int64_t origin, int wave,
+                                              int lane) {
+    static_assert(KMAJOR && ES == 2, "paired rows are bf16 and K-major");
+    ld_bytes = ld * ES;
+    K = k;
+    const int64_t last = rows - 1;
+    const int64_t b0 = origin < last ? origin : last;
+    base = static_cast<const unsigned char*>((wave & 1) ? pt : ps) + b0 * ld_bytes;
+#pragma unroll
+    for (int i = 0; i < kXfers; ++i) {
+      const int P = (i * 4 + wave) * 64 + lane;
+      const int r = P / CPR;
+      const int c = (P % CPR) ^ kmaj_swz(r);
+      const int64_t src = origin + 16 * (r >> 5) + (r & 15);
+      const int64_t rr = src < last ? src : last;
+      goff[i] = static_cast<uint32_t>((rr - b0) * ld_bytes + c * 16);
+      kidx[i] = c * EPC;
+    }
+  }
+
+  // Source of stage kt (from its first K element on).
   __device__ __forceinline__ const unsigned char* stage_src(int kt) const {
     const int64_t k0 = static_cast<int64_t>(kt) * SK;
     return KMAJOR ? base + k0 * ES : base + k0 * ld_bytes;
@@ -209,7 +234,7 @@ struct Loader {
   // K write zeros instead, so the tail stage contributes nothing.
   __device__ __forceinline__ void issue(unsigned char* tile, int kt, int wave, int lane) const {
     const int64_t k0 = static_cast<int64_t>(kt) * SK;
-    const unsigned char* s = KMAJOR ? base + k0 * ES : base + k0 * ld_bytes;
+    const unsigned char* s = stage_src(kt);
     const int64_t krem = K - k0;
     if (krem >= SK) {
 #pragma unroll
@@ -271,6 +296,30 @@ struct PairLoader {
         const int cc = c < cmax ? c : cmax;
         goff[t] = static_cast<uint32_t>(r * ldb + cc * 16);
       }
+    }
+  }
+  // K-major paired rows read in place (LogitStatsArgs::pair_teacher): tile
+  // row r of 32-row block b = r/32 is row origin + 16b + r%16 of the student
+  // tensor ps (r%32 < 16) or of the teacher tensor pt. Transfer t of wave w
+  // covers tile rows 32t + 8w .. 32t + 8w + 7, so waves 0-1 move student
+  // rows only and waves 2-3 teacher rows only: one base per wave. Rows past
+  // `rows` are clamped to the last one (their outputs are not stored).
+  __device__ __forceinline__ void init_paired(const void* ps, const void* pt, int64_t ld,
+                                              int64_t rows, int64_t origin, int wave, int lane) {
+    static_assert(KMAJOR, "paired rows are K-major");
+    const int64_t ldb = ld * 2;
+    const int64_t last = rows - 1;
+    const int64_t b0 = origin < last ? origin : last;   // base row, within the tensor
+    base = static_cast<const unsigned char*>(wave < 2 ? ps : pt) + b0 * ldb;
+    step = 128;
+#pragma unroll
+    for (int t = 0; t < kX; ++t) {
+      const int P = (t * 4 + wave) * 64 + lane;
+      const int r = P >> 3;
+      const int q = (P & 7) ^ (r & 7);
+      const int64_t src = origin + 16 * (r >> 5) + (r & 15);
+      const int64_t rr = src < last ? src : last;
+      goff[t] = static_cast<uint32_t>((rr - b0) * ldb + q * 16);
     }
   }
   __device__ __forceinline__ const unsigned char* src(int pair) const { return base + pair * step; }
@@ -520,6 +569,20 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
     pr.b = static_cast<const unsigned char*>(pr.b) + kbeg * (BK ? 1 : g.ldb) * ES;
     pr.c = static_cast<float*>(pr.c) + static_cast<int64_t>(split) * g.split_stride;
   }
+  // A loader over this workgroup's K range (paired rows read in place for
+  // the paired logits GEMM).
+  auto init_a = [&](Loader<T, AK>& l) {
+    if constexpr (EPI == GemmEpilogue::Logits && AK && Elem<T>::kSize == 2) {
+      if (g.lg.pair_rows > 0) {
+        l.init_paired(pr.a, g.lg.pair_teacher, g.lda, g.lg.pair_rows, Kl, tc.m0 >> 1, wave, lane);
+        return;
+      }
+    }
+    l.init(pr.a, g.lda, g.M, Kl, tc.m0, wave, lane);
+  };
+  // B loader over this workgroup's K range.
+  using LoaderB = Loader<T, BK>;
+  auto init_b = [&](LoaderB& l) { l.init(pr.b, g.ldb, g.N, Kl, tc.n0, wave, lane); };
 
   // Logits: this thread's tile-row label, loaded now so that it has long
   // landed when the epilogue needs it (tile row -> student row as in the
@@ -599,7 +662,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       // operations ride between the MFMAs (64 per stage, issued as 32 pairs).
       PairLoader<AK> pa;
       PairLoader<BK> pb;
-      pa.init(pr.a, g.lda, g.M, tc.m0, wave, lane);
+      if (EPI == GemmEpilogue::Logits && g.lg.pair_rows > 0)
+        pa.init_paired(pr.a, g.lg.pair_teacher, g.lda, g.lg.pair_rows, tc.m0 >> 1, wave, lane);
+      else
+        pa.init(pr.a, g.lda, g.M, tc.m0, wave, lane);
       pb.init(pr.b, g.ldb, g.N, tc.n0, wave, lane);
       const int np = nkf / 2;
       // Transfer x (0-7 A, 8-15 B) of a pair's DMA into double slot D, from
@@ -743,8 +809,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       const int ns = 2 * np;
       PairLoader<AK> pa;
       pa.init(pr.a, g.lda, g.M, tc.m0, wave, lane);
-      Loader<T, BK> lb;
-      lb.init(pr.b, g.ldb, g.N, Kl, tc.n0, wave, lane);
+      LoaderB lb;
+      init_b(lb);
       // Transfer x (0-7) of an A pair into double slot D.
       auto dma_a = [&](auto d_c, int x, uint64_t sa) {
         constexpr int MA = decltype(d_c)::value * 2 * kOpBytes;
@@ -881,9 +947,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       // s+1 has landed". An iteration whose stage s+1 does not exist reads a
       // slot whose contents are never used.
       Loader<T, AK> la;
-      Loader<T, BK> lb;
-      la.init(pr.a, g.lda, g.M, Kl, tc.m0, wave, lane);
-      lb.init(pr.b, g.ldb, g.N, Kl, tc.n0, wave, lane);
+      LoaderB lb;
+      init_a(la);
+      init_b(lb);
       if (nkf > 0) {
 #pragma unroll
         for (int t = 0; t < kRing; ++t) {
@@ -975,9 +1041,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
     // stage, an in-bounds dummy copy of stage 0 into a slot nobody reads
     // again), so one constant vmcnt wait always means "stage s has landed".
     Loader<T, AK> la;
-    Loader<T, BK> lb;
-    la.init(pr.a, g.lda, g.M, Kl, tc.m0, wave, lane);
-    lb.init(pr.b, g.ldb, g.N, Kl, tc.n0, wave, lane);
+    LoaderB lb;
+    init_a(la);
+    init_b(lb);
     auto issue_stage = [&](int slot_idx, int st) {
       const int src = st < nkf ? st : 0;
       la.issue(tileA(slot_idx), src, wave, lane);
@@ -1002,9 +1068,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
     // and a partial last stage — one at a time through slot 0 in the
     // single-stage layout: DMA the valid part, zero the rest.
     Loader<T, AK> la;
-    Loader<T, BK> lb;
-    la.init(pr.a, g.lda, g.M, Kl, tc.m0, wave, lane);
-    lb.init(pr.b, g.ldb, g.N, Kl, tc.n0, wave, lane);
+    LoaderB lb;
+    init_a(la);
+    init_b(lb);
     auto tail_stage = [&](int st) {
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_waitcnt(kWaitAll);
@@ -1482,7 +1548,8 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
   if ((g.lda % 8) || (g.ldb % 8) || (g.ldc % 8 && g.epi == GemmEpilogue::Logits))
     return hipErrorInvalidValue;
   if (g.epi == GemmEpilogue::Logits && g.lg.pair_rows > 0 &&
-      (g.nprob != 1 || g.lg.cross == nullptr || g.M != 2 * ((g.lg.pair_rows + 15) / 16 * 16)))
+      (g.nprob != 1 || g.lg.cross == nullptr || g.lg.pair_teacher == nullptr ||
+       g.in_type != DType::BF16 || g.M != 2 * ((g.lg.pair_rows + 15) / 16 * 16)))
     return hipErrorInvalidValue;
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
   const int64_t tiles = ((g.M + kTile - 1) / kTile) * ((g.N + kTile - 1) / kTile) * g.nprob;

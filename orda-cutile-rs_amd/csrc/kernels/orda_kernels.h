@@ -41,15 +41,17 @@ struct LogitStatsArgs {
   const int64_t* labels;  // label of row m of either problem = labels[m]
   int64_t ignore_index;
   float inv_t;            // 1/T
-  // Paired rows (one problem): pair_rows > 0 means A interleaves student
-  // and teacher rows in blocks of 16 (student rows 16b..16b+15 at A rows
-  // 32b..32b+15, the same teacher rows at 32b+16..32b+31, rows past
-  // pair_rows zero), M = 2*round16(pair_rows). Student row r is stored as
-  // row r of C / stats / xy, teacher row r as row pair_rows + r, and
+  // Paired rows (one problem, bf16): pair_rows > 0 means the GEMM's rows
+  // are student and teacher rows in blocks of 16 (student rows 16b..16b+15
+  // as rows 32b..32b+15, the same teacher rows as 32b+16..32b+31),
+  // M = 2*round16(pair_rows), read in place: student rows from prob[0].a,
+  // teacher rows from pair_teacher, both with pitch lda. Student row r is
+  // stored as row r of C / stats / xy, teacher row r as row pair_rows + r, and
   //   cross[r * stats_ld + n_tile] = Σ e^((t_j - max_t)/T) · (t_j - s_j)
   // over the tile's columns, max_t being the teacher row's tile maximum.
   int64_t pair_rows;
   float* cross;
+  const void* pair_teacher;
 };
 
 struct GemmArgs {
@@ -133,13 +135,6 @@ struct RowPassArgs {
 };
 
 hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t stream);
-
-// Paired-row staging for the logits GEMM (LogitStatsArgs::pair_rows): dst row
-// 32b + i = s0 row 16b + i, dst row 32b + 16 + i = s1 row 16b + i, rows past
-// n_rows zero. Copies `cols` (multiple of 8) bf16 columns per row; pitches in
-// elements, multiples of 8.
-hipError_t launch_interleave_rows(void* dst, int64_t ldd, const void* s0, const void* s1,
-                                  int64_t lds, int64_t n_rows, int64_t cols, hipStream_t stream);
 
 // Per-row statistics of rows that were not produced by the GEMM (Precomputed
 // teacher logits, the chunk-launcher entry point). Reads src (fp32 or bf16,

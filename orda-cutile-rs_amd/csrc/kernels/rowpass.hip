@@ -704,32 +704,7 @@ __global__ void zero_pad_kernel(T* base, int64_t ld, int64_t n_rows, int64_t v) 
     base[(i / w) * ld + v + i % w] = static_cast<T>(0.f);
 }
 
-// Paired-row staging (launch_interleave_rows); pitches and columns in
-// 16-byte chunks, one workgroup row per destination row.
-__global__ void interleave_rows_kernel(u32x4* dst, int64_t ldd, const u32x4* s0, const u32x4* s1,
-                                       int64_t lds, int64_t n_rows, int64_t chunks) {
-  const int64_t R = blockIdx.y;
-  const int64_t r = ((R >> 5) << 4) + (R & 15);
-  const u32x4* src = ((R >> 4) & 1) ? s1 : s0;
-  for (int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; c < chunks;
-       c += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    dst[R * ldd + c] = r < n_rows ? src[r * lds + c] : u32x4{0u, 0u, 0u, 0u};
-}
-
 }  // namespace
-
-hipError_t launch_interleave_rows(void* dst, int64_t ldd, const void* s0, const void* s1,
-                                  int64_t lds, int64_t n_rows, int64_t cols, hipStream_t s) {
-  if (n_rows <= 0) return hipSuccess;
-  if ((ldd % 8) || (lds % 8) || (cols % 8)) return hipErrorInvalidValue;
-  const int64_t rows = 2 * ((n_rows + 15) / 16 * 16);
-  const int64_t chunks = cols / 8;
-  dim3 grid(static_cast<unsigned>((chunks + 255) / 256), static_cast<unsigned>(rows));
-  hipLaunchKernelGGL(interleave_rows_kernel, grid, dim3(256), 0, s, static_cast<u32x4*>(dst),
-                     ldd / 8, static_cast<const u32x4*>(s0), static_cast<const u32x4*>(s1), lds / 8,
-                     n_rows, chunks);
-  return hipGetLastError();
-}
 
 hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
   if (a.n_rows <= 0) return hipSuccess;
