@@ -1,8 +1,8 @@
 /*
  * orda_oracle.c — CPU restatement of malcolmgreaves/orda-cutile-rs's
  * `distillation_loss` path. TEST INFRASTRUCTURE ONLY: it is the parity
- * checker for the HIP library and the CPU baseline of bench.py; the product
- * never links it.
+ * oracle of the HIP library's tests and the CPU baseline of bench.py; the
+ * product never links it.
  *
  * Each function cites the reference file:line it restates. Types follow the
  * reference exactly (Rust f32 -> float, f64 -> double, usize -> size_t), loops

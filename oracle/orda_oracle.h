@@ -1,6 +1,6 @@
 /*
  * orda_oracle.h — CPU restatement of the reference crate's distillation-loss
- * path (malcolmgreaves/orda-cutile-rs), used ONLY as the parity checker.
+ * path (malcolmgreaves/orda-cutile-rs), used ONLY as the parity oracle.
  *
  * TEST INFRASTRUCTURE. Only tests/, __graft_entry__.smoke() and bench.py's
  * cpu_baseline leg load this library. The product (liborda_hip.so) never
