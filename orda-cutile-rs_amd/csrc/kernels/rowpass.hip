@@ -57,6 +57,27 @@ __device__ __forceinline__ Stat shfl_xor_stat(Stat s, int o) {
   return r;
 }
 
+// merge() of teacher statistics that also carries x, a sum of terms
+// c·e^((x_j - m)/T) relative to the statistics' maximum m (the KL cross
+// partials): rescaled by the same factors as dT.
+__device__ __forceinline__ void merge_cross(Stat& a, float& ax, Stat b, float bx, float it2) {
+  const float m = fmaxf(a.m, b.m);
+  a.sx += b.sx;
+  if (m == -INFINITY) {
+    a.m = m;
+    a.d1 = 0.f;
+    a.dT = 0.f;
+    ax = 0.f;
+    return;
+  }
+  const float fa = __builtin_amdgcn_exp2f((a.m - m) * it2), fb = __builtin_amdgcn_exp2f((b.m - m) * it2);
+  a.d1 = a.d1 * __builtin_amdgcn_exp2f((a.m - m) * kLog2e) +
+         b.d1 * __builtin_amdgcn_exp2f((b.m - m) * kLog2e);
+  a.dT = a.dT * fa + b.dT * fb;
+  ax = ax * fa + bx * fb;
+  a.m = m;
+}
+
 // Block-wide merge of per-thread partial stats; every thread gets the result.
 __device__ Stat block_merge(Stat s, float it2, Stat* scratch) {
 #pragma unroll
@@ -500,13 +521,16 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
 //   log2(kd·T) - lseT_s·log2e, log2(kd·T) - lseT_t·log2e, log2(w_t) - lse1_t·log2e.
 template <bool KL, bool TG>
 __global__ __launch_bounds__(kThreads) void row_consts_kernel(RowPassArgs a) {
-  __shared__ Stat sstat[kThreads / 64];
-  __shared__ float ssum[kThreads / 64];
-  const int64_t r = blockIdx.x;
-  const int tid = threadIdx.x;
+  // One wave per row, kThreads / 64 rows per workgroup: each lane merges
+  // every 64th tile entry, then a butterfly over the wave. No LDS, no
+  // barrier. The teacher's KL cross partials are merged with its
+  // statistics, rescaled like Σe^((x-max)/T).
+  const int lane = threadIdx.x & 63;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+  if (r >= a.n_rows) return;
   const int64_t y = a.labels[r];
   if (y == a.ignore_index) {   // cross_entropy.rs:59, kl.rs:92
-    if (tid == 0) {
+    if (lane == 0) {
       a.row_nll_s[r] = 0.f;
       a.row_nll_t[r] = 0.f;
       a.row_kl[r] = 0.f;
@@ -517,20 +541,40 @@ __global__ __launch_bounds__(kThreads) void row_consts_kernel(RowPassArgs a) {
   const float T = a.temperature;
   const float inv_t = 1.0f / T;
   const float it2 = inv_t * kLog2e;
-  const Stat ss = load_row_stats(a.stats_s + r * a.stats_ld, a.stats_tiles, it2, sstat);
-  Stat st{-INFINITY, 0.f, 0.f, 0.f};
-  if (KL || TG || a.teacher_ce)
-    st = load_row_stats(a.stats_t + r * a.stats_ld, a.stats_tiles_t, it2, sstat);
+  Stat ss{-INFINITY, 0.f, 0.f, 0.f}, st{-INFINITY, 0.f, 0.f, 0.f};
   float xc = 0.f;
-  if (KL) {
-    const float4* srow_t = a.stats_t + r * a.stats_ld;
-    const float* crow = a.cross + r * a.stats_ld;
-    float part = 0.f;
-    for (int64_t t = tid; t < a.stats_tiles_t; t += kThreads)
-      part = fmaf(crow[t], __builtin_amdgcn_exp2f((srow_t[t].x - st.m) * it2), part);
-    xc = block_sum(part, ssum);
+  const float4* rs = a.stats_s + r * a.stats_ld;
+  const bool teacher = KL || TG || a.teacher_ce;
+  const float4* rt = a.stats_t + r * a.stats_ld;
+  const float* rc = KL ? a.cross + r * a.stats_ld : nullptr;
+  const int64_t nt = a.stats_tiles > a.stats_tiles_t ? a.stats_tiles : a.stats_tiles_t;
+  // kPer entries per lane in flight before any merge; a missing entry is
+  // {-inf, 0, 0, 0}, which merges as nothing.
+  constexpr int kPer = 8;
+  const float4 none = make_float4(-INFINITY, 0.f, 0.f, 0.f);
+  for (int64_t t0 = 0; t0 < nt; t0 += 64 * kPer) {
+    float4 vs[kPer], vt[kPer];
+    float vc[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int64_t t = t0 + i * 64 + lane;
+      vs[i] = t < a.stats_tiles ? rs[t] : none;
+      const bool tok = teacher && t < a.stats_tiles_t;
+      vt[i] = tok ? rt[t] : none;
+      vc[i] = KL && tok ? rc[t] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      ss = merge(ss, Stat{vs[i].x, vs[i].y, vs[i].z, vs[i].w}, it2);
+      merge_cross(st, xc, Stat{vt[i].x, vt[i].y, vt[i].z, vt[i].w}, vc[i], it2);
+    }
   }
-  if (tid == 0) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    ss = merge(ss, shfl_xor_stat(ss, o), it2);
+    merge_cross(st, xc, shfl_xor_stat(st, o), __shfl_xor(xc, o), it2);
+  }
+  if (lane == 0) {
     const double alpha = static_cast<double>(a.label_smoothing);
     const float lse1_s = ss.m + logf(ss.d1);
     const float lseT_s = ss.m * inv_t + logf(ss.dT);
@@ -730,21 +774,22 @@ hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
     // elementwise gradient.
     const int64_t chunks = (a.v + kChunk - 1) / kChunk;
     const int64_t blocks = a.n_rows * chunks;
+    const dim3 cgrid(static_cast<unsigned>((a.n_rows + kThreads / 64 - 1) / (kThreads / 64)));
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     if (kl && tg) {
-      hipLaunchKernelGGL((row_consts_kernel<true, true>), grid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((row_consts_kernel<true, true>), cgrid, dim3(kThreads), 0, s, a);
       hipLaunchKernelGGL((row_grad_kernel<true, true>), dim3(static_cast<unsigned>(blocks)),
                          dim3(kThreads), 0, s, a, chunks);
     } else if (kl) {
-      hipLaunchKernelGGL((row_consts_kernel<true, false>), grid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((row_consts_kernel<true, false>), cgrid, dim3(kThreads), 0, s, a);
       hipLaunchKernelGGL((row_grad_kernel<true, false>), dim3(static_cast<unsigned>(blocks)),
                          dim3(kThreads), 0, s, a, chunks);
     } else if (tg) {
-      hipLaunchKernelGGL((row_consts_kernel<false, true>), grid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((row_consts_kernel<false, true>), cgrid, dim3(kThreads), 0, s, a);
       hipLaunchKernelGGL((row_grad_kernel<false, true>), dim3(static_cast<unsigned>(blocks)),
                          dim3(kThreads), 0, s, a, chunks);
     } else {
-      hipLaunchKernelGGL((row_consts_kernel<false, false>), grid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((row_consts_kernel<false, false>), cgrid, dim3(kThreads), 0, s, a);
       hipLaunchKernelGGL((row_grad_kernel<false, false>), dim3(static_cast<unsigned>(blocks)),
                          dim3(kThreads), 0, s, a, chunks);
     }
