@@ -61,3 +61,43 @@ def test_tied_bf16_int8_full_benchmark_shape():
     assert int(codes.abs().max()) <= 127
     assert bool((codes[other].abs().amax(1) == 127).all())
     assert torch.equal(got.grad_weight[other], codes[other].float() * scales[other, None])
+
+
+FP32_WORKLOADS = ["tied-2048x4096x32000-f32", "separate-4096x2048x4096x32000-f32",
+                  "precomputed-4096x4096x65536-f32"]
+
+
+@pytest.mark.parametrize("name", FP32_WORKLOADS)
+def test_fp32_workloads_full_shape(name):
+    """The fp32 workloads at their full shapes, on bench.py's own inputs (its
+    seeded generator), every 17th label ignored, against loss_chunked run on
+    the same GPU: loss terms to 1e-4, fp32 gradients to 1e-3."""
+    import torch
+    import bench
+    from torch_reference import loss_chunked
+    assert torch.cuda.is_available(), "GPU tests need a visible GPU"
+    assert H.is_available(), "liborda_hip.so does not see a gfx950 device"
+    torch.backends.cuda.matmul.allow_tf32 = False
+    wl = bench.WORKLOADS[name]
+    mode, bt, h, ht, v, dt, kd, T, alpha, w_t, _ = wl
+    dev = torch.device("cuda:0")
+    s, w, y, t = bench.make_inputs(torch, wl, dev, seed=7)
+    y[::17] = -100
+    opts = bench.options(H, wl)
+    print(f"case {name}", flush=True)
+    got = H.distillation_loss(s, w, y, bench.teacher_obj(H, t), opts)
+    th = t[1] if mode in ("tied", "separate") else None
+    tw = t[2] if mode == "separate" else None
+    tl = t[1] if mode == "precomputed" else None
+    ref = loss_chunked(s, w, y, mode, th, tw, tl, kd=kd, T=T, alpha=alpha,
+                       w_t=opts.teacher_ce_weight)
+    rel = {}
+    for k in ("loss", "student_ce", "teacher_ce", "kl"):
+        check_scalar(k, getattr(got, k), ref[k])
+        rel[k] = abs(getattr(got, k) - ref[k]) / max(abs(ref[k]), 1e-2)
+    for k in ("grad_student_hidden", "grad_weight", "grad_teacher_hidden", "grad_teacher_weight"):
+        g, r = getattr(got, k), ref[k]
+        assert (g is None) == (r is None), f"{k}: presence differs"
+        if r is not None:
+            rel[k] = check_grad_device(k, g, r, "f32")
+    print("relative errors:", {k: f"{e:.2e}" for k, e in rel.items()})

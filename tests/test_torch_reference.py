@@ -9,7 +9,7 @@ import pytest
 import oracle as O
 from helpers import labels, mat
 from orda_hip.types import LossOptions, Reduction, Teacher
-from torch_reference import loss_f64, loss_tied_chunked
+from torch_reference import loss_chunked, loss_f64, loss_tied_chunked
 
 CASES = {
     # name: (mode, bt, h, ht, v, options, ignore_every)
@@ -101,4 +101,44 @@ def test_chunked_tied_reference_matches_oracle(opts, rows):
         t = got[k].numpy().astype(np.float64)
         r = np.asarray(r, np.float64)
         err = np.linalg.norm(t - r) / max(np.linalg.norm(r), 1e-30)
+        assert err <= 1e-5, f"{k}: rel fro err {err:.3e}"
+
+
+@pytest.mark.parametrize("name,rows", [(n, r) for n in sorted(CASES) for r in (3, 1024)])
+def test_chunked_reference_matches_oracle_all_modes(name, rows):
+    """loss_chunked for every teacher mode (the full-size GPU tests' reference)
+    against the oracle on the CASES inputs, in chunks of 3 rows and in one
+    chunk: loss terms to 1e-6, gradients to 1e-5."""
+    import torch
+    mode, bt, h, ht, v, o, every = CASES[name]
+    s, w = mat(bt, h, 1, 0.5), mat(v, h, 2, 0.4)
+    y = labels(bt, v, every)
+    th = tw = tl = None
+    if mode == "tied":
+        th = mat(bt, h, 3, 0.5)
+        teacher = Teacher.Tied(th)
+    elif mode == "separate":
+        th, tw = mat(bt, ht, 3, 0.5), mat(v, ht, 4, 0.4)
+        teacher = Teacher.Separate(th, tw)
+    else:
+        tl = mat(bt, v, 5, 2.0)
+        teacher = Teacher.Precomputed(tl)
+    opts = LossOptions(**o)
+    ref = O.distillation_loss(s, w, y, teacher, opts)
+    t = lambda a: None if a is None else torch.from_numpy(a)
+    got = loss_chunked(t(s), t(w), t(y), mode, t(th), t(tw), t(tl), kd=opts.kd_weight,
+                       T=opts.temperature, alpha=opts.label_smoothing, w_s=opts.student_ce_weight,
+                       w_t=opts.teacher_ce_weight, ignore=opts.ignore_index,
+                       mean=opts.reduction == Reduction.Mean, rows=rows)
+    for k in ("loss", "student_ce", "teacher_ce", "kl"):
+        r = getattr(ref, k)
+        assert abs(got[k] - r) <= 1e-6 * max(abs(r), 1e-2), f"{k}: chunked {got[k]!r} oracle {r!r}"
+    for k in ("grad_student_hidden", "grad_weight", "grad_teacher_hidden", "grad_teacher_weight"):
+        r = getattr(ref, k)
+        assert (r is None) == (got[k] is None), f"{k}: presence differs"
+        if r is None:
+            continue
+        g = got[k].numpy().astype(np.float64)
+        r = np.asarray(r, np.float64)
+        err = np.linalg.norm(g - r) / max(np.linalg.norm(r), 1e-30)
         assert err <= 1e-5, f"{k}: rel fro err {err:.3e}"

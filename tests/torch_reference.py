@@ -8,10 +8,10 @@ weights and deferred mean, src/api.rs:211-230, 401-405) and the gradients come
 from torch autograd. Used to pin the torch autograd op: the CPU tests check it
 against the oracle, the GPU tests check the op's .grad values against it.
 
-`loss_tied_chunked` states the same Tied-teacher loss row-chunked with explicit
-gradients (float32 GEMMs, float64 row arithmetic), on any device: the
-full-size GPU test runs it on the GPU beside the library; the CPU tests pin it
-to the oracle at small sizes.
+`loss_chunked` states the same loss row-chunked with explicit gradients
+(float32 GEMMs, float64 row arithmetic) for every teacher mode, on any
+device: the full-size GPU tests run it on the GPU beside the library; the CPU
+tests pin it to the oracle at small sizes.
 """
 import numpy as np
 import torch
@@ -73,20 +73,26 @@ def loss_f64(hs, w, labels, mode, th=None, tw=None, tl=None, *, w_s=1.0, w_t=Non
     }
 
 
-def loss_tied_chunked(hs, ht, w, labels, *, kd, T, alpha, w_s=1.0, w_t=1.0, ignore=-100,
-                      mean=True, rows=1024):
-    """Tied teacher at any size, on the tensors' own device, `rows` rows at a
-    time: logits hs·Wᵀ and ht·Wᵀ as float32 GEMMs; log-sum-exp, losses and
-    dlogits in float64 (label-smoothed CE per row, src/reference/
-    cross_entropy.rs:27-73; teacher-detached KL at T, gradient kd·T·(p_s − p_t),
-    src/reference/kl.rs:83-124; KL merged into the student rows, src/api.rs:
-    336-344); the deferred mean as the float32 1/max(n_valid, 1) applied to
-    every gradient (src/api.rs:225-230, 381-388); backward GEMMs dlogits·W and
-    dlogitsᵀ·h in float32 (src/api.rs:346-361). Explicit gradients, no
-    autograd, so the full benchmark shape fits. Returns the loss terms as
-    floats and float32 gradient tensors."""
+def loss_chunked(hs, w, labels, mode, th=None, tw=None, tl=None, *, kd, T, alpha, w_s=1.0,
+                 w_t=None, ignore=-100, mean=True, rows=1024):
+    """Any teacher mode at any size, on the tensors' own device, `rows` rows
+    at a time: logits hs·Wᵀ and the teacher's (th·Wᵀ Tied, th·twᵀ Separate,
+    tl Precomputed) as float32 GEMMs; log-sum-exp, losses and dlogits in
+    float64 (label-smoothed CE per row, src/reference/cross_entropy.rs:27-73;
+    teacher-detached KL at T, gradient kd·T·(p_s − p_t), src/reference/
+    kl.rs:83-124; KL merged into the student rows, src/api.rs:336-344;
+    teacher CE and its gradient to the teacher's parameters when w_t > 0,
+    src/api.rs:316-333); the deferred mean as the float32 1/max(n_valid, 1)
+    applied to every gradient (src/api.rs:225-230, 381-388); backward GEMMs
+    in float32 (src/api.rs:346-370). Explicit gradients, no autograd, so the
+    full benchmark shapes fit. Returns the loss terms as floats and float32
+    gradient tensors (None where the reference returns none,
+    src/api.rs:244-258)."""
     dev = hs.device
+    if w_t is None:
+        w_t = 1.0 if mode == "tied" else 0.0
     wf = w.float()
+    twf = tw.float() if mode == "separate" else None
     n, h = hs.shape
     V = w.shape[0]
     y = labels.to(dev)
@@ -94,9 +100,11 @@ def loss_tied_chunked(hs, ht, w, labels, *, kd, T, alpha, w_s=1.0, w_t=1.0, igno
     nv = int(valid.sum())
     scale = float(np.float32(1.0) / np.float32(max(nv, 1))) if mean else 1.0
     f32 = torch.float32
+    t_grad = mode in ("tied", "separate") and w_t > 0
     gs = torch.empty(n, h, dtype=f32, device=dev)
-    gt = torch.empty(n, h, dtype=f32, device=dev) if w_t > 0 else None
     gw = torch.zeros(V, h, dtype=f32, device=dev)
+    gt = torch.empty(n, th.shape[1], dtype=f32, device=dev) if t_grad else None
+    gtw = torch.zeros(V, th.shape[1], dtype=f32, device=dev) if t_grad and mode == "separate" else None
     sums = {"s": 0.0, "t": 0.0, "kl": 0.0}
 
     def ce(x, vm, ys, idx):
@@ -114,11 +122,18 @@ def loss_tied_chunked(hs, ht, w, labels, *, kd, T, alpha, w_s=1.0, w_t=1.0, igno
 
     for r0 in range(0, n, rows):
         r1 = min(r0 + rows, n)
-        hs_c, ht_c = hs[r0:r1].float(), ht[r0:r1].float()
+        hs_c = hs[r0:r1].float()
         vm = valid[r0:r1]
         ys = torch.where(vm, y[r0:r1], torch.zeros_like(y[r0:r1]))
         idx = torch.arange(r1 - r0, device=dev)
-        ls, lt = hs_c @ wf.T, ht_c @ wf.T
+        ls = hs_c @ wf.T
+        ht_c = th[r0:r1].float() if mode in ("tied", "separate") else None
+        if mode == "tied":
+            lt = ht_c @ wf.T
+        elif mode == "separate":
+            lt = ht_c @ twf.T
+        else:
+            lt = tl[r0:r1].float()
         nll, ds = ce(ls, vm, ys, idx)
         sums["s"] += nll
         ds *= w_s
@@ -139,11 +154,24 @@ def loss_tied_chunked(hs, ht, w, labels, *, kd, T, alpha, w_s=1.0, w_t=1.0, igno
         if w_t > 0:
             nll, dt = ce(lt, vm, ys, idx)
             sums["t"] += nll
-            dtf = (dt * (w_t * scale)).to(f32)
+            if t_grad:
+                dtf = (dt * (w_t * scale)).to(f32)
+                if mode == "tied":
+                    gt[r0:r1] = dtf @ wf
+                    gw += dtf.T @ ht_c
+                else:
+                    gt[r0:r1] = dtf @ twf
+                    gtw += dtf.T @ ht_c
+                del dtf
             del dt
-            gt[r0:r1] = dtf @ wf
-            gw += dtf.T @ ht_c
     loss = (w_s * sums["s"] + w_t * sums["t"] + kd * sums["kl"]) * scale
     return {"loss": loss, "student_ce": sums["s"] * scale, "teacher_ce": sums["t"] * scale,
             "kl": sums["kl"] * scale, "grad_student_hidden": gs, "grad_weight": gw,
-            "grad_teacher_hidden": gt}
+            "grad_teacher_hidden": gt, "grad_teacher_weight": gtw}
+
+
+def loss_tied_chunked(hs, ht, w, labels, *, kd, T, alpha, w_s=1.0, w_t=1.0, ignore=-100,
+                      mean=True, rows=1024):
+    """loss_chunked for a Tied teacher (teacher CE weight 1 by default)."""
+    return loss_chunked(hs, w, labels, "tied", th=ht, kd=kd, T=T, alpha=alpha, w_s=w_s, w_t=w_t,
+                        ignore=ignore, mean=mean, rows=rows)
