@@ -50,6 +50,11 @@ struct orda_ctx {
     int64_t bytes = 0;
   };
   std::map<std::string, Buf> bufs;
+  // Pinned host staging for small device-to-host reads (the labels, which
+  // the host validates and counts): a copy into pageable memory costs
+  // several times as long.
+  void* pinned = nullptr;
+  int64_t pinned_bytes = 0;
   bool timing = false;
   struct Pending {
     int kind;
@@ -304,9 +309,17 @@ std::vector<int64_t> host_labels(orda_ctx* c, const int64_t* labels, int64_t n, 
   if (n == 0) return h;
   if (!labels) fail(ORDA_ERR_INVALID, "labels is null");
   if (loc == ORDA_DEVICE) {
-    hip_check(hipMemcpyAsync(h.data(), labels, n * 8, hipMemcpyDeviceToHost, c->stream),
+    if (c->pinned_bytes < n * 8) {
+      if (c->pinned) hip_check(hipHostFree(c->pinned), "hipHostFree");
+      c->pinned = nullptr;
+      c->pinned_bytes = 0;
+      hip_check(hipHostMalloc(&c->pinned, n * 8, hipHostMallocDefault), "hipHostMalloc");
+      c->pinned_bytes = n * 8;
+    }
+    hip_check(hipMemcpyAsync(c->pinned, labels, n * 8, hipMemcpyDeviceToHost, c->stream),
               "read labels");
     hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    memcpy(h.data(), c->pinned, n * 8);
   } else {
     memcpy(h.data(), labels, n * 8);
   }
@@ -1026,6 +1039,7 @@ void orda_ctx_destroy(orda_ctx* c) {
     c->pool.push_back(p.b);
   }
   for (hipEvent_t e : c->pool) (void)hipEventDestroy(e);
+  if (c->pinned) (void)hipHostFree(c->pinned);
   ws_trim(c);
   if (c->own) (void)hipStreamDestroy(c->own);
   delete c;
