@@ -771,7 +771,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
           for (int q = 0; q < 2; ++q) {
             const int mm = 2 * pr + q;
             if constexpr (kSwapAB)
-              mfma_bf16(acc[mm >> 3][mm & 7], rcB[mm & 7], rcA[mm >> 3]);
+              mfma_bf16(acc[mm & 7][mm >> 3], rcB[mm >> 3], rcA[mm & 7]);
             else
               mfma_bf16(acc[mm >> 3][mm & 7], rcA[mm >> 3], rcB[mm & 7]);
           }
@@ -904,7 +904,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
           for (int q = 0; q < 2; ++q) {
             const int mm = 2 * pr + q;
             if constexpr (kSwapAB)
-              mfma_bf16(acc[mm >> 3][mm & 7], rcB[mm & 7], rcA[mm >> 3]);
+              mfma_bf16(acc[mm & 7][mm >> 3], rcB[mm >> 3], rcA[mm & 7]);
             else
               mfma_bf16(acc[mm >> 3][mm & 7], rcA[mm >> 3], rcB[mm & 7]);
           }
@@ -1010,7 +1010,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
           for (int q = 0; q < 2; ++q) {
             const int mm = 2 * pr + q;
             if constexpr (kSwapAB)
-              mfma_bf16(acc[mm >> 3][mm & 7], rcB[mm & 7], rcA[mm >> 3]);
+              mfma_bf16(acc[mm & 7][mm >> 3], rcB[mm >> 3], rcA[mm & 7]);
             else
               mfma_bf16(acc[mm >> 3][mm & 7], rcA[mm >> 3], rcB[mm & 7]);
           }
