@@ -316,9 +316,6 @@ __device__ __forceinline__ void store8(__bf16* p, const float (&g)[8]) {
   *reinterpret_cast<u32x4*>(p) = Vec<__bf16>::pack(g);
 }
 // Streaming forms for data touched once (non-temporal hint on the access).
-__device__ __forceinline__ void load8_nt(const __bf16* p, float (&x)[8]) {
-  Vec<__bf16>::unpack(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)), x);
-}
 __device__ __forceinline__ void store8_nt(__bf16* p, const float (&g)[8]) {
   __builtin_nontemporal_store(Vec<__bf16>::pack(g), reinterpret_cast<u32x4*>(p));
 }
@@ -639,24 +636,30 @@ __global__ __launch_bounds__(kThreads) void row_grad_kernel(RowPassArgs a, int64
     xs_y = static_cast<float>(srow[y]);
     if (KL || TG) xt_y = static_cast<float>(trow[y]);
   }
-  float xs[kChunkVec][NV], xt[kChunkVec][NV];
+  // The loads stay packed (bf16 pairs) until their group is computed: half
+  // the registers of unpacked floats, 84 VGPRs instead of 110, five waves per
+  // SIMD instead of four (3.6 % faster; six waves, forced, were 2 % slower).
+  u32x4 rs[kChunkVec], rt[kChunkVec];
 #pragma unroll
   for (int q = 0; q < kChunkVec; ++q) {
     const int64_t j = c0 + (static_cast<int64_t>(q) * kThreads + tid) * NV;
     if (j < v) {
-      load8_nt(srow + j, xs[q]);
-      if (KL || TG) load8_nt(trow + j, xt[q]);
+      rs[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(srow + j));
+      if (KL || TG) rt[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(trow + j));
     }
   }
 #pragma unroll
   for (int q = 0; q < kChunkVec; ++q) {
     const int64_t j = c0 + (static_cast<int64_t>(q) * kThreads + tid) * NV;
     if (j >= v) continue;
+    float xs[NV], xt[NV] = {};
+    Vec<__bf16>::unpack(rs[q], xs);
+    if (KL || TG) Vec<__bf16>::unpack(rt[q], xt);
     float g[NV], gt[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       float gi = 0.f, ti = 0.f;
-      elem(xs[q][i], (KL || TG) ? xt[q][i] : 0.f, gi, ti);
+      elem(xs[i], xt[i], gi, ti);
       const bool valid = j + i < v;
       g[i] = valid ? gi : 0.f;
       gt[i] = valid ? ti : 0.f;
