@@ -719,7 +719,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       constexpr int kReads = kOpsA + kOpsB;
       // MFMA pair of an even iteration's barrier. The earlier the barrier,
       // the longer the next pair has to land: measured 13.4 ms at pair 22,
-      // 13.1 ms at 16, 12.8 ms at 10, 12.7 ms at 6 and 12.8 ms at 4.
+      // 13.1 ms at 16, 12.8 ms at 10, 12.7 ms at 6 and 12.8 ms at 4 (and,
+      // with the final epilogue, 0.5 % slower at 5 and at 7 than at 6).
       constexpr int kMid = 6;
       // MFMA pairs the pair's 16 transfers spread over: all the rest of the
       // iteration (over 16 pairs measured 4 % slower, over 8 pairs 8 %).
