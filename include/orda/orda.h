@@ -167,6 +167,9 @@ int32_t orda_ctx_set_memory_limit(orda_ctx *ctx, int64_t bytes);
 int32_t orda_ctx_set_staging_budget(orda_ctx *ctx, int64_t bytes);
 /* Release the cached workspace. */
 int32_t orda_ctx_trim(orda_ctx *ctx);
+/* Device bytes the context's workspace holds (what orda_ctx_set_memory_limit
+ * bounds): staged inputs, the logits group, statistics, split-K partials. */
+int32_t orda_ctx_workspace_bytes(orda_ctx *ctx, int64_t *bytes);
 /* Per-kernel timing with HIP events on the context's stream. */
 typedef enum {
     ORDA_KERNEL_GEMM_LOGITS = 0,
@@ -186,7 +189,12 @@ int32_t orda_ctx_reset_kernel_time(orda_ctx *ctx);
 /* distillation_loss(student_hidden, weight, labels, teacher, opts)
  * (src/api.rs:188-422). student_hidden [BT,H], weight [V,H] (f32 or bf16,
  * host or device; all float inputs share one dtype), labels [BT] int64 at
- * labels_location. ctx may be NULL (a temporary context on device 0). */
+ * labels_location. ctx may be NULL (a temporary context on device 0).
+ * Labels on the device are validated on the device and the result is read
+ * back with the loss at the call's one synchronisation, so an out-of-range
+ * label is reported (with the reference's message, and ahead of any later
+ * validation error, as in src/api.rs:104-181) after the kernels have run:
+ * the output buffers then hold unspecified values. */
 int32_t orda_distillation_loss(orda_ctx *ctx, const orda_tensor *student_hidden,
                                const orda_tensor *weight, const int64_t *labels,
                                int64_t n_labels, int32_t labels_location,
@@ -199,8 +207,9 @@ int32_t orda_distillation_loss(orda_ctx *ctx, const orda_tensor *student_hidden,
  * KlCeChunkOutput (launch.rs:28-37) in separate buffers: grad_kl_student
  * [n_rows,V], kl_per_row [n_rows], grad_ce [grid_rows,V], ce_loss
  * [grid_rows], grid_rows = student_only ? n_rows : 2*n_rows. Any V (no
- * V % BLOCK requirement). Tensors may live on host or device; targets are
- * int32 like the reference's launcher. */
+ * V % BLOCK requirement); a device logits_chunk is read in place at any
+ * pitch. Tensors may live on host or device; targets are int32 like the
+ * reference's launcher. */
 int32_t orda_kl_ce_on_logits_chunk(orda_ctx *ctx, const orda_tensor *logits_chunk,
                                    const int32_t *targets, int32_t targets_location,
                                    int64_t n_rows, float inv_t, float kl_grad_scale, float t_sq,

@@ -215,6 +215,14 @@ struct DMat {
   DType t = DType::F32;
 };
 
+// The checks every caller tensor passes before any kernel reads it: a
+// non-negative shape, a data pointer when it has elements, ld >= cols.
+void check_view(const orda_tensor& t, const char* what) {
+  if (t.rows < 0 || t.cols < 0) fail(ORDA_ERR_INVALID, "%s has a negative shape", what);
+  if (t.rows > 0 && t.cols > 0 && !t.data) fail(ORDA_ERR_INVALID, "%s has a null data pointer", what);
+  if (tensor_ld(t) < t.cols) fail(ORDA_ERR_INVALID, "%s has ld < cols", what);
+}
+
 // Device-resident view of an input matrix with a pitch that is a multiple of
 // 8 elements and a 16-byte aligned base; copies only when needed.
 DMat stage(orda_ctx* c, const orda_tensor& t, const std::string& name, const char* what) {
@@ -224,8 +232,7 @@ DMat stage(orda_ctx* c, const orda_tensor& t, const std::string& name, const cha
   d.cols = t.cols;
   const int64_t ld = tensor_ld(t);
   const int es = orda::dtype_size(d.t);
-  if (t.rows > 0 && t.cols > 0 && !t.data) fail(ORDA_ERR_INVALID, "%s has a null data pointer", what);
-  if (ld < t.cols) fail(ORDA_ERR_INVALID, "%s has ld < cols", what);
+  check_view(t, what);
   // Pass-through needs whole 16-byte chunks inside every row, including the
   // last one: pitch and width both multiples of 8 elements.
   if (t.location == ORDA_DEVICE && ld % 8 == 0 && t.cols % 8 == 0 &&
@@ -267,7 +274,7 @@ OutMat out_mat(orda_ctx* c, const orda_tensor& t, int64_t rows, int64_t cols,
     fail(ORDA_ERR_INVALID, "%s must be (%lld, %lld), got (%lld, %lld)", what,
          static_cast<long long>(rows), static_cast<long long>(cols),
          static_cast<long long>(t.rows), static_cast<long long>(t.cols));
-  if (!t.data && rows * cols > 0) fail(ORDA_ERR_INVALID, "%s has a null data pointer", what);
+  check_view(t, what);
   OutMat o;
   o.t = &t;
   if (t.location == ORDA_DEVICE) {
@@ -304,36 +311,58 @@ void deliver(orda_ctx* c, const orda_tensor& t, const void* src, int64_t rows, i
             what);
 }
 
+// Pinned host staging of at least `bytes` (small device-to-host reads).
+void* pinned(orda_ctx* c, int64_t bytes) {
+  if (c->pinned_bytes < bytes) {
+    if (c->pinned) hip_check(hipHostFree(c->pinned), "hipHostFree");
+    c->pinned = nullptr;
+    c->pinned_bytes = 0;
+    const int64_t b = std::max<int64_t>(bytes, 256);
+    hip_check(hipHostMalloc(&c->pinned, b, hipHostMallocDefault), "hipHostMalloc");
+    c->pinned_bytes = b;
+  }
+  return c->pinned;
+}
+
+// A host copy of the labels. For labels on the device this reads them back on
+// the context's stream and waits: only the error path of distillation_loss
+// does that (to report a bad label ahead of a later validation failure).
 std::vector<int64_t> host_labels(orda_ctx* c, const int64_t* labels, int64_t n, int32_t loc) {
   std::vector<int64_t> h(static_cast<size_t>(n));
   if (n == 0) return h;
   if (!labels) fail(ORDA_ERR_INVALID, "labels is null");
   if (loc == ORDA_DEVICE) {
-    if (c->pinned_bytes < n * 8) {
-      if (c->pinned) hip_check(hipHostFree(c->pinned), "hipHostFree");
-      c->pinned = nullptr;
-      c->pinned_bytes = 0;
-      hip_check(hipHostMalloc(&c->pinned, n * 8, hipHostMallocDefault), "hipHostMalloc");
-      c->pinned_bytes = n * 8;
-    }
-    hip_check(hipMemcpyAsync(c->pinned, labels, n * 8, hipMemcpyDeviceToHost, c->stream),
-              "read labels");
+    void* p = pinned(c, n * 8);
+    hip_check(hipMemcpyAsync(p, labels, n * 8, hipMemcpyDeviceToHost, c->stream), "read labels");
     hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    memcpy(h.data(), c->pinned, n * 8);
+    memcpy(h.data(), p, n * 8);
   } else {
     memcpy(h.data(), labels, n * 8);
   }
   return h;
 }
 
-const int64_t* device_labels(orda_ctx* c, const int64_t* labels, const std::vector<int64_t>& h,
-                             int32_t loc, const std::string& name) {
+// The labels as a device array the kernels can read: device labels in place
+// (8-byte aligned) or copied on the stream; host labels uploaded.
+const int64_t* device_labels(orda_ctx* c, const int64_t* labels, int64_t n, int32_t loc,
+                             const std::string& name) {
+  if (n > 0 && !labels) fail(ORDA_ERR_INVALID, "labels is null");
   if (loc == ORDA_DEVICE && (reinterpret_cast<uintptr_t>(labels) % 8) == 0) return labels;
-  void* d = ws(c, name, std::max<int64_t>(8, h.size() * 8));
-  if (!h.empty())
-    hip_check(hipMemcpyAsync(d, h.data(), h.size() * 8, hipMemcpyHostToDevice, c->stream),
-              "upload labels");
+  void* d = ws(c, name, std::max<int64_t>(8, n * 8));
+  if (n > 0)
+    hip_check(hipMemcpyAsync(d, labels, n * 8,
+                             loc == ORDA_DEVICE ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                             c->stream),
+              "stage labels");
   return static_cast<const int64_t*>(d);
+}
+
+// api.rs:125-133 on host labels.
+void check_labels_host(const std::vector<int64_t>& hl, int64_t v, int64_t ignore) {
+  for (int64_t t : hl)
+    if (t != ignore && (t < 0 || t >= v))
+      fail(ORDA_ERR_INVALID, "label %lld out of range [0, %lld) and != ignore_index %lld",
+           static_cast<long long>(t), static_cast<long long>(v), static_cast<long long>(ignore));
 }
 
 void config_validate(const orda_kernel_config& k) {
@@ -353,7 +382,7 @@ struct LossPlan {
   float w_s, w_t, kd, T, ls;
   int64_t ignore;
   bool need_teacher, has_ght, has_gwt;
-  float mean_scale;
+  bool mean;                // Reduction::Mean; the scale itself is computed on the device
   int64_t bt, h, v, ht;
   DType dt;
   bool quant, stochastic;
@@ -399,7 +428,9 @@ bool teacher_logits_direct(const LossPlan& P, const Inputs& in) {
          in.tl.ld % 8 == 0 && reinterpret_cast<uintptr_t>(in.tl.p) % 16 == 0;
 }
 
-// Device bytes the loss stages per chunk row.
+// Device bytes the loss stages per chunk row: the buffers run_loss sizes by
+// the group's rows. (The split-K partials of small backward GEMMs are sized
+// by the GEMM, at most 256 MB, and come on top.)
 int64_t staged_bytes_per_row(const LossPlan& P, const Inputs& in) {
   const bool paired = paired_rows(P, in);
   const orda::DType lt = logits_dtype(P, paired);
@@ -409,6 +440,8 @@ int64_t staged_bytes_per_row(const LossPlan& P, const Inputs& in) {
               (orda::dtype_size(lt) + (lt == P.dt ? 0 : orda::dtype_size(P.dt)));
   b += 2 * nst * 16 + 2 * 4;   // statistics, label logits
   if (paired) b += nst * 4 + 16;   // cross partials, row constants
+  if (P.mode == ORDA_TEACHER_TIED && P.w_t > 0.f)
+    b += 2 * round8(P.h) * orda::dtype_size(P.dt);   // hcat: [h_s; h_t] rows for grad_W
   return b;
 }
 
@@ -425,8 +458,9 @@ void attach_split_ws(orda_ctx* c, orda::GemmArgs& g) {
   g.split_ws_bytes = b;
 }
 
+// ms_dev: the deferred-mean scale on the device (LabelStatus::mean_scale).
 void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan plan, int64_t G,
-              float* row3_out, float* scal_dev) {
+              float* row3_out, float* scal_dev, const float* ms_dev) {
   using namespace orda;
   const int64_t cs = plan.chunk_size, nc = plan.num_chunks;
   const int64_t bt = P.bt, v = P.v, h = P.h;
@@ -602,7 +636,8 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       d.b_kmajor = false;
       d.in_type = dt;
       d.epi = GemmEpilogue::StoreF32;
-      d.alpha = P.mean_scale;
+      d.alpha = 1.f;
+      d.alpha_ptr = ms_dev;
       d.group_m = 4;
       d.nprob = 1;
       d.prob[0] = {Gs, in.W.p, in.gh.p + gs * in.gh.ld};
@@ -637,7 +672,8 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       w.b_kmajor = false;
       w.in_type = dt;
       w.epi = first ? GemmEpilogue::StoreF32 : GemmEpilogue::AccumF32;
-      w.alpha = last ? P.mean_scale : 1.f;
+      w.alpha = 1.f;
+      w.alpha_ptr = last ? ms_dev : nullptr;
       w.group_m = 4;
       w.nprob = 1;
       if (tied_tce) {
@@ -682,7 +718,8 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   fa.w_s = P.w_s;
   fa.w_t = P.w_t;
   fa.kd = P.kd;
-  fa.mean_scale = P.mean_scale;
+  fa.mean_scale = 1.f;
+  fa.mean_scale_ptr = ms_dev;
   fa.out = scal_dev;
   timed(c, ORDA_KERNEL_OTHER, [&] { return launch_finalize(fa, c->stream); });
 }
@@ -704,126 +741,139 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
   if (n_labels != bt)
     fail(ORDA_ERR_INVALID, "labels must have length BT=%lld, got %lld", static_cast<long long>(bt),
          static_cast<long long>(n_labels));
-  const std::vector<int64_t> hl = host_labels(c, labels, n_labels, lab_loc);
-  for (int64_t t : hl)
-    if (t != o->ignore_index && (t < 0 || t >= v))
-      fail(ORDA_ERR_INVALID, "label %lld out of range [0, %lld) and != ignore_index %lld",
-           static_cast<long long>(t), static_cast<long long>(v),
-           static_cast<long long>(o->ignore_index));
-  if (!(o->label_smoothing >= 0.f && o->label_smoothing <= 1.f))
-    fail(ORDA_ERR_INVALID, "label_smoothing must be in [0,1], got %s",
-         fmt_f32(o->label_smoothing).c_str());
-  if (o->kd_weight < 0.f)
-    fail(ORDA_ERR_INVALID, "kd_weight must be >= 0, got %s", fmt_f32(o->kd_weight).c_str());
-  if (o->temperature <= 0.f)
-    fail(ORDA_ERR_INVALID, "temperature must be > 0, got %s", fmt_f32(o->temperature).c_str());
-  const int mode = teacher->mode;
-  int64_t ht = h;
-  switch (mode) {
-    case ORDA_TEACHER_TIED:
-      if (teacher->hidden.rows != bt || teacher->hidden.cols != h)
-        fail(ORDA_ERR_INVALID, "Tied teacher hidden must be (%lld, %lld), got (%lld, %lld)",
-             static_cast<long long>(bt), static_cast<long long>(h),
-             static_cast<long long>(teacher->hidden.rows),
-             static_cast<long long>(teacher->hidden.cols));
-      break;
-    case ORDA_TEACHER_SEPARATE:
-      if (teacher->hidden.rows != bt)
-        fail(ORDA_ERR_INVALID, "Separate teacher hidden must have BT=%lld rows",
-             static_cast<long long>(bt));
-      ht = teacher->hidden.cols;
-      if (teacher->weight.rows != v || teacher->weight.cols != ht)
-        fail(ORDA_ERR_INVALID, "Separate teacher weight must be (%lld, %lld), got (%lld, %lld)",
-             static_cast<long long>(v), static_cast<long long>(ht),
-             static_cast<long long>(teacher->weight.rows),
-             static_cast<long long>(teacher->weight.cols));
-      break;
-    case ORDA_TEACHER_PRECOMPUTED:
-      if (teacher->logits.rows != bt || teacher->logits.cols != v)
-        fail(ORDA_ERR_INVALID, "Precomputed teacher logits must be (%lld, %lld), got (%lld, %lld)",
-             static_cast<long long>(bt), static_cast<long long>(v),
-             static_cast<long long>(teacher->logits.rows),
-             static_cast<long long>(teacher->logits.cols));
-      break;
-    default:
-      fail(ORDA_ERR_INVALID, "unknown teacher mode %d", mode);
-  }
-  // ---- backend (api.rs:197-207)
-  if (o->backend == ORDA_BACKEND_CPU)
-    fail(ORDA_ERR_INVALID,
-         "Backend::Cpu is the reference crate's CPU path; liborda_hip serves Backend::Auto and "
-         "Backend::Hip");
-  if (o->backend != ORDA_BACKEND_AUTO && o->backend != ORDA_BACKEND_HIP)
-    fail(ORDA_ERR_INVALID, "unknown backend %d", o->backend);
+  if (!labels) fail(ORDA_ERR_INVALID, "labels is null");
+  // Labels on the host are range-checked here (api.rs:125-133). Labels on the
+  // device are checked by a kernel with the non-ignored count, and the
+  // result is read back with the loss at the end of the call: no wait before
+  // the first kernel. If one of the later checks fails first, the device
+  // labels are read back then, so that a bad label is still the error
+  // reported, as in the reference's order.
+  const bool dev_labels = lab_loc == ORDA_DEVICE;
+  if (!dev_labels) check_labels_host(host_labels(c, labels, n_labels, lab_loc), v, o->ignore_index);
 
   LossPlan P{};
-  P.mode = mode;
-  P.w_s = o->student_ce_weight;
-  P.w_t = o->has_teacher_ce_weight ? o->teacher_ce_weight : (mode == ORDA_TEACHER_TIED ? 1.f : 0.f);
-  if (P.w_t < 0.f)
-    fail(ORDA_ERR_INVALID, "teacher_ce_weight must be >= 0, got %s", fmt_f32(P.w_t).c_str());
-  P.kd = o->kd_weight;
-  P.T = o->temperature;
-  P.ls = o->label_smoothing;
-  P.ignore = o->ignore_index;
-  P.need_teacher = P.kd > 0.f || P.w_t > 0.f;
-  P.has_ght = P.w_t > 0.f && (mode == ORDA_TEACHER_TIED || mode == ORDA_TEACHER_SEPARATE);
-  P.has_gwt = P.w_t > 0.f && mode == ORDA_TEACHER_SEPARATE;
-  int64_t n_valid = 0;
-  for (int64_t t : hl) n_valid += t != P.ignore;
-  const int64_t denom = o->reduction == ORDA_REDUCTION_MEAN ? std::max<int64_t>(n_valid, 1) : 1;
-  P.mean_scale = 1.0f / static_cast<float>(denom);
-  P.bt = bt;
-  P.h = h;
-  P.v = v;
-  P.ht = ht;
-  P.quant = o->config.quantize_grad_weight != 0;
-  P.stochastic = o->config.stochastic_rounding != 0;
-  P.seed = o->config.has_stochastic_seed ? o->config.stochastic_seed : 0;
+  Inputs in;
+  const int mode = teacher->mode;
+  int64_t ht = h;
+  try {
+    if (!(o->label_smoothing >= 0.f && o->label_smoothing <= 1.f))
+      fail(ORDA_ERR_INVALID, "label_smoothing must be in [0,1], got %s",
+           fmt_f32(o->label_smoothing).c_str());
+    if (o->kd_weight < 0.f)
+      fail(ORDA_ERR_INVALID, "kd_weight must be >= 0, got %s", fmt_f32(o->kd_weight).c_str());
+    if (o->temperature <= 0.f)
+      fail(ORDA_ERR_INVALID, "temperature must be > 0, got %s", fmt_f32(o->temperature).c_str());
+    switch (mode) {
+      case ORDA_TEACHER_TIED:
+        if (teacher->hidden.rows != bt || teacher->hidden.cols != h)
+          fail(ORDA_ERR_INVALID, "Tied teacher hidden must be (%lld, %lld), got (%lld, %lld)",
+               static_cast<long long>(bt), static_cast<long long>(h),
+               static_cast<long long>(teacher->hidden.rows),
+               static_cast<long long>(teacher->hidden.cols));
+        break;
+      case ORDA_TEACHER_SEPARATE:
+        if (teacher->hidden.rows != bt)
+          fail(ORDA_ERR_INVALID, "Separate teacher hidden must have BT=%lld rows",
+               static_cast<long long>(bt));
+        ht = teacher->hidden.cols;
+        if (teacher->weight.rows != v || teacher->weight.cols != ht)
+          fail(ORDA_ERR_INVALID, "Separate teacher weight must be (%lld, %lld), got (%lld, %lld)",
+               static_cast<long long>(v), static_cast<long long>(ht),
+               static_cast<long long>(teacher->weight.rows),
+               static_cast<long long>(teacher->weight.cols));
+        break;
+      case ORDA_TEACHER_PRECOMPUTED:
+        if (teacher->logits.rows != bt || teacher->logits.cols != v)
+          fail(ORDA_ERR_INVALID, "Precomputed teacher logits must be (%lld, %lld), got (%lld, %lld)",
+               static_cast<long long>(bt), static_cast<long long>(v),
+               static_cast<long long>(teacher->logits.rows),
+               static_cast<long long>(teacher->logits.cols));
+        break;
+      default:
+        fail(ORDA_ERR_INVALID, "unknown teacher mode %d", mode);
+    }
+    // ---- backend (api.rs:197-207)
+    if (o->backend == ORDA_BACKEND_CPU)
+      fail(ORDA_ERR_INVALID,
+           "Backend::Cpu is the reference crate's CPU path; liborda_hip serves Backend::Auto and "
+           "Backend::Hip");
+    if (o->backend != ORDA_BACKEND_AUTO && o->backend != ORDA_BACKEND_HIP)
+      fail(ORDA_ERR_INVALID, "unknown backend %d", o->backend);
 
-  // ---- dtypes: every float input shares the student's dtype
-  P.dt = to_dtype(sh->dtype, "student_hidden");
-  if (to_dtype(w->dtype, "weight") != P.dt)
-    fail(ORDA_ERR_INVALID, "weight must be %s like student_hidden", dt_name(P.dt));
-  if (P.need_teacher && (mode == ORDA_TEACHER_TIED || mode == ORDA_TEACHER_SEPARATE) &&
-      to_dtype(teacher->hidden.dtype, "teacher hidden") != P.dt)
-    fail(ORDA_ERR_INVALID, "teacher hidden must be %s like student_hidden", dt_name(P.dt));
-  if (P.need_teacher && mode == ORDA_TEACHER_SEPARATE &&
-      to_dtype(teacher->weight.dtype, "teacher weight") != P.dt)
-    fail(ORDA_ERR_INVALID, "teacher weight must be %s like student_hidden", dt_name(P.dt));
+    P.mode = mode;
+    P.w_s = o->student_ce_weight;
+    P.w_t = o->has_teacher_ce_weight ? o->teacher_ce_weight : (mode == ORDA_TEACHER_TIED ? 1.f : 0.f);
+    if (P.w_t < 0.f)
+      fail(ORDA_ERR_INVALID, "teacher_ce_weight must be >= 0, got %s", fmt_f32(P.w_t).c_str());
+    P.kd = o->kd_weight;
+    P.T = o->temperature;
+    P.ls = o->label_smoothing;
+    P.ignore = o->ignore_index;
+    P.need_teacher = P.kd > 0.f || P.w_t > 0.f;
+    P.has_ght = P.w_t > 0.f && (mode == ORDA_TEACHER_TIED || mode == ORDA_TEACHER_SEPARATE);
+    P.has_gwt = P.w_t > 0.f && mode == ORDA_TEACHER_SEPARATE;
+    P.mean = o->reduction == ORDA_REDUCTION_MEAN;
+    P.bt = bt;
+    P.h = h;
+    P.v = v;
+    P.ht = ht;
+    P.quant = o->config.quantize_grad_weight != 0;
+    P.stochastic = o->config.stochastic_rounding != 0;
+    P.seed = o->config.has_stochastic_seed ? o->config.stochastic_seed : 0;
+
+    // ---- dtypes: every float input shares the student's dtype
+    P.dt = to_dtype(sh->dtype, "student_hidden");
+    if (to_dtype(w->dtype, "weight") != P.dt)
+      fail(ORDA_ERR_INVALID, "weight must be %s like student_hidden", dt_name(P.dt));
+    if (P.need_teacher && (mode == ORDA_TEACHER_TIED || mode == ORDA_TEACHER_SEPARATE) &&
+        to_dtype(teacher->hidden.dtype, "teacher hidden") != P.dt)
+      fail(ORDA_ERR_INVALID, "teacher hidden must be %s like student_hidden", dt_name(P.dt));
+    if (P.need_teacher && mode == ORDA_TEACHER_SEPARATE &&
+        to_dtype(teacher->weight.dtype, "teacher weight") != P.dt)
+      fail(ORDA_ERR_INVALID, "teacher weight must be %s like student_hidden", dt_name(P.dt));
+
+    hip_check(hipSetDevice(c->device), "hipSetDevice");
+    // ---- device inputs and outputs
+    in.hs = stage(c, *sh, "in.student", "student_hidden");
+    in.W = stage(c, *w, "in.weight", "weight");
+    if (P.need_teacher && (mode == ORDA_TEACHER_TIED || mode == ORDA_TEACHER_SEPARATE))
+      in.th = stage(c, teacher->hidden, "in.t_hidden", "teacher hidden");
+    if (P.need_teacher && mode == ORDA_TEACHER_SEPARATE)
+      in.tw = stage(c, teacher->weight, "in.t_weight", "teacher weight");
+    if (P.need_teacher && mode == ORDA_TEACHER_PRECOMPUTED) {
+      const orda_tensor& tl = teacher->logits;
+      if (tl.location == ORDA_DEVICE) {
+        check_view(tl, "teacher logits");
+        in.tl.p = tl.data;
+        in.tl.ld = tensor_ld(tl);
+        in.tl.t = to_dtype(tl.dtype, "teacher logits");
+        in.tl.rows = tl.rows;
+        in.tl.cols = tl.cols;
+      } else {
+        in.tl = stage(c, tl, "in.t_logits", "teacher logits");
+      }
+    }
+    in.gh = out_mat(c, out->grad_student_hidden, bt, h, "out.gh", "grad_student_hidden");
+    in.gw = out_mat(c, out->grad_weight, v, h, "out.gw", "grad_weight");
+    if (P.has_ght) in.ght = out_mat(c, out->grad_teacher_hidden, bt, ht, "out.ght", "grad_teacher_hidden");
+    if (P.has_gwt) in.gwt = out_mat(c, out->grad_teacher_weight, v, ht, "out.gwt", "grad_teacher_weight");
+  } catch (const Error& e) {
+    if (dev_labels && e.status == ORDA_ERR_INVALID)
+      check_labels_host(host_labels(c, labels, n_labels, lab_loc), v, o->ignore_index);
+    throw;
+  }
+  in.labels = device_labels(c, labels, n_labels, lab_loc, "in.labels");
+  float* row3 = static_cast<float*>(ws(c, "rows", 3 * bt * 4));
+  // Loss scalars (4 floats) followed by the label status, read back together.
+  char* scal_blk = static_cast<char*>(ws(c, "scalars", 64));
+  float* scal = reinterpret_cast<float*>(scal_blk);
+  LabelStatus* lstat = reinterpret_cast<LabelStatus*>(scal_blk + 16);
+  static_assert(16 + sizeof(LabelStatus) <= 64, "scalar block");
+  hip_check(launch_label_check(in.labels, bt, v, P.ignore, P.mean, lstat, c->stream), "label check");
 
   const orda::ChunkPlan plan0 = resolve_chunk_size(bt, o->chunk_fixed != 0, o->chunk_rows, true, v,
                                                    o->config.has_max_chunks != 0,
                                                    o->config.max_chunks);
-
-  hip_check(hipSetDevice(c->device), "hipSetDevice");
-  // ---- device inputs and outputs
-  Inputs in;
-  in.hs = stage(c, *sh, "in.student", "student_hidden");
-  in.W = stage(c, *w, "in.weight", "weight");
-  if (P.need_teacher && (mode == ORDA_TEACHER_TIED || mode == ORDA_TEACHER_SEPARATE))
-    in.th = stage(c, teacher->hidden, "in.t_hidden", "teacher hidden");
-  if (P.need_teacher && mode == ORDA_TEACHER_SEPARATE)
-    in.tw = stage(c, teacher->weight, "in.t_weight", "teacher weight");
-  if (P.need_teacher && mode == ORDA_TEACHER_PRECOMPUTED) {
-    const orda_tensor& tl = teacher->logits;
-    if (tl.location == ORDA_DEVICE) {
-      in.tl.p = tl.data;
-      in.tl.ld = tensor_ld(tl);
-      in.tl.t = to_dtype(tl.dtype, "teacher logits");
-      in.tl.rows = tl.rows;
-      in.tl.cols = tl.cols;
-    } else {
-      in.tl = stage(c, tl, "in.t_logits", "teacher logits");
-    }
-  }
-  in.labels = device_labels(c, labels, hl, lab_loc, "in.labels");
-  in.gh = out_mat(c, out->grad_student_hidden, bt, h, "out.gh", "grad_student_hidden");
-  in.gw = out_mat(c, out->grad_weight, v, h, "out.gw", "grad_weight");
-  if (P.has_ght) in.ght = out_mat(c, out->grad_teacher_hidden, bt, ht, "out.ght", "grad_teacher_hidden");
-  if (P.has_gwt) in.gwt = out_mat(c, out->grad_teacher_weight, v, ht, "out.gwt", "grad_teacher_weight");
-  float* row3 = static_cast<float*>(ws(c, "rows", 3 * bt * 4));
-  float* scal = static_cast<float*>(ws(c, "scalars", 64));
 
   // ---- chunk plan, staging group, OOM retry (resolver.rs:103-126)
   orda::ChunkPlan plan = plan0;
@@ -832,7 +882,7 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
   int64_t G = std::max<int64_t>(1, std::min<int64_t>(plan.num_chunks, c->staging_budget / std::max<int64_t>(chunk_bytes, 1)));
   for (;;) {
     try {
-      run_loss(c, P, in, plan, G, row3, scal);
+      run_loss(c, P, in, plan, G, row3, scal, &lstat->mean_scale);
       break;
     } catch (const Error& e) {
       if (e.status != ORDA_ERR_OOM) throw;
@@ -926,10 +976,19 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
   deliver(c, out->row_nll_student, row3, bt, 1, 4, "row_nll_student");
   deliver(c, out->row_nll_teacher, row3 + bt, bt, 1, 4, "row_nll_teacher");
   deliver(c, out->row_kl, row3 + 2 * bt, bt, 1, 4, "row_kl");
-  float hs[4];
-  hip_check(hipMemcpyAsync(hs, scal, 16, hipMemcpyDeviceToHost, c->stream), "read loss");
+  // The one wait of the call: loss scalars and label status together.
+  char* hblk = static_cast<char*>(pinned(c, 64));
+  hip_check(hipMemcpyAsync(hblk, scal_blk, 64, hipMemcpyDeviceToHost, c->stream), "read loss");
   hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
   collect_timing(c);
+  float hs[4];
+  LabelStatus ls;
+  memcpy(hs, hblk, 16);
+  memcpy(&ls, hblk + 16, sizeof ls);
+  if (ls.bad_index >= 0)
+    fail(ORDA_ERR_INVALID, "label %lld out of range [0, %lld) and != ignore_index %lld",
+         static_cast<long long>(ls.bad_label), static_cast<long long>(v),
+         static_cast<long long>(P.ignore));
   out->loss = hs[0];
   out->student_ce = hs[1];
   out->teacher_ce = hs[2];
@@ -957,6 +1016,146 @@ orda_ctx* ensure_ctx(orda_ctx* ctx, TempCtx& tmp) {
 }
 
 }  // namespace
+
+namespace orda {
+
+int32_t ctx_device(const orda_ctx* c) { return c->device; }
+
+// kl_ce_on_logits_chunk (src/cuda/launch.rs:51-158): row statistics of both
+// halves of the chunk, then the split row pass. Device logits are read in
+// place at any pitch; host tensors are staged. With `sc`, every tensor must
+// be on the device and the per-row scratch comes from sc instead of the
+// context's workspace (nothing is allocated).
+void kl_ce_slot(orda_ctx* c, const orda_tensor* logits_chunk, const int32_t* targets,
+                int32_t targets_location, int64_t n_rows, float inv_t, float kl_grad_scale,
+                float t_sq, float student_ce_weight, float teacher_ce_weight,
+                float label_smoothing, int32_t ignore_index, int32_t student_only,
+                int32_t compute_kl, orda_tensor* grad_kl_student, orda_tensor* kl_per_row,
+                orda_tensor* grad_ce, orda_tensor* ce_loss, const SlotScratch* sc) {
+  if (!logits_chunk || !grad_kl_student || !kl_per_row || !grad_ce || !ce_loss)
+    fail(ORDA_ERR_INVALID, "null argument");
+  // launch.rs:67-73
+  const int64_t v = logits_chunk->cols;
+  if (n_rows < 0 || v < 1) fail(ORDA_ERR_INVALID, "empty logits_chunk");
+  if (logits_chunk->rows != 2 * n_rows) fail(ORDA_ERR_INVALID, "logits_chunk must be [2*n_rows, V]");
+  if (n_rows > 0 && !targets) fail(ORDA_ERR_INVALID, "targets is null");
+  check_view(*logits_chunk, "logits_chunk");
+  const int64_t grid_rows = student_only ? n_rows : 2 * n_rows;
+  if (sc) {
+    if (n_rows > sc->max_rows)
+      fail(ORDA_ERR_INVALID, "n_rows=%lld exceeds the no-allocation scratch limit of %lld rows",
+           static_cast<long long>(n_rows), static_cast<long long>(sc->max_rows));
+    const orda_tensor* dev_only[] = {logits_chunk, grad_kl_student, kl_per_row, grad_ce, ce_loss};
+    for (const orda_tensor* t : dev_only)
+      if (t->location != ORDA_DEVICE)
+        fail(ORDA_ERR_INVALID, "the no-allocation entry point takes device tensors only");
+    if (targets_location != ORDA_DEVICE)
+      fail(ORDA_ERR_INVALID, "the no-allocation entry point takes device targets only");
+  }
+  hip_check(hipSetDevice(c->device), "hipSetDevice");
+  DMat L;
+  if (logits_chunk->location == ORDA_DEVICE) {
+    L.p = logits_chunk->data;
+    L.ld = tensor_ld(*logits_chunk);
+    L.t = to_dtype(logits_chunk->dtype, "logits_chunk");
+    L.rows = logits_chunk->rows;
+    L.cols = v;
+  } else {
+    L = stage(c, *logits_chunk, "slot.logits", "logits_chunk");
+  }
+  OutMat gk = out_mat(c, *grad_kl_student, n_rows, v, "slot.gkl", "grad_kl_student");
+  OutMat gc = out_mat(c, *grad_ce, grid_rows, v, "slot.gce", "grad_ce");
+  OutMat kr = out_mat(c, *kl_per_row, n_rows, 1, "slot.klr", "kl_per_row");
+  OutMat cl = out_mat(c, *ce_loss, grid_rows, 1, "slot.cel", "ce_loss");
+  if (gk.ld != v || gc.ld != v) fail(ORDA_ERR_INVALID, "gradient outputs must be dense");
+  const int64_t n2 = std::max<int64_t>(1, 2 * n_rows);
+  int64_t* lab;
+  float4* stats;
+  float* xy;
+  float* nll_unused;
+  if (sc) {
+    lab = sc->labels;
+    stats = sc->stats;
+    xy = sc->xy;
+    nll_unused = sc->nll;
+  } else {
+    lab = static_cast<int64_t*>(ws(c, "slot.labels", std::max<int64_t>(1, n_rows) * 8));
+    stats = static_cast<float4*>(ws(c, "slot.stats", n2 * 16));
+    xy = static_cast<float*>(ws(c, "slot.xy", n2 * 4));
+    nll_unused = static_cast<float*>(ws(c, "slot.unused", n2 * 4));
+  }
+  // Targets widened to the kernels' int64 labels on the stream (device
+  // targets), or on the host and uploaded; the label logits start at zero.
+  std::vector<int64_t> hl;   // lives until the stream is synchronized below
+  if (targets_location == ORDA_DEVICE) {
+    hip_check(launch_widen_targets(targets, n_rows, lab, xy, 2 * n_rows, c->stream), "targets");
+  } else {
+    hl.resize(static_cast<size_t>(n_rows));
+    for (int64_t i = 0; i < n_rows; ++i) hl[i] = targets[i];
+    if (n_rows > 0)
+      hip_check(hipMemcpyAsync(lab, hl.data(), n_rows * 8, hipMemcpyHostToDevice, c->stream),
+                "upload targets");
+    hip_check(launch_widen_targets(nullptr, 0, nullptr, xy, 2 * n_rows, c->stream), "targets");
+  }
+  for (int half = 0; half < 2; ++half) {
+    RowStatsArgs r{};
+    r.src_type = L.t;
+    r.src = at(L.p, half * n_rows * L.ld, L.t);
+    r.lds = L.ld;
+    r.dst = nullptr;
+    r.n_rows = n_rows;
+    r.v = v;
+    r.stats = stats + half * n_rows;
+    r.stats_ld = 1;
+    r.xy = xy + half * n_rows;
+    r.labels = lab;
+    r.ignore_index = ignore_index;
+    r.inv_t = inv_t;
+    timed(c, ORDA_KERNEL_OTHER, [&] { return launch_row_stats(r, c->stream); });
+  }
+  RowPassArgs a{};
+  a.ltype = L.t;
+  a.student = const_cast<void*>(L.p);
+  a.teacher = at(L.p, n_rows * L.ld, L.t);
+  a.ld = L.ld;
+  a.n_rows = n_rows;
+  a.v = v;
+  a.stats_s = stats;
+  a.stats_t = stats + n_rows;
+  a.stats_ld = 1;
+  a.stats_tiles = 1;
+  a.stats_tiles_t = 1;
+  a.xy_s = xy;
+  a.xy_t = xy + n_rows;
+  a.labels = lab;
+  a.ignore_index = ignore_index;
+  a.w_s = student_ce_weight;
+  a.w_t = teacher_ce_weight;
+  a.kd = 0.f;
+  a.temperature = 1.f / inv_t;
+  a.label_smoothing = label_smoothing;
+  a.kl = compute_kl != 0;
+  a.row_nll_s = nll_unused;
+  a.row_nll_t = nll_unused + n_rows;
+  a.row_kl = kr.p;
+  a.split = true;
+  a.grad_kl = gk.p;
+  a.grad_ce = gc.p;
+  a.ce_loss = cl.p;
+  a.kl_grad_scale = kl_grad_scale;
+  a.t_sq = t_sq;
+  a.inv_t = inv_t;
+  a.student_only = student_only != 0;
+  timed(c, ORDA_KERNEL_ROW_PASS, [&] { return launch_row_pass(a, c->stream); });
+  download(c, gk);
+  download(c, gc);
+  download(c, kr);
+  download(c, cl);
+  hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  collect_timing(c);
+}
+
+}  // namespace orda
 
 extern "C" {
 
@@ -1063,6 +1262,12 @@ int32_t orda_ctx_set_staging_budget(orda_ctx* c, int64_t bytes) {
   return ORDA_OK;
 }
 
+int32_t orda_ctx_workspace_bytes(orda_ctx* c, int64_t* bytes) {
+  if (!c || !bytes) return ORDA_ERR_INVALID;
+  *bytes = c->held;
+  return ORDA_OK;
+}
+
 int32_t orda_ctx_trim(orda_ctx* c) {
   if (!c) return ORDA_ERR_INVALID;
   (void)hipSetDevice(c->device);
@@ -1121,98 +1326,13 @@ int32_t orda_kl_ce_on_logits_chunk(orda_ctx* ctx, const orda_tensor* logits_chun
                                    orda_tensor* grad_kl_student, orda_tensor* kl_per_row,
                                    orda_tensor* grad_ce, orda_tensor* ce_loss, char* err,
                                    size_t err_len) {
-  using namespace orda;
   TempCtx tmp;
   try {
     orda_ctx* c = ensure_ctx(ctx, tmp);
-    if (!logits_chunk || !grad_kl_student || !kl_per_row || !grad_ce || !ce_loss)
-      fail(ORDA_ERR_INVALID, "null argument");
-    // launch.rs:67-73
-    const int64_t v = logits_chunk->cols;
-    if (logits_chunk->rows != 2 * n_rows) fail(ORDA_ERR_INVALID, "logits_chunk must be [2*n_rows, V]");
-    if (n_rows < 0 || v < 1) fail(ORDA_ERR_INVALID, "empty logits_chunk");
-    hip_check(hipSetDevice(c->device), "hipSetDevice");
-    const DMat L = stage(c, *logits_chunk, "slot.logits", "logits_chunk");
-    std::vector<int64_t> hl(static_cast<size_t>(n_rows));
-    {
-      std::vector<int32_t> t32(static_cast<size_t>(n_rows));
-      if (n_rows > 0) {
-        if (!targets) fail(ORDA_ERR_INVALID, "targets is null");
-        if (targets_location == ORDA_DEVICE) {
-          hip_check(hipMemcpy(t32.data(), targets, n_rows * 4, hipMemcpyDeviceToHost), "read targets");
-        } else {
-          memcpy(t32.data(), targets, n_rows * 4);
-        }
-      }
-      for (int64_t i = 0; i < n_rows; ++i) hl[i] = t32[i];
-    }
-    const int64_t* lab = device_labels(c, nullptr, hl, ORDA_HOST, "slot.labels");
-    const int64_t grid_rows = student_only ? n_rows : 2 * n_rows;
-    OutMat gk = out_mat(c, *grad_kl_student, n_rows, v, "slot.gkl", "grad_kl_student");
-    OutMat gc = out_mat(c, *grad_ce, grid_rows, v, "slot.gce", "grad_ce");
-    OutMat kr = out_mat(c, *kl_per_row, n_rows, 1, "slot.klr", "kl_per_row");
-    OutMat cl = out_mat(c, *ce_loss, grid_rows, 1, "slot.cel", "ce_loss");
-    if (gk.ld != v || gc.ld != v) fail(ORDA_ERR_INVALID, "gradient outputs must be dense");
-    float4* stats = static_cast<float4*>(ws(c, "slot.stats", std::max<int64_t>(1, 2 * n_rows) * 16));
-    float* xy = static_cast<float*>(ws(c, "slot.xy", std::max<int64_t>(1, 2 * n_rows) * 4));
-    hip_check(hipMemsetAsync(xy, 0, std::max<int64_t>(1, 2 * n_rows) * 4, c->stream), "hipMemsetAsync");
-    for (int half = 0; half < 2; ++half) {
-      RowStatsArgs r{};
-      r.src_type = L.t;
-      r.src = at(L.p, half * n_rows * L.ld, L.t);
-      r.lds = L.ld;
-      r.dst = nullptr;
-      r.n_rows = n_rows;
-      r.v = v;
-      r.stats = stats + half * n_rows;
-      r.stats_ld = 1;
-      r.xy = xy + half * n_rows;
-      r.labels = lab;
-      r.ignore_index = ignore_index;
-      r.inv_t = inv_t;
-      timed(c, ORDA_KERNEL_OTHER, [&] { return launch_row_stats(r, c->stream); });
-    }
-    float* nll_t_unused = static_cast<float*>(ws(c, "slot.unused", std::max<int64_t>(1, n_rows) * 8));
-    RowPassArgs a{};
-    a.ltype = L.t;
-    a.student = const_cast<void*>(L.p);
-    a.teacher = at(L.p, n_rows * L.ld, L.t);
-    a.ld = L.ld;
-    a.n_rows = n_rows;
-    a.v = v;
-    a.stats_s = stats;
-    a.stats_t = stats + n_rows;
-    a.stats_ld = 1;
-    a.stats_tiles = 1;
-    a.stats_tiles_t = 1;
-    a.xy_s = xy;
-    a.xy_t = xy + n_rows;
-    a.labels = lab;
-    a.ignore_index = ignore_index;
-    a.w_s = student_ce_weight;
-    a.w_t = teacher_ce_weight;
-    a.kd = 0.f;
-    a.temperature = 1.f / inv_t;
-    a.label_smoothing = label_smoothing;
-    a.kl = compute_kl != 0;
-    a.row_nll_s = nll_t_unused;
-    a.row_nll_t = nll_t_unused + n_rows;
-    a.row_kl = kr.p;
-    a.split = true;
-    a.grad_kl = gk.p;
-    a.grad_ce = gc.p;
-    a.ce_loss = cl.p;
-    a.kl_grad_scale = kl_grad_scale;
-    a.t_sq = t_sq;
-    a.inv_t = inv_t;
-    a.student_only = student_only != 0;
-    timed(c, ORDA_KERNEL_ROW_PASS, [&] { return launch_row_pass(a, c->stream); });
-    download(c, gk);
-    download(c, gc);
-    download(c, kr);
-    download(c, cl);
-    hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    collect_timing(c);
+    orda::kl_ce_slot(c, logits_chunk, targets, targets_location, n_rows, inv_t, kl_grad_scale,
+                     t_sq, student_ce_weight, teacher_ce_weight, label_smoothing, ignore_index,
+                     student_only, compute_kl, grad_kl_student, kl_per_row, grad_ce, ce_loss,
+                     nullptr);
     return ORDA_OK;
   } catch (const Error& e) {
     copy_err(e, err, err_len);
@@ -1238,8 +1358,7 @@ int32_t orda_quant_rows_int8(orda_ctx* ctx, const orda_tensor* m, const int64_t*
     const int64_t rows = m->rows, cols = m->cols;
     const DMat src = stage(c, *m, "q.src", "m");
     OutMat o = out_mat(c, *outp, rows, cols, "q.out", "out");
-    const std::vector<int64_t> hl = host_labels(c, targets, n_targets, targets_location);
-    const int64_t* lab = device_labels(c, targets, hl, targets_location, "q.labels");
+    const int64_t* lab = device_labels(c, targets, n_targets, targets_location, "q.labels");
     uint8_t* keep = static_cast<uint8_t*>(ws(c, "q.keep", std::max<int64_t>(rows, 1)));
     hip_check(hipMemsetAsync(keep, 0, std::max<int64_t>(rows, 1), c->stream), "hipMemsetAsync");
     hip_check(launch_mark_targets(lab, n_targets, ignore_index, keep, rows, c->stream), "mark targets");

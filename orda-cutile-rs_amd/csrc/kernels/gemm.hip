@@ -1101,6 +1101,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
   const int lgrp = lane >> 4;
   if constexpr (EPI == GemmEpilogue::StoreF32 || EPI == GemmEpilogue::AccumF32) {
     float* C = static_cast<float*>(pr.c);
+    const float alpha = g.alpha_ptr != nullptr ? g.alpha * *g.alpha_ptr : g.alpha;
     if constexpr (!kSwapAB) {
       // acc[i][j][e] is row wm*128 + 16i + 4*lgrp + e, column wn*128 + 16j + lrow.
       const int row_w = tc.m0 + wm * 128;
@@ -1117,8 +1118,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
             const int64_t col = col_l + j * 16;
             if (col < g.N) {
               float v = acc[i][j][e];
-              if constexpr (EPI == GemmEpilogue::AccumF32) v = g.alpha * (crow[col] + v);
-              else v = g.alpha * v;
+              if constexpr (EPI == GemmEpilogue::AccumF32) v = alpha * (crow[col] + v);
+              else v = alpha * v;
               crow[col] = v;
             }
           }
@@ -1142,16 +1143,16 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         f32x4 v = acc[i][j];
         if (vec && col + 4 <= g.N) {
           f32x4* dst = reinterpret_cast<f32x4*>(crow + j * 16);
-          if constexpr (EPI == GemmEpilogue::AccumF32) v = g.alpha * (*dst + v);
-          else v = g.alpha * v;
+          if constexpr (EPI == GemmEpilogue::AccumF32) v = alpha * (*dst + v);
+          else v = alpha * v;
           *dst = v;
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             if (col + e < g.N) {
               float x = v[e];
-              if constexpr (EPI == GemmEpilogue::AccumF32) x = g.alpha * (crow[j * 16 + e] + x);
-              else x = g.alpha * x;
+              if constexpr (EPI == GemmEpilogue::AccumF32) x = alpha * (crow[j * 16 + e] + x);
+              else x = alpha * x;
               crow[j * 16 + e] = x;
             }
           }
@@ -1494,7 +1495,8 @@ GemmKernel select_kernel(const GemmArgs& g) {
 // accumulating), the partials summed in split order.
 __global__ void splitk_reduce_kernel(const float* ws, int64_t stride, int splits, int64_t M,
                                      int64_t N, int64_t ldp, float* c0, float* c1, int64_t ldc,
-                                     float alpha, bool accum) {
+                                     float alpha0, const float* alpha_ptr, bool accum) {
+  const float alpha = alpha_ptr != nullptr ? alpha0 * *alpha_ptr : alpha0;
   const int64_t per = M * N;
   const int64_t total = per * (c1 ? 2 : 1);
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
@@ -1567,6 +1569,7 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
     GemmArgs s = g;
     s.epi = GemmEpilogue::StoreF32;
     s.alpha = 1.f;
+    s.alpha_ptr = nullptr;
     s.ldc = sp.ldp;
     s.split_k = sp.splits;
     s.split_len = sp.len;
@@ -1581,7 +1584,7 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, g.split_ws,
                        sp.stride, sp.splits, g.M, g.N, sp.ldp, static_cast<float*>(g.prob[0].c),
                        g.nprob > 1 ? static_cast<float*>(g.prob[1].c) : nullptr, g.ldc, g.alpha,
-                       g.epi == GemmEpilogue::AccumF32);
+                       g.alpha_ptr, g.epi == GemmEpilogue::AccumF32);
     return hipGetLastError();
   }
   GemmArgs one = g;

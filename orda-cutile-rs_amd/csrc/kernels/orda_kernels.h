@@ -64,6 +64,9 @@ struct GemmArgs {
   DType logits_type;      // dtype of C for the Logits epilogue
   GemmEpilogue epi;
   float alpha;
+  // When set, the epilogue scales by alpha * *alpha_ptr (a device value, e.g.
+  // the deferred mean computed on the device by launch_label_check).
+  const float* alpha_ptr;
   int group_m;            // M-tiles per raster group (L2 reuse of B)
   LogitStatsArgs lg;
   // Split-K workspace for Store/Accum GEMMs with fewer tiles than CUs: when
@@ -173,6 +176,7 @@ struct FinalizeArgs {
   int64_t chunk_size;      // KL is summed per chunk then rounded to f32
   float w_s, w_t, kd;
   float mean_scale;
+  const float* mean_scale_ptr;   // when set, *mean_scale_ptr replaces mean_scale
   float* out;              // 4 floats
 };
 hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t stream);
@@ -193,6 +197,26 @@ struct QuantArgs {
   float grad_output;
 };
 hipError_t launch_quant(const QuantArgs& a, hipStream_t stream);
+
+// Label validation on the device (src/api.rs:125-133) and the deferred-mean
+// scale (src/api.rs:225-230): n_valid counts labels != ignore_index; the
+// first label (lowest index) that is neither ignore_index nor in [0, v) is
+// reported with its value (bad_index -1: none); mean_scale =
+// 1 / max(n_valid, 1) as f32 for the Mean reduction, 1 for Sum.
+struct LabelStatus {
+  int64_t n_valid;
+  int64_t bad_index;
+  int64_t bad_label;
+  float mean_scale;
+  float pad;
+};
+hipError_t launch_label_check(const int64_t* labels, int64_t n, int64_t v, int64_t ignore_index,
+                              bool mean, LabelStatus* out, hipStream_t stream);
+
+// out64[i] = in32[i] for i < n, and zero[i] = 0 for i < n_zero (the targets of
+// the chunk-launcher entry point widened to the kernels' int64 labels).
+hipError_t launch_widen_targets(const int32_t* in32, int64_t n, int64_t* out64, float* zero,
+                                int64_t n_zero, hipStream_t stream);
 
 // keep[labels[i]] = 1 for every in-range, non-ignored label.
 hipError_t launch_mark_targets(const int64_t* labels, int64_t n, int64_t ignore_index,

@@ -158,6 +158,60 @@ __global__ void mark_targets_kernel(const int64_t* labels, int64_t n, int64_t ig
   }
 }
 
+// One workgroup: the label count, the first invalid label and the mean
+// scale, reduced over the block (no atomics, nothing to clear beforehand).
+constexpr int kCheckThreads = 1024;
+__global__ __launch_bounds__(kCheckThreads) void label_check_kernel(const int64_t* labels, int64_t n,
+                                                                    int64_t v, int64_t ignore,
+                                                                    bool mean, LabelStatus* out) {
+  __shared__ int64_t cnt[kCheckThreads / 64], first[kCheckThreads / 64];
+  int64_t c = 0, f = INT64_MAX;
+  for (int64_t i = threadIdx.x; i < n; i += kCheckThreads) {
+    const int64_t t = labels[i];
+    if (t != ignore) {
+      ++c;
+      if ((t < 0 || t >= v) && i < f) f = i;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    c += __shfl_xor(c, o);
+    const int64_t g = __shfl_xor(f, o);
+    f = g < f ? g : f;
+  }
+  if ((threadIdx.x & 63) == 0) {
+    cnt[threadIdx.x >> 6] = c;
+    first[threadIdx.x >> 6] = f;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    c = 0;
+    f = INT64_MAX;
+    for (int w = 0; w < kCheckThreads / 64; ++w) {
+      c += cnt[w];
+      f = first[w] < f ? first[w] : f;
+    }
+    LabelStatus s;
+    s.n_valid = c;
+    s.bad_index = f == INT64_MAX ? -1 : f;
+    s.bad_label = f == INT64_MAX ? 0 : labels[f];
+    const int64_t denom = mean ? (c > 1 ? c : 1) : 1;
+    s.mean_scale = 1.0f / static_cast<float>(denom);   // api.rs:230
+    s.pad = 0.f;
+    *out = s;
+  }
+}
+
+__global__ void widen_targets_kernel(const int32_t* in32, int64_t n, int64_t* out64, float* zero,
+                                     int64_t n_zero) {
+  const int64_t total = n > n_zero ? n : n_zero;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    if (i < n) out64[i] = in32[i];
+    if (i < n_zero) zero[i] = 0.f;
+  }
+}
+
 template <typename S, typename D>
 __global__ void convert_rows_kernel(const S* src, int64_t lds, D* dst, int64_t ldd, int64_t rows,
                                     int64_t cols) {
@@ -198,6 +252,22 @@ hipError_t launch_mark_targets(const int64_t* labels, int64_t n, int64_t ignore_
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(mark_targets_kernel, dim3(grid_for(n)), dim3(256), 0, s, labels, n,
                      ignore_index, keep, rows);
+  return hipGetLastError();
+}
+
+hipError_t launch_label_check(const int64_t* labels, int64_t n, int64_t v, int64_t ignore_index,
+                              bool mean, LabelStatus* out, hipStream_t s) {
+  hipLaunchKernelGGL(label_check_kernel, dim3(1), dim3(kCheckThreads), 0, s, labels, n, v,
+                     ignore_index, mean, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_widen_targets(const int32_t* in32, int64_t n, int64_t* out64, float* zero,
+                                int64_t n_zero, hipStream_t s) {
+  const int64_t total = n > n_zero ? n : n_zero;
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(widen_targets_kernel, dim3(grid_for(total)), dim3(256), 0, s, in32, n, out64,
+                     zero, n_zero);
   return hipGetLastError();
 }
 

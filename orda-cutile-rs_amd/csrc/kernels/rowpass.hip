@@ -156,6 +156,15 @@ struct Vec<__bf16> {
   }
 };
 
+// lse_s^T - lse_t^T of two rows from their merged statistics, as
+// (m_s - m_t)/T + log(dT_s / dT_t): the maxima are logits, so their
+// difference is exact when they are close, and the log of a ratio near 1
+// keeps the small KL of nearly equal rows (where lse_s^T and lse_t^T agree
+// to many digits) from being swamped by the rounding of two O(|lse|) logs.
+__device__ __forceinline__ float lse_t_diff(const Stat& s, const Stat& t, float inv_t) {
+  return (s.m - t.m) * inv_t + logf(s.dT / t.dT);
+}
+
 // nll of cross_entropy.rs:46-56 from merged stats, in f64.
 __device__ __forceinline__ double row_nll(const Stat& s, float xy, double alpha, int64_t v) {
   const double lse = static_cast<double>(s.m) + log(static_cast<double>(s.d1));
@@ -172,7 +181,9 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(RowPassArgs a) {
   const int64_t r = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t y = a.labels[r];
-  const bool ignored = (y == a.ignore_index);
+  // A label outside [0, V) that is not ignore_index is an error the host
+  // reports; the row is then treated as ignored so no access leaves the row.
+  const bool ignored = y == a.ignore_index || y < 0 || y >= a.v;
   const bool has_t = a.teacher != nullptr;
   const float T = a.temperature;
   const float inv_t = SPLIT ? a.inv_t : 1.0f / T;
@@ -210,10 +221,25 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(RowPassArgs a) {
   constexpr int NV = VT::N;
   float cross = 0.f, sum_pt = 0.f;
   const int64_t vpad = (a.v + NV - 1) / NV * NV;
+  // Rows are read where they are, at any pitch: 16-byte vectors where the
+  // row is 16-byte aligned and the vector lies inside the row, single
+  // elements otherwise (nothing past column V is read).
+  const bool vec = (reinterpret_cast<uintptr_t>(srow) & 15) == 0 &&
+                   (!has_t || (reinterpret_cast<uintptr_t>(trow) & 15) == 0);
   for (int64_t j0 = static_cast<int64_t>(tid) * NV; j0 < vpad; j0 += kThreads * NV) {
     float xs[NV], xt[NV], gs[NV], gt[NV];
-    VT::unpack(*reinterpret_cast<const typename VT::raw*>(srow + j0), xs);
-    if (has_t) VT::unpack(*reinterpret_cast<const typename VT::raw*>(trow + j0), xt);
+    const bool whole = vec && j0 + NV <= a.v;
+    if (whole) {
+      VT::unpack(*reinterpret_cast<const typename VT::raw*>(srow + j0), xs);
+      if (has_t) VT::unpack(*reinterpret_cast<const typename VT::raw*>(trow + j0), xt);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const bool in = j0 + i < a.v;
+        xs[i] = in ? static_cast<float>(srow[j0 + i]) : 0.f;
+        xt[i] = in && has_t ? static_cast<float>(trow[j0 + i]) : 0.f;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int64_t j = j0 + i;
@@ -250,8 +276,17 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(RowPassArgs a) {
       }
     }
     if (!SPLIT) {
-      *reinterpret_cast<typename VT::raw*>(srow + j0) = VT::pack(gs);
-      if (do_tgrad) *reinterpret_cast<typename VT::raw*>(trow + j0) = VT::pack(gt);
+      if (whole) {
+        *reinterpret_cast<typename VT::raw*>(srow + j0) = VT::pack(gs);
+        if (do_tgrad) *reinterpret_cast<typename VT::raw*>(trow + j0) = VT::pack(gt);
+      } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          if (j0 + i >= a.v) break;
+          srow[j0 + i] = static_cast<LT>(gs[i]);
+          if (do_tgrad) trow[j0 + i] = static_cast<LT>(gt[i]);
+        }
+      }
     }
   }
   if (SPLIT && !do_kl && a.grad_kl) {
@@ -268,7 +303,7 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(RowPassArgs a) {
     float kl_row = 0.f;
     if (do_kl && !ignored) {
       const float t_sq = SPLIT ? a.t_sq : T * T;   // kl.rs:86
-      kl_row = (cross * inv_t + (lseT_s - lseT_t) * sum_pt) * t_sq;
+      kl_row = (cross * inv_t + lse_t_diff(ss, st, inv_t) * sum_pt) * t_sq;
     }
     double nll_t = 0.0;
     const bool tce = SPLIT ? (!a.student_only && has_t) : (a.teacher_ce && has_t);
@@ -352,7 +387,9 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
   GT* gsrow = static_cast<GT*>(a.grad_s ? a.grad_s : a.student) + r * a.ld;
   GT* gtrow = TG ? static_cast<GT*>(a.grad_s ? a.grad_t : a.teacher) + r * a.ld : nullptr;
 
-  if (y == a.ignore_index) {   // cross_entropy.rs:59, kl.rs:92: zero gradient and losses
+  // cross_entropy.rs:59, kl.rs:92: zero gradient and losses (also for a
+  // label outside [0, V), which the host reports as an error).
+  if (y == a.ignore_index || y < 0 || y >= v) {
     const float z[NV] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int vi = tid; vi < nvec; vi += kThreads) {
       store8(gsrow + static_cast<int64_t>(vi) * NV, z);
@@ -498,9 +535,9 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
     a.row_nll_s[r] = static_cast<float>(row_nll(ss, a.xy_s[r], alpha, v));
     float kl_row = 0.f;
     if (KL && a.cross != nullptr)
-      kl_row = ((xc / st.dT) * inv_t + (lseT_s - lseT_t)) * (T * T);
+      kl_row = ((xc / st.dT) * inv_t + lse_t_diff(ss, st, inv_t)) * (T * T);
     else if (KL)
-      kl_row = ((cross / gsc) * inv_t + (lseT_s - lseT_t) * (sum_c / gsc)) * (T * T);
+      kl_row = ((cross / gsc) * inv_t + lse_t_diff(ss, st, inv_t) * (sum_c / gsc)) * (T * T);
     a.row_kl[r] = kl_row;
     a.row_nll_t[r] = a.teacher_ce ? static_cast<float>(row_nll(st, a.xy_t[r], alpha, v)) : 0.f;
   }
@@ -526,7 +563,7 @@ __global__ __launch_bounds__(kThreads) void row_consts_kernel(RowPassArgs a) {
   const int64_t r = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
   if (r >= a.n_rows) return;
   const int64_t y = a.labels[r];
-  if (y == a.ignore_index) {   // cross_entropy.rs:59, kl.rs:92
+  if (y == a.ignore_index || y < 0 || y >= a.v) {   // cross_entropy.rs:59, kl.rs:92
     if (lane == 0) {
       a.row_nll_s[r] = 0.f;
       a.row_nll_t[r] = 0.f;
@@ -585,7 +622,7 @@ __global__ __launch_bounds__(kThreads) void row_consts_kernel(RowPassArgs a) {
     k.w = TG ? log2f(a.w_t) - lse1_t * kLog2e : 0.f;
     a.row_consts[r] = k;
     a.row_nll_s[r] = static_cast<float>(row_nll(ss, a.xy_s[r], alpha, a.v));
-    a.row_kl[r] = KL ? ((xc / st.dT) * inv_t + (lseT_s - lseT_t)) * (T * T) : 0.f;
+    a.row_kl[r] = KL ? ((xc / st.dT) * inv_t + lse_t_diff(ss, st, inv_t)) * (T * T) : 0.f;
     a.row_nll_t[r] = a.teacher_ce ? static_cast<float>(row_nll(st, a.xy_t[r], alpha, a.v)) : 0.f;
   }
 }
@@ -605,7 +642,7 @@ __global__ __launch_bounds__(kThreads) void row_grad_kernel(RowPassArgs a, int64
   const int64_t v = a.v;
   __bf16* srow = static_cast<__bf16*>(a.student) + r * a.ld;
   __bf16* trow = (KL || TG) ? static_cast<__bf16*>(a.teacher) + r * a.ld : nullptr;
-  if (y == a.ignore_index) {   // zero gradient rows
+  if (y == a.ignore_index || y < 0 || y >= v) {   // zero gradient rows
     const float z[NV] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int q = 0; q < kChunkVec; ++q) {
@@ -731,7 +768,7 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(FinalizeArgs a) {
     __syncthreads();
   }
   if (threadIdx.x == 0) {
-    const double ms = static_cast<double>(a.mean_scale);
+    const double ms = static_cast<double>(a.mean_scale_ptr ? *a.mean_scale_ptr : a.mean_scale);
     const double S = red[0][0], Tt = red[1][0], K = red[2][0];
     a.out[0] = static_cast<float>((static_cast<double>(a.w_s) * S +
                                    static_cast<double>(a.w_t) * Tt +
@@ -755,15 +792,15 @@ __global__ void zero_pad_kernel(T* base, int64_t ld, int64_t n_rows, int64_t v) 
 
 hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
   if (a.n_rows <= 0) return hipSuccess;
-  if (a.ld % 8) return hipErrorInvalidValue;
   dim3 grid(static_cast<unsigned>(a.n_rows));
-  if (a.split) {
+  if (a.split) {   // any pitch and alignment
     if (a.ltype == DType::BF16)
       hipLaunchKernelGGL((row_pass_kernel<__bf16, true>), grid, dim3(kThreads), 0, s, a);
     else
       hipLaunchKernelGGL((row_pass_kernel<float, true>), grid, dim3(kThreads), 0, s, a);
     return hipGetLastError();
   }
+  if (a.ld % 8) return hipErrorInvalidValue;
   const bool has_t = a.teacher != nullptr;
   const bool kl = a.kl && has_t;
   const bool tg = a.teacher_grad && has_t;

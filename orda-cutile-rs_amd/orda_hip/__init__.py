@@ -202,6 +202,12 @@ class Context:
     def trim(self):
         self._lib.orda_ctx_trim(self.handle)
 
+    def workspace_bytes(self) -> int:
+        """Device bytes the context's workspace holds."""
+        n = C.c_int64()
+        self._lib.orda_ctx_workspace_bytes(self.handle, C.byref(n))
+        return n.value
+
     def set_timing(self, on: bool):
         self._lib.orda_ctx_set_timing(self.handle, int(on))
 

@@ -90,6 +90,7 @@ SIGNATURES = [
     ("orda_ctx_set_memory_limit", C.c_int32, [C.c_void_p, C.c_int64]),
     ("orda_ctx_set_staging_budget", C.c_int32, [C.c_void_p, C.c_int64]),
     ("orda_ctx_trim", C.c_int32, [C.c_void_p]),
+    ("orda_ctx_workspace_bytes", C.c_int32, [C.c_void_p, C.POINTER(C.c_int64)]),
     ("orda_ctx_set_timing", C.c_int32, [C.c_void_p, C.c_int32]),
     ("orda_ctx_get_kernel_time", C.c_int32,
      [C.c_void_p, C.c_int32, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),

@@ -19,7 +19,8 @@ import pytest
 
 import oracle as O
 from helpers import bf16_round, normal, uniform_labels
-from parity import check_grad, check_output, check_quantized_grad_weight, to_np
+from parity import (check_grad, check_output, check_quant_of_own_gradient,
+                    check_quantized_grad_weight, to_np)
 
 import orda_hip as H
 from orda_hip import ChunkSize, KernelConfig, LossOptions, Teacher
@@ -165,13 +166,19 @@ def test_stochastic_int8_through_the_path(torch_dev, dtype):
     cfg = KernelConfig(quantize_grad_weight=True, stochastic_rounding=True, stochastic_seed=987)
     opts = LossOptions(kd_weight=0.4, temperature=1.5, label_smoothing=0.1, config=cfg,
                        chunk_size=ChunkSize.Fixed(64))
-    got = H.distillation_loss(dev(torch_dev, s, dtype), dev(torch_dev, w, dtype),
-                              dev(torch_dev, y), Teacher.Tied(dev(torch_dev, th, dtype)), opts,
-                              quant_codes=True)
+    args = (dev(torch_dev, s, dtype), dev(torch_dev, w, dtype), dev(torch_dev, y),
+            Teacher.Tied(dev(torch_dev, th, dtype)))
+    got = H.distillation_loss(*args, opts, quant_codes=True)
+    plain_opts = LossOptions(kd_weight=0.4, temperature=1.5, label_smoothing=0.1,
+                             chunk_size=ChunkSize.Fixed(64))
+    plain = H.distillation_loss(*args, plain_opts)
+    check_quant_of_own_gradient(got, plain.grad_weight, y, stochastic=True, seed=987)
     ref = O.distillation_loss(s, w, y, Teacher.Tied(th), opts)
     if dtype is None:
+        ref_plain = O.distillation_loss(s, w, y, Teacher.Tied(th), plain_opts)
         check_output(got, ref, skip_grad_weight=True)
-        check_quantized_grad_weight(got, ref, y)
+        check_quantized_grad_weight(got, ref, y, plain.grad_weight, ref_plain.grad_weight,
+                                    stochastic=True, seed=987)
     else:
         check_output(got, ref, kind="bf16", skip_grad_weight=True)
         check_grad("grad_weight (dequantized)", to_np(got.grad_weight), ref.grad_weight, "bf16")

@@ -8,11 +8,16 @@ pinned to the oracle at small sizes on the CPU) run on the same GPU.
 Tolerances as in tests/parity.py (loss terms 1e-4, bf16 gradients 2e-2).
 Size-independent properties of the INT8 result are checked besides: codes
 within ±127, every non-target row reaching ±127 at its largest element, and
-non-target rows of the returned grad_W equal to code x scale exactly.
+non-target rows of the returned grad_W equal to code x scale exactly. The
+INT8 step itself is pinned end to end: the same call with quantization off
+gives the fp32 grad_W that the quantized call quantized, and quantizing it
+with orda_quant_rows_int8 (bit-exact against the oracle's quantizer) must
+give identical codes, scales and dequantized rows (src/api.rs:380-399).
 """
 import pytest
 
-from parity import check_grad_device, check_scalar
+from parity import (check_grad_device, check_quant_of_own_gradient,
+                    check_quantized_vs_reference_device, check_scalar)
 from torch_reference import loss_tied_chunked
 
 import orda_hip as H
@@ -62,6 +67,13 @@ def test_tied_bf16_int8_full_benchmark_shape():
     assert bool((codes[other].abs().amax(1) == 127).all())
     assert torch.equal(got.grad_weight[other], codes[other].float() * scales[other, None])
 
+    print("quantization off: same call", flush=True)
+    plain_opts = LossOptions(kd_weight=0.4, temperature=1.5, label_smoothing=0.1)
+    plain = H.distillation_loss(hs, w, y, Teacher.Tied(ht), plain_opts)
+    check_quant_of_own_gradient(
+        got, plain.grad_weight, y,
+        quant=lambda m, t: H.quant_rows_int8(m, t, -100, False, 0))
+
 
 FP32_WORKLOADS = ["tied-2048x4096x32000-f32", "separate-4096x2048x4096x32000-f32",
                   "precomputed-4096x4096x65536-f32"]
@@ -101,3 +113,20 @@ def test_fp32_workloads_full_shape(name):
         if r is not None:
             rel[k] = check_grad_device(k, g, r, "f32")
     print("relative errors:", {k: f"{e:.2e}" for k, e in rel.items()})
+    if mode == "tied":
+        # The INT8 clause of the gate at this fp32 shape: the quantized call
+        # quantizes its own fp32 grad_W exactly, and its codes and scales
+        # meet the gate against the reference's fp32 grad_W quantized by
+        # orda_quant_rows_int8 (bit-exact against the oracle's quantizer).
+        import dataclasses
+        qopts = dataclasses.replace(opts, config=dataclasses.replace(opts.config,
+                                                                      quantize_grad_weight=True))
+        print("quantized call", flush=True)
+        q = H.distillation_loss(s, w, y, bench.teacher_obj(H, t), qopts, quant_codes=True)
+
+        def quant(m, tg):
+            return H.quant_rows_int8(m, tg, -100, False, 0)
+        check_quant_of_own_gradient(q, got.grad_weight, y, quant=quant)
+        _, rq, rs = quant(ref["grad_weight"], y)
+        flips = check_quantized_vs_reference_device(q, got.grad_weight, ref["grad_weight"], rq, rs)
+        print(f"INT8 codes differing at rounding boundaries: {flips} of {v * h}")

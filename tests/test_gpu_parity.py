@@ -6,12 +6,15 @@ shapes that exercise every tail and padding path), the Tied
 256/512/8192 fp32 shape in full, and reduced versions of the four larger
 shapes (same mode, dtype and options; sizes the oracle finishes in seconds).
 """
+import dataclasses
+
 import numpy as np
 import pytest
 
 import oracle as O
 from helpers import bf16_round, labels, mat, normal, uniform_labels
-from parity import check_grad, check_output, check_quantized_grad_weight, check_scalar, to_np
+from parity import (check_grad, check_output, check_quant_of_own_gradient,
+                    check_quantized_grad_weight, check_scalar, to_np)
 
 import orda_hip as H
 from orda_hip import (ChunkSize, KernelConfig, LossOptions, OrdaError, Reduction, Teacher)
@@ -64,6 +67,20 @@ def base_opts(**kw):
     d = dict(student_ce_weight=1.0, kd_weight=0.5, temperature=1.5)
     d.update(kw)
     return LossOptions(**d)
+
+
+def quant_off(opts):
+    """The same options with quantize_grad_weight off."""
+    return dataclasses.replace(opts, config=dataclasses.replace(opts.config,
+                                                                quantize_grad_weight=False))
+
+
+def int8_runs(torch_dev, s, w, y, teacher, opts, dtype=None):
+    """The quantized call and the same call with quantization off, on the GPU
+    and in the oracle: (got, ref, got_plain, ref_plain)."""
+    got, ref = run_pair(torch_dev, s, w, y, teacher, opts, dtype)
+    got_plain, ref_plain = run_pair(torch_dev, s, w, y, teacher, quant_off(opts), dtype)
+    return got, ref, got_plain, ref_plain
 
 
 # ------------------------------------------------ reference end-to-end cases
@@ -120,12 +137,39 @@ def test_sum_reduction_small(torch_dev):
 
 def test_int8_small(torch_dev):
     bt, h, v = 8, 4, 20
-    got, ref = run_pair(torch_dev, mat(bt, h, 71, 0.3), mat(v, h, 72, 0.2), labels(bt, v, None),
-                        Teacher.Tied(mat(bt, h, 73, 0.3)),
-                        base_opts(teacher_ce_weight=1.0,
-                                  config=KernelConfig(quantize_grad_weight=True)))
+    y = labels(bt, v, None)
+    got, ref, plain, ref_plain = int8_runs(
+        torch_dev, mat(bt, h, 71, 0.3), mat(v, h, 72, 0.2), y, Teacher.Tied(mat(bt, h, 73, 0.3)),
+        base_opts(teacher_ce_weight=1.0, config=KernelConfig(quantize_grad_weight=True)))
     check_output(got, ref, skip_grad_weight=True)
-    check_quantized_grad_weight(got, ref, labels(bt, v, None))
+    check_quantized_grad_weight(got, ref, y, plain.grad_weight, ref_plain.grad_weight)
+    check_quant_of_own_gradient(got, plain.grad_weight, y)
+
+
+@pytest.mark.parametrize("stochastic", [False, True])
+def test_int8_fp32_gate(torch_dev, stochastic):
+    """The INT8 clause of the gate end to end on an fp32 multi-chunk Tied
+    run with smoothing and ignored labels: codes, scales and the returned
+    grad_W are those of quantizing the call's own fp32 grad_W (the same call
+    with quantization off), and against the oracle the scales agree to 1e-5
+    relative and a code differs (by 1) only where the two fp32 gradients
+    straddle a rounding boundary (src/api.rs:380-399, src/quant.rs:91-202)."""
+    bt, h, v = 512, 128, 3000
+    s, th = normal((bt, h), 201), normal((bt, h), 202)
+    w = normal((v, h), 203, 0.03)
+    y = uniform_labels(bt, v, 204)
+    y[::7] = -100
+    seed = 4242 if stochastic else 0
+    cfg = KernelConfig(quantize_grad_weight=True, stochastic_rounding=stochastic,
+                       stochastic_seed=seed if stochastic else None)
+    opts = LossOptions(kd_weight=0.4, temperature=1.5, label_smoothing=0.1, config=cfg,
+                       chunk_size=ChunkSize.Fixed(128))
+    got, ref, plain, ref_plain = int8_runs(torch_dev, s, w, y, Teacher.Tied(th), opts)
+    check_output(got, ref, skip_grad_weight=True)
+    flips = check_quantized_grad_weight(got, ref, y, plain.grad_weight, ref_plain.grad_weight,
+                                        stochastic=stochastic, seed=seed)
+    check_quant_of_own_gradient(got, plain.grad_weight, y, stochastic=stochastic, seed=seed)
+    print(f"codes differing from the oracle at rounding boundaries: {flips} of {v * h}")
 
 
 # ------------------------------------------------ benchmark-shape cases
@@ -204,10 +248,12 @@ def test_tied_reduced_bf16_int8(torch_dev):
     opts = LossOptions(kd_weight=0.4, temperature=1.5, label_smoothing=0.1,
                        chunk_size=ChunkSize.Fixed(128),
                        config=KernelConfig(quantize_grad_weight=True))
-    got, ref = run_pair(torch_dev, s, w, y, Teacher.Tied(th), opts, dtype="bf16")
+    got, ref, plain, _ = int8_runs(torch_dev, s, w, y, Teacher.Tied(th), opts, dtype="bf16")
     check_output(got, ref, kind="bf16", skip_grad_weight=True)
     gw, rw = to_np(got.grad_weight), ref.grad_weight
     check_grad("grad_weight (dequantized)", gw, rw, "bf16")
+    # the quant step itself is exact on the call's own fp32 grad_W
+    check_quant_of_own_gradient(got, plain.grad_weight, y)
 
 
 @pytest.mark.parametrize("bt,h,v,chunk", [(300, 224, 1000, 200), (96, 112, 1064, 48)])
@@ -411,26 +457,71 @@ def test_validation_errors_match_reference(torch_dev):
         assert str(e2.value) == msg
 
 
-def test_oom_retry_doubles_chunks(torch_dev):
-    """A context memory limit below the single-chunk footprint forces the
-    doubling schedule (resolver.rs:114-126); results are unchanged."""
+# Device bytes one staged chunk row takes at this fp32 Tied shape with teacher
+# CE: student and teacher logits rows (pitch 20000), the per-256-column tile
+# statistics and label logits of both rows, and the two hidden rows that
+# grad_W multiplies ([h_s; h_t]).
+def _tied_f32_row_bytes(h, v):
+    pitch = (v + 7) // 8 * 8
+    pitch += 64 if pitch % 1024 == 0 else 0
+    return 2 * pitch * 4 + 2 * ((v + 255) // 256) * 16 + 2 * 4 + 2 * ((h + 7) // 8 * 8) * 4
+
+
+def test_oom_retry_walks_the_doubling_schedule(torch_dev):
+    """A memory limit that one chunk of 1024 rows exceeds and two chunks of
+    512 rows fit: the retry takes the next entry of chunk_doubling_schedule
+    (src/resolver.rs:103-126) after the Auto plan, and the result equals the
+    oracle's at that plan (ChunkSize::Fixed(512), src/api.rs:232,264-270)."""
     bt, h, v = 1024, 64, 20000
     s, th = normal((bt, h), 61), normal((bt, h), 62)
     w = normal((v, h), 63, 0.05)
     y = uniform_labels(bt, v, 64)
-    opts = LossOptions(kd_weight=0.4, temperature=1.5)
-    args = (gpu(torch_dev, s), gpu(torch_dev, w), gpu(torch_dev, y), Teacher.Tied(gpu(torch_dev, th)))
-    free = H.Context(0)
-    a = H.distillation_loss(*args, opts, ctx=free)
-    tight = H.Context(0)
-    tight.set_memory_limit(48 << 20)
-    b = H.distillation_loss(*args, opts, ctx=tight)
-    assert b.chunk_plan.num_chunks > a.chunk_plan.num_chunks
-    check_scalar("loss", b.loss, a.loss, 1e-5)
-    check_grad("grad_weight", b.grad_weight, a.grad_weight)
-    check_grad("grad_student_hidden", b.grad_student_hidden, a.grad_student_hidden)
-    free.close()
-    tight.close()
+    y[::9] = -100
+    opts = LossOptions(kd_weight=0.4, temperature=1.5, label_smoothing=0.1)
+    start = H.resolve_chunk_size(bt, ChunkSize.Auto, v, None)
+    assert (start.chunk_size, start.num_chunks) == (1024, 1)
+    sched = O.chunk_doubling_schedule(bt, start.num_chunks, O.default_max_chunks_limit(bt))
+    nxt = next(n for n in sched if n > start.num_chunks)
+    want = (O.ceil_div(bt, nxt), nxt)
+    row = _tied_f32_row_bytes(h, v)
+    limit = int(1.25 * want[0] * row) + (4 << 20)
+    assert limit < bt * row          # the Auto plan does not fit
+    ctx = H.Context(0)
+    ctx.set_memory_limit(limit)
+    got = H.distillation_loss(gpu(torch_dev, s), gpu(torch_dev, w), gpu(torch_dev, y),
+                              Teacher.Tied(gpu(torch_dev, th)), opts, ctx=ctx)
+    ctx.close()
+    assert (got.chunk_plan.chunk_size, got.chunk_plan.num_chunks) == want
+    ref = O.distillation_loss(s, w, y, Teacher.Tied(th),
+                              dataclasses.replace(opts, chunk_size=ChunkSize.Fixed(want[0])))
+    check_output(got, ref)
+
+
+def test_oom_retry_halves_the_staging_group(torch_dev):
+    """Eight Fixed(128) chunks staged together exceed the limit, two fit: the
+    first stage of the retry halves the group (8 -> 4 -> 2 chunks) and keeps
+    the plan; four groups run (four logits GEMMs). Result as the oracle's."""
+    bt, h, v = 1024, 64, 20000
+    s, th = normal((bt, h), 71), normal((bt, h), 72)
+    w = normal((v, h), 73, 0.05)
+    y = uniform_labels(bt, v, 74)
+    opts = LossOptions(kd_weight=0.4, temperature=1.5, chunk_size=ChunkSize.Fixed(128))
+    row = _tied_f32_row_bytes(h, v)
+    limit = int(1.25 * 256 * row) + (4 << 20)
+    assert limit < 512 * row
+    ctx = H.Context(0)
+    ctx.set_memory_limit(limit)
+    ctx.set_timing(True)
+    got = H.distillation_loss(gpu(torch_dev, s), gpu(torch_dev, w), gpu(torch_dev, y),
+                              Teacher.Tied(gpu(torch_dev, th)), opts, ctx=ctx)
+    _, launches = ctx.kernel_time("gemm_logits")
+    ctx.close()
+    assert (got.chunk_plan.chunk_size, got.chunk_plan.num_chunks) == (128, 8)
+    # attempts at 8 and 4 chunks per group fail before their logits GEMM; the
+    # run at 2 chunks per group launches one logits GEMM per group
+    assert launches == 4, launches
+    ref = O.distillation_loss(s, w, y, Teacher.Tied(th), opts)
+    check_output(got, ref)
 
 
 def test_host_buffers_round_trip(torch_dev):
