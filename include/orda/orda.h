@@ -220,6 +220,23 @@ int32_t orda_kl_ce_on_logits_chunk(orda_ctx *ctx, const orda_tensor *logits_chun
                                    orda_tensor *grad_ce, orda_tensor *ce_loss, char *err,
                                    size_t err_len);
 
+/* The same slot with no device allocation: no counterpart in the reference.
+ * For callers that cannot allocate during the call (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). ctx is
+ * required; every tensor and the targets must be on the device; n_rows is at
+ * most 32768 (ORDA_ERR_INVALID beyond). The per-row scratch is one 1.75 MiB
+ * array per GPU held until the process ends and shared by every call on that
+ * GPU: calls that overlap on one GPU race. */
+int32_t orda_kl_ce_on_logits_chunk_noalloc(orda_ctx *ctx, const orda_tensor *logits_chunk,
+                                           const int32_t *targets, int32_t targets_location,
+                                           int64_t n_rows, float inv_t, float kl_grad_scale,
+                                           float t_sq, float student_ce_weight,
+                                           float teacher_ce_weight, float label_smoothing,
+                                           int32_t ignore_index, int32_t student_only,
+                                           int32_t compute_kl, orda_tensor *grad_kl_student,
+                                           orda_tensor *kl_per_row, orda_tensor *grad_ce,
+                                           orda_tensor *ce_loss, char *err, size_t err_len);
+
 /* ---- INT8 row-wise quantization (src/quant.rs:96-202) --------------------- */
 /* quantize_grad_w followed by dequantize_grad_w(·, grad_output): m [rows,cols]
  * float32; out receives the dequantized matrix (may alias m) with the rows

@@ -1221,6 +1221,8 @@ int32_t orda_ctx_create(int32_t device, orda_ctx** out, char* err, size_t err_le
     // reads the inputs, and the null stream waits for it in turn.
     hip_check(hipStreamCreateWithFlags(&c->own, hipStreamDefault), "hipStreamCreate");
     c->stream = c->own;
+    // The no-allocation entry point's scratch address on this device.
+    hip_check(orda::noalloc_scratch_init(device), "no-allocation scratch");
     *out = c.release();
     return ORDA_OK;
   } catch (const Error& e) {

@@ -53,4 +53,8 @@ void kl_ce_slot(orda_ctx* c, const orda_tensor* logits_chunk, const int32_t* tar
 
 int32_t ctx_device(const orda_ctx* c);
 
+// Looks up, once per device, the device address of the no-allocation entry
+// point's scratch array (call with that device current). Returns a HIP error.
+hipError_t noalloc_scratch_init(int device);
+
 }  // namespace orda

@@ -104,6 +104,11 @@ SIGNATURES = [
       C.c_float, C.c_float, C.c_float, C.c_float, C.c_int32, C.c_int32, C.c_int32,
       C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), C.c_char_p,
       C.c_size_t]),
+    ("orda_kl_ce_on_logits_chunk_noalloc", C.c_int32,
+     [C.c_void_p, C.POINTER(Tensor), C.c_void_p, C.c_int32, C.c_int64, C.c_float, C.c_float,
+      C.c_float, C.c_float, C.c_float, C.c_float, C.c_int32, C.c_int32, C.c_int32,
+      C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor), C.c_char_p,
+      C.c_size_t]),
     ("orda_quant_rows_int8", C.c_int32,
      [C.c_void_p, C.POINTER(Tensor), C.c_void_p, C.c_int64, C.c_int32, C.c_int64, C.c_int32,
       C.c_uint64, C.c_float, C.POINTER(Tensor), C.POINTER(Tensor), C.POINTER(Tensor),
