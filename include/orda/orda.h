@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define ORDA_ABI_VERSION 1
+#define ORDA_ABI_VERSION 2
 
 typedef enum {
     ORDA_OK = 0,
@@ -64,7 +64,27 @@ typedef struct {
     orda_tensor logits;     /* Precomputed [BT,V] */
 } orda_teacher;
 
-/* KernelConfig (src/config.rs:45-63). Option<T> fields carry has_* flags. */
+/* KernelConfig (src/config.rs:45-63). Option<T> fields carry has_* flags.
+ * The reference's CPU path ignores the tuning fields (src/config.rs:3-7); on
+ * this GPU path they act as follows:
+ *   fast_math       (Profile::Fast) fp32 inputs are rounded to bf16 once and
+ *                   run the bf16 MFMA pipeline with bf16 logits storage
+ *                   (upstream's half-precision logits, docs/BLOCKERS.md:
+ *                   129-131); per-row logs and divisions use the hardware
+ *                   approximations. Gradients match the reference on the
+ *                   bf16-rounded inputs to the bf16 tolerance.
+ *   profile         ORDA_PROFILE_DEBUG (the precise preset): bf16 inputs are
+ *                   widened to fp32 and run the fp32 pipeline (fp32 logits,
+ *                   fp32 GEMMs), matching the reference to the fp32
+ *                   tolerance. Set by orda_kernel_config_from_profile; the
+ *                   reference records the preset only through the fields
+ *                   it sets, so this one field is new.
+ *   online_softmax  row statistics of logits the GEMM did not produce
+ *                   (Precomputed teacher logits, the chunk-launcher slot) in
+ *                   one online pass instead of a max pass and a sum pass.
+ *   fp32_grad_weight_accumulation, max_fused_size: accepted and validated;
+ *                   grad_W always accumulates in fp32 (the reference's
+ *                   output is f32) and the tile widths are fixed. */
 typedef struct {
     int32_t online_softmax;
     int32_t fast_math;
@@ -76,6 +96,7 @@ typedef struct {
     int64_t max_fused_size;
     int32_t has_stochastic_seed;
     uint64_t stochastic_seed;
+    int32_t profile;            /* orda_profile the config was made from */
 } orda_kernel_config;
 
 /* LossOptions (src/api.rs:25-47). */

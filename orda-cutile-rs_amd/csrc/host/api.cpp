@@ -372,6 +372,29 @@ void config_validate(const orda_kernel_config& k) {
          static_cast<long long>(mf));
   if (k.has_max_chunks && k.max_chunks < 1)
     fail(ORDA_ERR_INVALID, "max_chunks must be >= 1, got %lld", static_cast<long long>(k.max_chunks));
+  if (k.profile < ORDA_PROFILE_BALANCED || k.profile > ORDA_PROFILE_DEBUG)
+    fail(ORDA_ERR_INVALID, "unknown profile %d", k.profile);
+}
+
+// The dtype the GEMMs and the logits run in: the inputs' own, except fp32
+// inputs under fast_math (bf16, half-precision storage) and bf16 inputs
+// under the Debug profile (fp32, the precise preset).
+DType compute_dtype(const orda_kernel_config& k, DType in) {
+  if (k.profile == ORDA_PROFILE_DEBUG) return DType::F32;
+  if (k.fast_math && in == DType::F32) return DType::BF16;
+  return in;
+}
+
+// A device copy of an input view in another dtype (pitch round8(cols)).
+DMat convert(orda_ctx* c, const DMat& src, DType want, const std::string& name) {
+  DMat d = src;
+  d.t = want;
+  d.ld = round8(src.cols > 0 ? src.cols : 1);
+  d.p = ws(c, name, std::max<int64_t>(1, src.rows) * d.ld * orda::dtype_size(want));
+  hip_check(orda::launch_convert_rows(src.t, src.p, src.ld, want, const_cast<void*>(d.p), d.ld,
+                                      src.rows, src.cols, c->stream),
+            "convert input");
+  return d;
 }
 
 const char* dt_name(DType t) { return t == DType::F32 ? "float32" : "bfloat16"; }
@@ -387,6 +410,8 @@ struct LossPlan {
   DType dt;
   bool quant, stochastic;
   uint64_t seed;
+  bool fast_math;           // approximate per-row logs and divisions
+  bool online;              // one-pass row statistics (KernelConfig::online_softmax)
 };
 
 struct Inputs {
@@ -569,6 +594,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
         r.labels = in.labels + gs;
         r.ignore_index = P.ignore;
         r.inv_t = inv_t;
+        r.online = P.online;
         timed(c, ORDA_KERNEL_OTHER, [&] { return launch_row_stats(r, c->stream); });
       } else {
         GemmArgs t = f;
@@ -620,6 +646,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       r.row_nll_t = rnll_t + gs;
       r.row_kl = rkl + gs;
       r.split = false;
+      r.fast_math = P.fast_math;
       timed(c, ORDA_KERNEL_ROW_PASS, [&] { return launch_row_pass(r, c->stream); });
     }
 
@@ -862,6 +889,19 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
       check_labels_host(host_labels(c, labels, n_labels, lab_loc), v, o->ignore_index);
     throw;
   }
+  // ---- compute dtype (KernelConfig::fast_math, Profile::Debug)
+  {
+    const DType ct = compute_dtype(o->config, P.dt);
+    if (ct != P.dt) {
+      in.hs = convert(c, in.hs, ct, "cv.student");
+      in.W = convert(c, in.W, ct, "cv.weight");
+      if (in.th.p) in.th = convert(c, in.th, ct, "cv.t_hidden");
+      if (in.tw.p) in.tw = convert(c, in.tw, ct, "cv.t_weight");
+      P.dt = ct;
+    }
+  }
+  P.fast_math = o->config.fast_math != 0;
+  P.online = o->config.online_softmax != 0;
   in.labels = device_labels(c, labels, n_labels, lab_loc, "in.labels");
   float* row3 = static_cast<float*>(ws(c, "rows", 3 * bt * 4));
   // Loss scalars (4 floats) followed by the label status, read back together.
@@ -1177,6 +1217,7 @@ void orda_kernel_config_from_profile(int32_t profile, orda_kernel_config* cfg) {
   memset(cfg, 0, sizeof *cfg);
   cfg->fast_math = profile == ORDA_PROFILE_FAST;
   cfg->max_fused_size = 65536 / 2;
+  cfg->profile = profile;
 }
 
 void orda_loss_options_default(orda_loss_options* o) {

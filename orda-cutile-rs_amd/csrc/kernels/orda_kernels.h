@@ -135,6 +135,7 @@ struct RowPassArgs {
   float t_sq;              // split mode: T^2 as given
   float inv_t;             // split mode: 1/T as given
   bool student_only;       // split mode: CE over student rows only
+  bool fast_math;          // per-row logs and divisions by the hardware approximations
 };
 
 hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t stream);
@@ -158,6 +159,7 @@ struct RowStatsArgs {
   const int64_t* labels;   // may be null (then xy is not written)
   int64_t ignore_index;
   float inv_t;
+  bool online;             // one online pass; else a max pass, then a sum pass
 };
 hipError_t launch_row_stats(const RowStatsArgs& a, hipStream_t stream);
 

@@ -24,6 +24,19 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Per-row constants: precise logf / IEEE division, or with fast_math the
+// hardware approximations (v_log_f32 times ln 2, v_rcp_f32 then a multiply).
+__device__ __forceinline__ float rlog(float x, bool fast) {
+  return fast ? __builtin_amdgcn_logf(x) * kLn2 : logf(x);
+}
+__device__ __forceinline__ float rlog2(float x, bool fast) {
+  return fast ? __builtin_amdgcn_logf(x) : log2f(x);
+}
+__device__ __forceinline__ float rdiv(float a, float b, bool fast) {
+  return fast ? a * __builtin_amdgcn_rcpf(b) : a / b;
+}
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -161,8 +174,9 @@ struct Vec<__bf16> {
 // difference is exact when they are close, and the log of a ratio near 1
 // keeps the small KL of nearly equal rows (where lse_s^T and lse_t^T agree
 // to many digits) from being swamped by the rounding of two O(|lse|) logs.
-__device__ __forceinline__ float lse_t_diff(const Stat& s, const Stat& t, float inv_t) {
-  return (s.m - t.m) * inv_t + logf(s.dT / t.dT);
+__device__ __forceinline__ float lse_t_diff(const Stat& s, const Stat& t, float inv_t,
+                                            bool fast = false) {
+  return (s.m - t.m) * inv_t + rlog(rdiv(s.dT, t.dT, fast), fast);
 }
 
 // nll of cross_entropy.rs:46-56 from merged stats, in f64.
@@ -403,8 +417,9 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
     return;
   }
 
+  const bool fm = a.fast_math;
   const float T = a.temperature;
-  const float inv_t = 1.0f / T;
+  const float inv_t = rdiv(1.0f, T, fm);
   const float it2 = inv_t * kLog2e;
   const Stat ss = load_row_stats(a.stats_s + r * a.stats_ld, a.stats_tiles, it2, sstat);
   Stat st{-INFINITY, 0.f, 0.f, 0.f};
@@ -422,20 +437,20 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
   }
 
   const double alpha = static_cast<double>(a.label_smoothing);
-  const float lse1_s = ss.m + logf(ss.d1);
-  const float lseT_s = ss.m * inv_t + logf(ss.dT);
-  const float lse1_t = st.m + logf(st.d1);
-  const float lseT_t = st.m * inv_t + logf(st.dT);
+  const float lse1_s = ss.m + rlog(ss.d1, fm);
+  const float lseT_s = ss.m * inv_t + rlog(ss.dT, fm);
+  const float lse1_t = st.m + rlog(st.d1, fm);
+  const float lseT_t = st.m * inv_t + rlog(st.dT, fm);
   const float eps = static_cast<float>(alpha / static_cast<double>(v));
   const float one_m_a = 1.0f - a.label_smoothing;
   const float ws = a.w_s, wt = a.w_t;
   const float gsc = a.kd * T;                              // kl.rs:85
   // w_s·p_s (w_s may be any sign; w_t, kd >= 0 are validated by the caller)
-  const float ca = log2f(fabsf(ws)) - lse1_s * kLog2e;
+  const float ca = rlog2(fabsf(ws), fm) - lse1_s * kLog2e;
   const float sgn = ws < 0.f ? -1.f : 1.f;
-  const float cb = KL ? log2f(gsc) - lseT_s * kLog2e : 0.f;   // kd·T·p_s^T
-  const float cc = KL ? log2f(gsc) - lseT_t * kLog2e : 0.f;   // kd·T·p_t^T
-  const float cd = TG ? log2f(wt) - lse1_t * kLog2e : 0.f;    // w_t·p_t
+  const float cb = KL ? rlog2(gsc, fm) - lseT_s * kLog2e : 0.f;   // kd·T·p_s^T
+  const float cc = KL ? rlog2(gsc, fm) - lseT_t * kLog2e : 0.f;   // kd·T·p_t^T
+  const float cd = TG ? rlog2(wt, fm) - lse1_t * kLog2e : 0.f;    // w_t·p_t
   const float k0 = -ws * eps, kt0 = -wt * eps;
   const float ky = ws * one_m_a, kyt = wt * one_m_a;
 
@@ -535,9 +550,10 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
     a.row_nll_s[r] = static_cast<float>(row_nll(ss, a.xy_s[r], alpha, v));
     float kl_row = 0.f;
     if (KL && a.cross != nullptr)
-      kl_row = ((xc / st.dT) * inv_t + lse_t_diff(ss, st, inv_t)) * (T * T);
+      kl_row = (rdiv(xc, st.dT, fm) * inv_t + lse_t_diff(ss, st, inv_t, fm)) * (T * T);
     else if (KL)
-      kl_row = ((cross / gsc) * inv_t + lse_t_diff(ss, st, inv_t) * (sum_c / gsc)) * (T * T);
+      kl_row = (rdiv(cross, gsc, fm) * inv_t + lse_t_diff(ss, st, inv_t, fm) * rdiv(sum_c, gsc, fm)) *
+               (T * T);
     a.row_kl[r] = kl_row;
     a.row_nll_t[r] = a.teacher_ce ? static_cast<float>(row_nll(st, a.xy_t[r], alpha, v)) : 0.f;
   }
@@ -572,8 +588,9 @@ __global__ __launch_bounds__(kThreads) void row_consts_kernel(RowPassArgs a) {
     }
     return;
   }
+  const bool fm = a.fast_math;
   const float T = a.temperature;
-  const float inv_t = 1.0f / T;
+  const float inv_t = rdiv(1.0f, T, fm);
   const float it2 = inv_t * kLog2e;
   Stat ss{-INFINITY, 0.f, 0.f, 0.f}, st{-INFINITY, 0.f, 0.f, 0.f};
   float xc = 0.f;
@@ -610,19 +627,19 @@ __global__ __launch_bounds__(kThreads) void row_consts_kernel(RowPassArgs a) {
   }
   if (lane == 0) {
     const double alpha = static_cast<double>(a.label_smoothing);
-    const float lse1_s = ss.m + logf(ss.d1);
-    const float lseT_s = ss.m * inv_t + logf(ss.dT);
-    const float lse1_t = st.m + logf(st.d1);
-    const float lseT_t = st.m * inv_t + logf(st.dT);
+    const float lse1_s = ss.m + rlog(ss.d1, fm);
+    const float lseT_s = ss.m * inv_t + rlog(ss.dT, fm);
+    const float lse1_t = st.m + rlog(st.d1, fm);
+    const float lseT_t = st.m * inv_t + rlog(st.dT, fm);
     const float gsc = a.kd * T;                              // kl.rs:85
     float4 k;
-    k.x = log2f(fabsf(a.w_s)) - lse1_s * kLog2e;
-    k.y = KL ? log2f(gsc) - lseT_s * kLog2e : 0.f;
-    k.z = KL ? log2f(gsc) - lseT_t * kLog2e : 0.f;
-    k.w = TG ? log2f(a.w_t) - lse1_t * kLog2e : 0.f;
+    k.x = rlog2(fabsf(a.w_s), fm) - lse1_s * kLog2e;
+    k.y = KL ? rlog2(gsc, fm) - lseT_s * kLog2e : 0.f;
+    k.z = KL ? rlog2(gsc, fm) - lseT_t * kLog2e : 0.f;
+    k.w = TG ? rlog2(a.w_t, fm) - lse1_t * kLog2e : 0.f;
     a.row_consts[r] = k;
     a.row_nll_s[r] = static_cast<float>(row_nll(ss, a.xy_s[r], alpha, a.v));
-    a.row_kl[r] = KL ? ((xc / st.dT) * inv_t + lse_t_diff(ss, st, inv_t)) * (T * T) : 0.f;
+    a.row_kl[r] = KL ? (rdiv(xc, st.dT, fm) * inv_t + lse_t_diff(ss, st, inv_t, fm)) * (T * T) : 0.f;
     a.row_nll_t[r] = a.teacher_ce ? static_cast<float>(row_nll(st, a.xy_t[r], alpha, a.v)) : 0.f;
   }
 }
@@ -655,7 +672,7 @@ __global__ __launch_bounds__(kThreads) void row_grad_kernel(RowPassArgs a, int64
     return;
   }
   const float4 k = a.row_consts[r];
-  const float it2 = kLog2e / a.temperature;
+  const float it2 = kLog2e * rdiv(1.0f, a.temperature, a.fast_math);
   const float eps = static_cast<float>(static_cast<double>(a.label_smoothing) / static_cast<double>(v));
   const float one_m_a = 1.0f - a.label_smoothing;
   const float sgn = a.w_s < 0.f ? -1.f : 1.f;
@@ -713,22 +730,63 @@ __global__ __launch_bounds__(kThreads) void row_grad_kernel(RowPassArgs a, int64
 }
 
 // ------------------------------------------------------------------ row stats
-template <typename ST, typename DT>
+__device__ float block_max(float v, float* scratch) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[wave] = v;
+  __syncthreads();
+  float r = scratch[0];
+#pragma unroll
+  for (int w = 1; w < kThreads / 64; ++w) r = fmaxf(r, scratch[w]);
+  return r;
+}
+
+// Per-row statistics {max, Σe^(x-max), Σe^((x-max)/T), Σx} of rows the GEMM
+// did not produce. ONLINE: one read, each element merged into running
+// statistics (two exponentials per statistic); otherwise a max pass, then a
+// pass summing e^(x-max) and e^((x-max)/T) (the second read of a row mostly
+// hits the cache).
+template <typename ST, typename DT, bool ONLINE>
 __global__ __launch_bounds__(kThreads) void row_stats_kernel(RowStatsArgs a) {
   __shared__ Stat sstat[kThreads / 64];
+  __shared__ float sred[kThreads / 64];
   const int64_t r = blockIdx.x;
   const ST* src = static_cast<const ST*>(a.src) + r * a.lds;
   DT* dst = a.dst ? static_cast<DT*>(a.dst) + r * a.ldd : nullptr;
   const float it2 = a.inv_t * kLog2e;
   Stat s{-INFINITY, 0.f, 0.f, 0.f};
-  for (int64_t j = threadIdx.x; j < a.v; j += kThreads) {
-    const float x = static_cast<float>(src[j]);
-    if (dst) dst[j] = static_cast<DT>(x);
-    s = merge(s, Stat{x, 1.f, 1.f, x}, it2);
+  if constexpr (ONLINE) {
+    for (int64_t j = threadIdx.x; j < a.v; j += kThreads) {
+      const float x = static_cast<float>(src[j]);
+      if (dst) dst[j] = static_cast<DT>(x);
+      s = merge(s, Stat{x, 1.f, 1.f, x}, it2);
+    }
+    s = block_merge(s, it2, sstat);
+  } else {
+    float m = -INFINITY, sx = 0.f;
+    for (int64_t j = threadIdx.x; j < a.v; j += kThreads) {
+      const float x = static_cast<float>(src[j]);
+      if (dst) dst[j] = static_cast<DT>(x);
+      m = fmaxf(m, x);
+      sx += x;
+    }
+    m = block_max(m, sred);
+    const float o1 = -m * kLog2e, oT = -m * it2;
+    float d1 = 0.f, dT = 0.f;
+    for (int64_t j = threadIdx.x; j < a.v; j += kThreads) {
+      const float x = static_cast<float>(src[j]);
+      d1 += __builtin_amdgcn_exp2f(fmaf(x, kLog2e, o1));
+      dT += __builtin_amdgcn_exp2f(fmaf(x, it2, oT));
+    }
+    s.m = m;
+    s.sx = block_sum(sx, sred);
+    s.d1 = block_sum(d1, sred);
+    s.dT = block_sum(dT, sred);
   }
   if (dst)
     for (int64_t j = a.v + threadIdx.x; j < a.ldd; j += kThreads) dst[j] = static_cast<DT>(0.f);
-  s = block_merge(s, it2, sstat);
   if (threadIdx.x == 0) {
     a.stats[r * a.stats_ld] = make_float4(s.m, s.d1, s.dT, s.sx);
     if (a.labels) {
@@ -858,10 +916,17 @@ hipError_t launch_row_stats(const RowStatsArgs& a, hipStream_t s) {
   dim3 grid(static_cast<unsigned>(a.n_rows));
   const bool sf = a.src_type == DType::F32;
   const bool df = a.dst_type == DType::F32;
-  if (sf && df) hipLaunchKernelGGL((row_stats_kernel<float, float>), grid, dim3(kThreads), 0, s, a);
-  else if (sf) hipLaunchKernelGGL((row_stats_kernel<float, __bf16>), grid, dim3(kThreads), 0, s, a);
-  else if (df) hipLaunchKernelGGL((row_stats_kernel<__bf16, float>), grid, dim3(kThreads), 0, s, a);
-  else hipLaunchKernelGGL((row_stats_kernel<__bf16, __bf16>), grid, dim3(kThreads), 0, s, a);
+#define ORDA_ROWSTATS(ONLINE)                                                                        \
+  if (sf && df) hipLaunchKernelGGL((row_stats_kernel<float, float, ONLINE>), grid, dim3(kThreads), 0, s, a);   \
+  else if (sf) hipLaunchKernelGGL((row_stats_kernel<float, __bf16, ONLINE>), grid, dim3(kThreads), 0, s, a);  \
+  else if (df) hipLaunchKernelGGL((row_stats_kernel<__bf16, float, ONLINE>), grid, dim3(kThreads), 0, s, a);  \
+  else hipLaunchKernelGGL((row_stats_kernel<__bf16, __bf16, ONLINE>), grid, dim3(kThreads), 0, s, a);
+  if (a.online) {
+    ORDA_ROWSTATS(true)
+  } else {
+    ORDA_ROWSTATS(false)
+  }
+#undef ORDA_ROWSTATS
   return hipGetLastError();
 }
 

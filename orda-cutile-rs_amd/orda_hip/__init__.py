@@ -262,6 +262,7 @@ def _options_c(o: LossOptions) -> LossOptionsC:
     c.config.max_fused_size = int(k.max_fused_size)
     c.config.has_stochastic_seed = int(k.stochastic_seed is not None)
     c.config.stochastic_seed = int(k.stochastic_seed or 0)
+    c.config.profile = int(k.profile)
     c.backend = int(o.backend)
     return c
 

@@ -46,7 +46,8 @@ class KernelConfigC(C.Structure):
                 ("quantize_grad_weight", C.c_int32), ("stochastic_rounding", C.c_int32),
                 ("fp32_grad_weight_accumulation", C.c_int32), ("has_max_chunks", C.c_int32),
                 ("max_chunks", C.c_int64), ("max_fused_size", C.c_int64),
-                ("has_stochastic_seed", C.c_int32), ("stochastic_seed", C.c_uint64)]
+                ("has_stochastic_seed", C.c_int32), ("stochastic_seed", C.c_uint64),
+                ("profile", C.c_int32)]
 
 
 class LossOptionsC(C.Structure):

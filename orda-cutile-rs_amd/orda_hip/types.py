@@ -58,9 +58,20 @@ def is_power_of_two(value: int) -> bool:
 
 @dataclass
 class KernelConfig:
-    """src/config.rs:45-120. Only ``max_chunks``, ``quantize_grad_weight``,
-    ``stochastic_rounding`` and ``stochastic_seed`` change results; the rest
-    are accepted and carried through, as in the reference."""
+    """src/config.rs:45-120. On the GPU path (the reference's CPU path
+    ignores the tuning fields):
+
+    * ``fast_math`` (``Profile.Fast``): fp32 inputs run the bf16 pipeline
+      (inputs rounded to bf16 once, bf16 logits storage); approximate
+      per-row logs and divisions;
+    * ``profile == Profile.Debug`` (the precise preset): bf16 inputs run the
+      fp32 pipeline; ``profile`` is set by ``from_profile`` (the reference
+      keeps only the fields a preset sets, so this field is added);
+    * ``online_softmax``: one-pass row statistics of logits the GEMM did not
+      produce (Precomputed teacher logits, the chunk-launcher slot);
+    * ``fp32_grad_weight_accumulation``, ``max_fused_size``: accepted and
+      validated; grad_W always accumulates in fp32.
+    """
     online_softmax: bool = False
     fast_math: bool = False
     quantize_grad_weight: bool = False
@@ -69,10 +80,11 @@ class KernelConfig:
     max_chunks: Optional[int] = None
     max_fused_size: int = DEFAULT_MAX_FUSED_SIZE
     stochastic_seed: Optional[int] = None
+    profile: Profile = Profile.Balanced
 
     @staticmethod
     def from_profile(profile: Profile) -> "KernelConfig":
-        return KernelConfig(fast_math=(profile == Profile.Fast))
+        return KernelConfig(fast_math=(profile == Profile.Fast), profile=Profile(profile))
 
     def fast_math_exp(self) -> bool:
         return self.fast_math

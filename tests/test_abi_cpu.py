@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_availability_without_gpu():
     lib = L.load()
-    assert lib.orda_abi_version() == 1
+    assert lib.orda_abi_version() == 2
     avail = H.is_available()
     assert avail in (True, False)
 
@@ -80,11 +80,16 @@ def test_option_defaults_match_reference():
     assert c.label_smoothing == 0.0 and c.reduction == 0 and c.chunk_fixed == 0
     assert c.backend == 0 and c.config.max_fused_size == 32768
     assert not c.config.fast_math and not c.config.quantize_grad_weight
+    assert c.config.profile == 0
     k = L.KernelConfigC()
     L.load().orda_kernel_config_from_profile(1, C.byref(k))
-    assert k.fast_math == 1
+    assert k.fast_math == 1 and k.profile == 1
     L.load().orda_kernel_config_from_profile(2, C.byref(k))
-    assert k.fast_math == 0
+    assert k.fast_math == 0 and k.profile == 2
+    # the Python mirror records the preset the same way
+    assert H.KernelConfig.from_profile(H.Profile.Debug).profile == H.Profile.Debug
+    assert H.KernelConfig().profile == H.Profile.Balanced
+    assert L.load().orda_abi_version() == 2
 
 
 def test_config_validate_messages():
@@ -99,6 +104,9 @@ def test_config_validate_messages():
     k.has_max_chunks, k.max_chunks = 1, 0
     assert L.load().orda_kernel_config_validate(C.byref(k), err, 256) == 1
     assert err.value.decode() == "max_chunks must be >= 1, got 0"
+    k.has_max_chunks, k.profile = 0, 7
+    assert L.load().orda_kernel_config_validate(C.byref(k), err, 256) == 1
+    assert err.value.decode() == "unknown profile 7"
 
 
 def test_no_gpu_fails_loudly_not_silently():
