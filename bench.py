@@ -25,7 +25,7 @@ PEAK_HBM_GBS = 8000.0           # MI355X HBM3E, GB/s
 PEAK_MFMA_TFLOPS = {"bf16": 2500.0, "f32": 157.3}   # dense
 
 WORKLOADS = {
-    # name: (teacher, BT, H, Ht, V, dtype, kd, T, alpha, w_t, quant)
+    # name: (teacher, BT, H, Ht, V, dtype, kd, T, alpha, w_t, quant[, profile])
     "tied-8192x4096x131072-bf16-int8": ("tied", 8192, 4096, 4096, 131072, "bf16", 0.4, 1.5, 0.1,
                                         None, True),
     "tied-2048x4096x32000-f32": ("tied", 2048, 4096, 4096, 32000, "f32", 0.4, 1.5, 0.0, None,
@@ -35,6 +35,14 @@ WORKLOADS = {
     "precomputed-4096x4096x65536-f32": ("precomputed", 4096, 4096, 4096, 65536, "f32", 0.7, 1.0,
                                         0.0, None, False),
     "tied-256x512x8192-f32": ("tied", 256, 512, 512, 8192, "f32", 0.4, 1.5, 0.0, None, False),
+    # fp32 inputs under Profile::Fast: the bf16 pipeline with half-precision
+    # logits storage (KernelConfig::fast_math)
+    "tied-2048x4096x32000-f32-fast": ("tied", 2048, 4096, 4096, 32000, "f32", 0.4, 1.5, 0.0, None,
+                                      False, "fast"),
+    "separate-4096x2048x4096x32000-f32-fast": ("separate", 4096, 2048, 4096, 32000, "f32", 0.5,
+                                               2.0, 0.1, 1.0, False, "fast"),
+    "precomputed-4096x4096x65536-f32-fast": ("precomputed", 4096, 4096, 4096, 65536, "f32", 0.7,
+                                             1.0, 0.0, None, False, "fast"),
 }
 DEFAULT = "tied-8192x4096x131072-bf16-int8"
 
@@ -76,16 +84,29 @@ def teacher_obj(H, t):
     return H.Teacher.Precomputed(t[1])
 
 
+def profile_of(wl):
+    return wl[11] if len(wl) > 11 else None
+
+
+def compute_dtype(wl):
+    """The dtype the GEMMs and logits run in (fast_math: fp32 inputs as bf16)."""
+    return "bf16" if profile_of(wl) == "fast" else wl[5]
+
+
 def options(H, wl):
-    _, _, _, _, _, _, kd, T, alpha, w_t, quant = wl
+    _, _, _, _, _, _, kd, T, alpha, w_t, quant = wl[:11]
+    cfg = H.KernelConfig(quantize_grad_weight=quant)
+    if profile_of(wl) == "fast":
+        cfg = H.KernelConfig.from_profile(H.Profile.Fast)
+        cfg.quantize_grad_weight = quant
     return H.LossOptions(kd_weight=kd, temperature=T, label_smoothing=alpha,
-                         teacher_ce_weight=w_t,
-                         config=H.KernelConfig(quantize_grad_weight=quant))
+                         teacher_ce_weight=w_t, config=cfg)
 
 
 def work_per_step(wl, plan):
     """Algorithmic flops (GEMMs) and bytes (row pass, quant) of one step."""
-    teacher, bt, h, ht, v, dt, kd, T, alpha, w_t, quant = wl
+    teacher, bt, h, ht, v, _, kd, T, alpha, w_t, quant = wl[:11]
+    dt = compute_dtype(wl)
     es = 2 if dt == "bf16" else 4
     wt = w_t if w_t is not None else (1.0 if teacher == "tied" else 0.0)
     hs = h
@@ -118,48 +139,82 @@ def work_per_step(wl, plan):
             "quant": ("hbm", quant_b)}
 
 
-def cpu_baseline(wl, budget_rows=(2, 6)):
-    """The CPU oracle (single thread) on two small samples of the same
-    workload; per-row and per-call costs are separated from the two timings
-    and extrapolated to the full BT and chunk count."""
+def cpu_info():
+    """(model name, usable cores) of the host."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    return model, cores
+
+
+def cpu_baseline(wl, sample_rows=(2, 4, 6)):
+    """The CPU oracle (one thread, as the reference: no threads, no
+    dependencies) on a bounded sample of the same workload: one chunk of 2, 4
+    and 6 rows (same H, V and options). A least-squares line through the three
+    timings gives the cost per row and per chunk (the residual is reported);
+    the per-call INT8 step is timed on its own so that it is not counted once
+    per chunk. Extrapolated to the full BT in the Auto plan's chunks."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle as O
     import orda_hip as H
-    teacher, bt, h, ht, v, dt, kd, T, alpha, w_t, quant = wl
+    teacher, bt, h, ht, v, dt, kd, T, alpha, w_t, quant = wl[:11]
     rng = np.random.default_rng(0)
+    w = (rng.standard_normal((v, h), dtype=np.float32) * 0.02).astype(np.float32)
+    tw = (rng.standard_normal((v, ht), dtype=np.float32) * 0.015) if teacher == "separate" else None
 
     def mk(n):
         s = rng.standard_normal((n, h), dtype=np.float32)
-        w = (rng.standard_normal((v, h), dtype=np.float32) * 0.02).astype(np.float32)
         y = rng.integers(0, v, n)
         if teacher == "tied":
             t = H.Teacher.Tied(rng.standard_normal((n, h), dtype=np.float32))
         elif teacher == "separate":
-            t = H.Teacher.Separate(rng.standard_normal((n, ht), dtype=np.float32),
-                                   (rng.standard_normal((v, ht), dtype=np.float32) * 0.015))
+            t = H.Teacher.Separate(rng.standard_normal((n, ht), dtype=np.float32), tw)
         else:
             t = H.Teacher.Precomputed(rng.standard_normal((n, v), dtype=np.float32) * 2)
-        return s, w, y, t
-    times = []
+        return s, y, t
     opts = options(H, wl)
-    for n in budget_rows:
-        s, w, y, t = mk(n)
+    times = []
+    for n in sample_rows:
+        s, y, t = mk(n)
         t0 = time.perf_counter()
         O.distillation_loss(s, w, y, t, opts)
         times.append(time.perf_counter() - t0)
         log(f"cpu oracle sample BT={n}: {times[-1]:.2f} s")
-    (n1, n2), (t1, t2) = budget_rows, times
-    per_row = max((t2 - t1) / (n2 - n1), 1e-9)
-    fixed = max(t1 - n1 * per_row, 0.0)
+    per_call = 0.0
+    if quant:
+        g = (rng.standard_normal((v, h), dtype=np.float32) * 1e-4).astype(np.float32)
+        t0 = time.perf_counter()
+        O.quant_dequant_grad_w(g, np.arange(8), -100)
+        per_call = time.perf_counter() - t0
+        log(f"cpu oracle INT8 step alone: {per_call:.2f} s")
+    x = np.array(sample_rows, np.float64)
+    tt = np.array(times, np.float64)
+    per_row, fixed = np.polyfit(x, tt, 1)
+    per_row = max(float(per_row), 1e-9)
+    resid = float(np.sqrt(np.mean((tt - (per_row * x + fixed)) ** 2)))
+    per_chunk = max(float(fixed) - per_call, 0.0)
     plan = H.resolve_chunk_size(bt, H.ChunkSize.Auto, v, None)
-    est = bt * per_row + plan.num_chunks * fixed
+    est = bt * per_row + plan.num_chunks * per_chunk + per_call
+    model, cores = cpu_info()
     return {"value": bt / est, "unit": "rows/s", "cores": 1, "kind": "port",
-            "sample": (f"oracle/liborda_oracle.so, one thread, BT={n1} and BT={n2} of this "
-                       f"workload (same H, V, options; f32 arithmetic as the reference); "
-                       f"per-row {per_row:.3f} s and per-chunk {fixed:.3f} s fitted from the two "
-                       f"timings, extrapolated to BT={bt} in {plan.num_chunks} chunks "
-                       f"({est:.0f} s)")}
+            "cpu": model, "host_cores": cores,
+            "sample": (f"oracle/liborda_oracle.so on one thread of a {cores}-core {model}: "
+                       f"one chunk of {', '.join(map(str, sample_rows))} rows of this workload "
+                       f"(same H, V, options; the reference's f32/f64 arithmetic), timed "
+                       f"{', '.join(f'{t:.2f}' for t in times)} s; least-squares per-row "
+                       f"{per_row:.3f} s and per-chunk {per_chunk:.3f} s (rms residual "
+                       f"{resid:.3f} s), per-call INT8 step {per_call:.2f} s timed alone; "
+                       f"extrapolated to BT={bt} in {plan.num_chunks} chunks ({est:.0f} s)")}
 
 
 # ------------------------------------------------------------ profiles
@@ -374,7 +429,8 @@ def main():
     elapsed = time.perf_counter() - t0
     ctx.set_timing(False)
     log(f"timed {args.steps} steps in {elapsed * 1e3:.1f} ms, loss {out.loss:.5f}")
-    teacher_kind, bt, h, ht, v, dt, *_ = wl
+    teacher_kind, bt, h, ht, v = wl[:5]
+    dt = compute_dtype(wl)
     work = work_per_step(wl, plan)
     kernels = {}
     for kind, (bound, amount) in work.items():
@@ -412,7 +468,8 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": dt, "data": "synthetic",
         "config": {"workload": args.workload, "teacher": teacher_kind, "bt": bt, "h": h,
-                   "v": v, "chunks": f"{plan.num_chunks}x{plan.chunk_size}"},
+                   "v": v, "chunks": f"{plan.num_chunks}x{plan.chunk_size}",
+                   "inputs": wl[5], "profile": profile_of(wl) or "balanced"},
         "roofline": roofline,
         "kernels": kernels,
         "mfma_util": {k: kernels[k]["frac"] for k in kernels if kernels[k]["bound"] == "mfma"},

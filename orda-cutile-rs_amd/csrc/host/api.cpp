@@ -595,6 +595,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
         r.ignore_index = P.ignore;
         r.inv_t = inv_t;
         r.online = P.online;
+        r.segmented = true;
         timed(c, ORDA_KERNEL_OTHER, [&] { return launch_row_stats(r, c->stream); });
       } else {
         GemmArgs t = f;
@@ -627,7 +628,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       r.stats_t = stats + btg * nst;
       r.stats_ld = nst;
       r.stats_tiles = nst;
-      r.stats_tiles_t = P.mode == ORDA_TEACHER_PRECOMPUTED ? 1 : nst;
+      r.stats_tiles_t = P.mode != ORDA_TEACHER_PRECOMPUTED ? nst : P.online ? 1 : row_stats_segments(v);
       r.xy_s = xy;
       r.xy_t = xy + btg;
       r.cross = cross;

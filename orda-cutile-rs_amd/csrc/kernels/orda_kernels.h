@@ -160,8 +160,13 @@ struct RowStatsArgs {
   int64_t ignore_index;
   float inv_t;
   bool online;             // one online pass; else a max pass, then a sum pass
+  // With segmented (and !online): one workgroup per 8192-column segment of a
+  // row, held in registers for both passes (one read), statistics of
+  // segment s at stats[r * stats_ld + s]; stats_ld >= row_stats_segments(v).
+  bool segmented;
 };
 hipError_t launch_row_stats(const RowStatsArgs& a, hipStream_t stream);
+int64_t row_stats_segments(int64_t v);
 
 // Zero columns [v, ld) of rows [0, n_rows) (keeps pitch padding zero).
 hipError_t launch_zero_pad_cols(DType t, void* base, int64_t ld, int64_t n_rows, int64_t v,

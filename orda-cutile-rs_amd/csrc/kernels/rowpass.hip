@@ -796,6 +796,62 @@ __global__ __launch_bounds__(kThreads) void row_stats_kernel(RowStatsArgs a) {
   }
 }
 
+// Segmented two-pass statistics: one workgroup per (row, 8192-column
+// segment); each thread holds its 32 columns in registers, so the max pass
+// and the sum pass read HBM once.
+constexpr int kSegCols = 8192;
+constexpr int kSegPer = kSegCols / kThreads;   // 32 columns per thread
+template <typename ST, typename DT>
+__global__ __launch_bounds__(kThreads) void row_stats_seg_kernel(RowStatsArgs a, int64_t nseg) {
+  __shared__ float sred[kThreads / 64];
+  const int64_t r = blockIdx.x / nseg;
+  const int64_t sg = blockIdx.x - r * nseg;
+  const int64_t c0 = sg * kSegCols;
+  const ST* src = static_cast<const ST*>(a.src) + r * a.lds;
+  DT* dst = a.dst ? static_cast<DT*>(a.dst) + r * a.ldd : nullptr;
+  const float it2 = a.inv_t * kLog2e;
+  float x[kSegPer];
+  float m = -INFINITY, sx = 0.f;
+  // Column c0 + k*kThreads + tid for k < kSegPer: each load instruction of a
+  // wave reads 64 consecutive elements.
+#pragma unroll
+  for (int k = 0; k < kSegPer; ++k) {
+    const int64_t j = c0 + k * kThreads + threadIdx.x;
+    x[k] = j < a.v ? static_cast<float>(src[j]) : -INFINITY;
+  }
+#pragma unroll
+  for (int k = 0; k < kSegPer; ++k) {
+    const int64_t j = c0 + k * kThreads + threadIdx.x;
+    if (j < a.v) {
+      m = fmaxf(m, x[k]);
+      sx += x[k];
+      if (dst) dst[j] = static_cast<DT>(x[k]);
+    }
+  }
+  m = block_max(m, sred);
+  const float o1 = -m * kLog2e, oT = -m * it2;
+  float d1 = 0.f, dT = 0.f;
+#pragma unroll
+  for (int k = 0; k < kSegPer; ++k) {
+    // e^(-inf) = 0 for the columns past V
+    d1 += __builtin_amdgcn_exp2f(fmaf(x[k], kLog2e, o1));
+    dT += __builtin_amdgcn_exp2f(fmaf(x[k], it2, oT));
+  }
+  sx = block_sum(sx, sred);
+  d1 = block_sum(d1, sred);
+  dT = block_sum(dT, sred);
+  if (dst && sg == nseg - 1)
+    for (int64_t j = a.v + threadIdx.x; j < a.ldd; j += kThreads) dst[j] = static_cast<DT>(0.f);
+  if (threadIdx.x == 0) {
+    a.stats[r * a.stats_ld + sg] = make_float4(m, d1, dT, sx);
+    if (a.labels) {
+      const int64_t y = a.labels[r];
+      if (y != a.ignore_index && y >= c0 && y < c0 + kSegCols && y < a.v)
+        a.xy[r] = static_cast<float>(src[y]);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ finalize
 __global__ __launch_bounds__(kThreads) void finalize_kernel(FinalizeArgs a) {
   __shared__ double red[3][kThreads];
@@ -911,11 +967,25 @@ hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+int64_t row_stats_segments(int64_t v) { return (v + kSegCols - 1) / kSegCols; }
+
 hipError_t launch_row_stats(const RowStatsArgs& a, hipStream_t s) {
   if (a.n_rows <= 0) return hipSuccess;
   dim3 grid(static_cast<unsigned>(a.n_rows));
   const bool sf = a.src_type == DType::F32;
   const bool df = a.dst_type == DType::F32;
+  if (a.segmented && !a.online) {
+    const int64_t nseg = row_stats_segments(a.v);
+    if (a.stats_ld < nseg) return hipErrorInvalidValue;
+    const int64_t blocks = a.n_rows * nseg;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 g(static_cast<unsigned>(blocks));
+    if (sf && df) hipLaunchKernelGGL((row_stats_seg_kernel<float, float>), g, dim3(kThreads), 0, s, a, nseg);
+    else if (sf) hipLaunchKernelGGL((row_stats_seg_kernel<float, __bf16>), g, dim3(kThreads), 0, s, a, nseg);
+    else if (df) hipLaunchKernelGGL((row_stats_seg_kernel<__bf16, float>), g, dim3(kThreads), 0, s, a, nseg);
+    else hipLaunchKernelGGL((row_stats_seg_kernel<__bf16, __bf16>), g, dim3(kThreads), 0, s, a, nseg);
+    return hipGetLastError();
+  }
 #define ORDA_ROWSTATS(ONLINE)                                                                        \
   if (sf && df) hipLaunchKernelGGL((row_stats_kernel<float, float, ONLINE>), grid, dim3(kThreads), 0, s, a);   \
   else if (sf) hipLaunchKernelGGL((row_stats_kernel<float, __bf16, ONLINE>), grid, dim3(kThreads), 0, s, a);  \
