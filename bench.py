@@ -133,6 +133,14 @@ def work_per_step(wl, plan):
     rows_read = 2 * bt if (kd > 0 or wt > 0) else bt
     ls = 2 if dt == "bf16" and (teacher == "tied" or kd == 0) else 4
     rowpass = rows_read * v * ls + (bt + t_rows_written) * v * es
+    # ... and, to form each row's lse at 1 and at T, the per-row statistics
+    # the logits GEMM wrote: one 16-byte entry per 256-column tile (for
+    # Precomputed teacher logits one per 8192-column segment), the teacher's
+    # 4-byte KL cross partial per tile in the paired bf16 layout, the label.
+    nst = -(-v // 256)
+    t_stats = (-(-v // 8192) if teacher == "precomputed" else nst) if rows_read > bt else 0
+    paired = teacher == "tied" and dt == "bf16" and (kd > 0 or wt > 0)
+    rowpass += bt * (nst * 16 + t_stats * 16 + (nst * 4 if paired else 0) + 8)
     quant_b = v * h * 8 if quant else 0
     return {"gemm_logits": ("mfma", fwd), "gemm_grad_hidden": ("mfma", dgrad),
             "gemm_grad_weight": ("mfma", wgrad), "row_pass": ("hbm", rowpass),
