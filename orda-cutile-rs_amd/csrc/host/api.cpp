@@ -444,13 +444,14 @@ orda::DType logits_dtype(const LossPlan& P, bool paired) {
                                                              : orda::DType::F32;
 }
 
-// Precomputed teacher logits already in the logits dtype, with a pitch of a
-// multiple of 8 elements and a 16-byte aligned base (the row pass reads
-// 16-byte vectors): the row pass reads them where they are instead of from a
-// copy in the staging buffer.
+// Precomputed teacher logits already in the logits dtype, with a pitch and a
+// width of a multiple of 8 elements and a 16-byte aligned base (the row pass
+// reads whole 16-byte vectors of 8 logits, so a narrower last vector would
+// read past the row, and past the tensor's storage on its last row): the row
+// pass reads them where they are instead of from a copy in the staging buffer.
 bool teacher_logits_direct(const LossPlan& P, const Inputs& in) {
   return P.need_teacher && P.mode == ORDA_TEACHER_PRECOMPUTED && in.tl.t == logits_dtype(P, false) &&
-         in.tl.ld % 8 == 0 && reinterpret_cast<uintptr_t>(in.tl.p) % 16 == 0;
+         in.tl.ld % 8 == 0 && in.tl.cols % 8 == 0 && reinterpret_cast<uintptr_t>(in.tl.p) % 16 == 0;
 }
 
 // Device bytes the loss stages per chunk row: the buffers run_loss sizes by
