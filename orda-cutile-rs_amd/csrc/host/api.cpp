@@ -466,8 +466,11 @@ int64_t staged_bytes_per_row(const LossPlan& P, const Inputs& in) {
               (orda::dtype_size(lt) + (lt == P.dt ? 0 : orda::dtype_size(P.dt)));
   b += 2 * nst * 16 + 2 * 4;   // statistics, label logits
   if (paired) b += nst * 4 + 16;   // cross partials, row constants
-  if (P.mode == ORDA_TEACHER_TIED && P.w_t > 0.f)
-    b += 2 * round8(P.h) * orda::dtype_size(P.dt);   // hcat: [h_s; h_t] rows for grad_W
+  // hcat: the hidden rows transposed for grad_W ([h_s; h_t] with a Tied
+  // teacher and teacher CE; else the student's, then the Separate teacher's).
+  b += (P.mode == ORDA_TEACHER_TIED && P.w_t > 0.f ? 2 * P.h
+                                                   : std::max(P.h, P.has_gwt ? P.ht : int64_t{0})) *
+       orda::dtype_size(P.dt);
   return b;
 }
 
@@ -516,8 +519,10 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   float* rnll_s = row3_out;
   float* rnll_t = row3_out + bt;
   float* rkl = row3_out + 2 * bt;
-  const int64_t ldh_cat = round8(h);
-  void* hcat = tied_tce ? ws(c, "hcat", 2 * cap * ldh_cat * es) : nullptr;
+  // The hidden rows of a group transposed ([width][rows], pitch ldh_cat):
+  // the K-major A operand of grad_Wᵀ.
+  const int64_t ldh_cat = round8(tied_tce ? 2 * cap : cap);
+  void* hcat = ws(c, "hcat", std::max(h, P.has_gwt ? P.ht : int64_t{0}) * ldh_cat * es);
   float* cross = paired ? static_cast<float*>(ws(c, "cross", cap * nst * 4)) : nullptr;
   float4* rconst = paired ? static_cast<float4*>(ws(c, "rconst", cap * 16)) : nullptr;
   const float inv_t = 1.0f / P.T;
@@ -690,51 +695,45 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       }
     }
 
-    // ---- grad_W (+)= dlogitsᵀ · hidden (api.rs:350, 360, 367-370)
-    {
+    // ---- grad_W (+)= dlogitsᵀ · hidden (api.rs:350, 360, 367-370), computed
+    // as grad_Wᵀ = hiddenᵀ · dlogits: the group's hidden rows are transposed
+    // into hcat (a K-major A over K = rows), the gradient rows are an N-major
+    // B read in place, and C is stored transposed, i.e. as grad_W. With a
+    // Tied teacher and teacher CE, [h_s; h_t]ᵀ · [dS; dT] is one GEMM over
+    // K = 2·rows (the teacher gradient rows follow the student rows).
+    auto grad_weight = [&](const void* ha, int64_t lda_h, const void* hb, int64_t ldb_h,
+                           int64_t width, const void* D, float* C, int64_t ldc) {
+      const int64_t k = hb != nullptr ? 2 * btg : btg;
+      timed(c, ORDA_KERNEL_OTHER, [&] {
+        return launch_transpose_rows(ha, lda_h, hb, ldb_h, btg, width, hcat, ldh_cat, dt,
+                                     c->stream);
+      });
       GemmArgs w{};
-      w.M = v;
-      w.N = h;
-      w.lda = ldl;
-      w.ldc = in.gw.ld;
-      w.a_kmajor = false;
+      w.M = width;
+      w.N = v;
+      w.K = k;
+      w.lda = ldh_cat;
+      w.ldb = ldl;
+      w.ldc = ldc;
+      w.a_kmajor = true;
       w.b_kmajor = false;
+      w.c_trans = true;
       w.in_type = dt;
       w.epi = first ? GemmEpilogue::StoreF32 : GemmEpilogue::AccumF32;
       w.alpha = 1.f;
       w.alpha_ptr = last ? ms_dev : nullptr;
-      w.group_m = 4;
+      w.group_m = 8;
       w.nprob = 1;
-      if (tied_tce) {
-        // [dS; dT]ᵀ · [h_s; h_t]: one GEMM over K = 2·rows.
-        hip_check(hipMemcpy2DAsync(hcat, ldh_cat * es, at(in.hs.p, gs * in.hs.ld, dt),
-                                   in.hs.ld * es, h * es, btg, hipMemcpyDeviceToDevice, c->stream),
-                  "stage hidden");
-        hip_check(hipMemcpy2DAsync(at(hcat, btg * ldh_cat, dt), ldh_cat * es,
-                                   at(in.th.p, gs * in.th.ld, dt), in.th.ld * es, h * es, btg,
-                                   hipMemcpyDeviceToDevice, c->stream),
-                  "stage hidden");
-        w.K = 2 * btg;
-        w.ldb = ldh_cat;
-        w.prob[0] = {Gs, hcat, in.gw.p};
-      } else {
-        w.K = btg;
-        w.ldb = in.hs.ld;
-        w.prob[0] = {Gs, at(in.hs.p, gs * in.hs.ld, dt), in.gw.p};
-      }
+      w.prob[0] = {hcat, D, C};
       attach_split_ws(c, w);
       timed(c, ORDA_KERNEL_GEMM_GRAD_WEIGHT, [&] { return launch_gemm(w, c->stream); });
-      if (P.has_gwt) {
-        GemmArgs t = w;
-        t.K = btg;
-        t.N = P.ht;
-        t.ldb = in.th.ld;
-        t.ldc = in.gwt.ld;
-        t.prob[0] = {Gt, at(in.th.p, gs * in.th.ld, dt), in.gwt.p};
-        attach_split_ws(c, t);
-        timed(c, ORDA_KERNEL_GEMM_GRAD_WEIGHT, [&] { return launch_gemm(t, c->stream); });
-      }
-    }
+    };
+    grad_weight(at(in.hs.p, gs * in.hs.ld, dt), in.hs.ld,
+                tied_tce ? at(in.th.p, gs * in.th.ld, dt) : nullptr, in.th.ld, h, Gs, in.gw.p,
+                in.gw.ld);
+    if (P.has_gwt)
+      grad_weight(at(in.th.p, gs * in.th.ld, dt), in.th.ld, nullptr, 0, P.ht, Gt, in.gwt.p,
+                  in.gwt.ld);
   }
 
   // ---- loss assembly (api.rs:401-405)

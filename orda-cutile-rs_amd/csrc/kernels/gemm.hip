@@ -4,7 +4,10 @@
 // :346-377, via src/mat.rs:63-130) all run through one kernel template:
 //   logits      C[2n,V]   = [h_s;h_t] · Wᵀ     A K-major, B K-major
 //   grad_hidden C[rows,H] = dlogits · W        A K-major, B N-major
-//   grad_W      C[V,H]    = dlogitsᵀ · hidden  A M-major, B N-major
+//   grad_W      C[V,H]    = (hiddenᵀ · dlogits)ᵀ, computed as
+//               Cᵀ[H,V]   = hiddenᵀ · dlogits  A K-major (the hidden rows
+//               transposed by transpose_rows_kernel), B N-major, C stored
+//               transposed
 //
 // Workgroup tile 256x256, 4 waves each owning 128x128 as 8x8 fragments of
 // 16x16. K advances 64 bytes per stage (32 bf16 / 16 fp32) through a ring of
@@ -1106,6 +1109,40 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       // acc[i][j][e] is row wm*128 + 16i + 4*lgrp + e, column wn*128 + 16j + lrow.
       const int row_w = tc.m0 + wm * 128;
       const int col_l = tc.n0 + wn * 128 + lrow;
+      if (g.c_trans) {
+        // C[n][m]: each lane holds 4 consecutive m of one n, one 16-byte
+        // store where the pitch and base allow (lanes lrow + 16g write 64
+        // contiguous bytes of row n).
+        const bool vec = (g.ldc % 4) == 0 && (reinterpret_cast<uintptr_t>(C) % 16) == 0;
+#pragma unroll
+        for (int j = 0; j < kFrag; ++j) {
+          const int64_t n = col_l + j * 16;
+          if (n >= g.N) continue;
+          float* cn = C + n * g.ldc;
+#pragma unroll
+          for (int i = 0; i < kFrag; ++i) {
+            const int64_t m = row_w + i * 16 + lgrp * 4;
+            f32x4 v = acc[i][j];
+            if (vec && m + 4 <= g.M) {
+              f32x4* dst = reinterpret_cast<f32x4*>(cn + m);
+              if constexpr (EPI == GemmEpilogue::AccumF32) v = alpha * (*dst + v);
+              else v = alpha * v;
+              *dst = v;
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                if (m + e < g.M) {
+                  float x = v[e];
+                  if constexpr (EPI == GemmEpilogue::AccumF32) x = alpha * (cn[m + e] + x);
+                  else x = alpha * x;
+                  cn[m + e] = x;
+                }
+              }
+            }
+          }
+        }
+        return;
+      }
 #pragma unroll
       for (int i = 0; i < kFrag; ++i) {
 #pragma unroll
@@ -1495,7 +1532,7 @@ GemmKernel select_kernel(const GemmArgs& g) {
 // accumulating), the partials summed in split order.
 __global__ void splitk_reduce_kernel(const float* ws, int64_t stride, int splits, int64_t M,
                                      int64_t N, int64_t ldp, float* c0, float* c1, int64_t ldc,
-                                     float alpha0, const float* alpha_ptr, bool accum) {
+                                     float alpha0, const float* alpha_ptr, bool accum, bool trans) {
   const float alpha = alpha_ptr != nullptr ? alpha0 * *alpha_ptr : alpha0;
   const int64_t per = M * N;
   const int64_t total = per * (c1 ? 2 : 1);
@@ -1507,8 +1544,71 @@ __global__ void splitk_reduce_kernel(const float* ws, int64_t stride, int splits
     const float* src = ws + p * M * ldp + m * ldp + n;
     float v = 0.f;
     for (int s = 0; s < splits; ++s) v += src[s * stride];
-    float* dst = (p ? c1 : c0) + m * ldc + n;
+    float* dst = (p ? c1 : c0) + (trans ? n * ldc + m : m * ldc + n);
     *dst = accum ? alpha * (*dst + v) : alpha * v;
+  }
+}
+
+// Transposed staging (launch_transpose_rows): a 64 x 64 block of source
+// rows r and columns c goes through LDS, read as 16-byte row segments when
+// VEC (pitches multiples of 8 elements, bases 16-byte aligned, cols % 8 == 0)
+// and written as 16-byte segments of 8 consecutive r of one column.
+// Element type E is 2 or 4 bytes wide. Rows krows .. round8(krows) - 1 of
+// every column are written as zeros (ldd >= round8(krows) as ldd % 8 == 0).
+template <typename E, bool VEC>
+__global__ __launch_bounds__(256) void transpose_rows_kernel(const E* a, int64_t lda, const E* b,
+                                                             int64_t ldb, int64_t rows,
+                                                             int64_t cols, E* dst, int64_t ldd) {
+  constexpr int kT = 64;
+  __shared__ E tile[kT][kT + 16 / sizeof(E)];
+  const int64_t krows = b != nullptr ? 2 * rows : rows;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kT;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kT;
+  constexpr int kVec = 16 / sizeof(E);   // elements per 16 bytes
+  constexpr int kPerRow = kT / kVec;     // 16-byte segments per tile row
+  const int tid = threadIdx.x;
+  // Load: rows r0.., columns c0.. of the stacked [a; b] rows.
+  for (int q = tid; q < kT * kPerRow; q += 256) {
+    const int rl = q / kPerRow, seg = q % kPerRow;
+    const int64_t r = r0 + rl, c = c0 + seg * kVec;
+    const E* src = nullptr;
+    if (r < krows) src = r < rows ? a + r * lda : b + (r - rows) * ldb;
+    if constexpr (VEC) {
+      typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+      u32x4v w = {0u, 0u, 0u, 0u};
+      if (src != nullptr && c < cols) w = *reinterpret_cast<const u32x4v*>(src + c);
+      const E* e = reinterpret_cast<const E*>(&w);
+#pragma unroll
+      for (int k = 0; k < kVec; ++k) tile[rl][seg * kVec + k] = e[k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < kVec; ++k)
+        tile[rl][seg * kVec + k] = (src != nullptr && c + k < cols) ? src[c + k] : E(0);
+    }
+  }
+  __syncthreads();
+  // Store: column c0 + cl, rows r0 + 8s .. +7 as one 16-byte (2-byte E) or
+  // two 16-byte (4-byte E) segments. The segment holding the last row is
+  // written whole, with zeros past it: a GEMM reading this as a K-major
+  // operand loads the 16-byte chunk that holds its last K element whole,
+  // and the other operand is zero there, so the padding must be finite.
+  constexpr int kSeg = 8;
+  for (int q = tid; q < kT * (kT / kSeg); q += 256) {
+    const int cl = q / (kT / kSeg), s = q % (kT / kSeg);
+    const int64_t c = c0 + cl, r = r0 + s * kSeg;
+    if (c >= cols || r >= krows) continue;
+    E* d = dst + c * ldd + r;
+    if ((reinterpret_cast<uintptr_t>(d) % 16) == 0) {
+      alignas(16) E v[kSeg];
+#pragma unroll
+      for (int k = 0; k < kSeg; ++k) v[k] = tile[s * kSeg + k][cl];
+      typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+#pragma unroll
+      for (int h = 0; h < kSeg * static_cast<int>(sizeof(E)) / 16; ++h)
+        reinterpret_cast<u32x4v*>(d)[h] = reinterpret_cast<const u32x4v*>(v)[h];
+    } else {
+      for (int k = 0; k < kSeg; ++k) d[k] = tile[s * kSeg + k][cl];
+    }
   }
 }
 
@@ -1547,6 +1647,42 @@ SplitPlan plan_split(const GemmArgs& g) {
 
 int64_t gemm_stat_tiles(int64_t n) { return (n + kTile - 1) / kTile; }
 
+hipError_t launch_transpose_rows(const void* a, int64_t lda, const void* b, int64_t ldb,
+                                 int64_t rows, int64_t cols, void* dst, int64_t ldd, DType t,
+                                 hipStream_t stream) {
+  const int64_t krows = b != nullptr ? 2 * rows : rows;
+  if (rows < 0 || cols < 0 || ldd < krows || (ldd % 8) != 0) return hipErrorInvalidValue;
+  if (rows == 0 || cols == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((krows + 63) / 64), static_cast<unsigned>((cols + 63) / 64));
+  const int es = dtype_size(t);
+  const bool vec = (lda % 8) == 0 && (b == nullptr || (ldb % 8) == 0) && (cols % 8) == 0 &&
+                   (reinterpret_cast<uintptr_t>(a) % 16) == 0 &&
+                   (reinterpret_cast<uintptr_t>(b) % 16) == 0;
+  (void)es;
+  if (t == DType::BF16) {
+    const auto* pa = static_cast<const uint16_t*>(a);
+    const auto* pb = static_cast<const uint16_t*>(b);
+    auto* pd = static_cast<uint16_t*>(dst);
+    if (vec)
+      hipLaunchKernelGGL((transpose_rows_kernel<uint16_t, true>), grid, dim3(256), 0, stream, pa,
+                         lda, pb, ldb, rows, cols, pd, ldd);
+    else
+      hipLaunchKernelGGL((transpose_rows_kernel<uint16_t, false>), grid, dim3(256), 0, stream, pa,
+                         lda, pb, ldb, rows, cols, pd, ldd);
+  } else {
+    const auto* pa = static_cast<const uint32_t*>(a);
+    const auto* pb = static_cast<const uint32_t*>(b);
+    auto* pd = static_cast<uint32_t*>(dst);
+    if (vec)
+      hipLaunchKernelGGL((transpose_rows_kernel<uint32_t, true>), grid, dim3(256), 0, stream, pa,
+                         lda, pb, ldb, rows, cols, pd, ldd);
+    else
+      hipLaunchKernelGGL((transpose_rows_kernel<uint32_t, false>), grid, dim3(256), 0, stream, pa,
+                         lda, pb, ldb, rows, cols, pd, ldd);
+  }
+  return hipGetLastError();
+}
+
 int64_t gemm_split_bytes(const GemmArgs& g) {
   const SplitPlan sp = plan_split(g);
   return sp.splits > 1 ? sp.bytes : 0;
@@ -1554,6 +1690,8 @@ int64_t gemm_split_bytes(const GemmArgs& g) {
 
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
   if (g.nprob < 1 || g.nprob > 2) return hipErrorInvalidValue;
+  if (g.c_trans && (g.epi == GemmEpilogue::Logits || !g.a_kmajor))
+    return hipErrorInvalidValue;   // only the unswapped store epilogue transposes
   if ((g.lda % 8) || (g.ldb % 8) || (g.ldc % 8 && g.epi == GemmEpilogue::Logits))
     return hipErrorInvalidValue;
   if (g.epi == GemmEpilogue::Logits && g.lg.pair_rows > 0 &&
@@ -1570,6 +1708,7 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
     s.epi = GemmEpilogue::StoreF32;
     s.alpha = 1.f;
     s.alpha_ptr = nullptr;
+    s.c_trans = false;
     s.ldc = sp.ldp;
     s.split_k = sp.splits;
     s.split_len = sp.len;
@@ -1584,7 +1723,7 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, g.split_ws,
                        sp.stride, sp.splits, g.M, g.N, sp.ldp, static_cast<float*>(g.prob[0].c),
                        g.nprob > 1 ? static_cast<float*>(g.prob[1].c) : nullptr, g.ldc, g.alpha,
-                       g.alpha_ptr, g.epi == GemmEpilogue::AccumF32);
+                       g.alpha_ptr, g.epi == GemmEpilogue::AccumF32, g.c_trans);
     return hipGetLastError();
   }
   GemmArgs one = g;

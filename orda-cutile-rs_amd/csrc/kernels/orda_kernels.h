@@ -68,6 +68,9 @@ struct GemmArgs {
   // the deferred mean computed on the device by launch_label_check).
   const float* alpha_ptr;
   int group_m;            // M-tiles per raster group (L2 reuse of B)
+  // Store/Accum only: C is stored transposed, element (m, n) of the
+  // product at C[n*ldc + m] (C is [N][ldc]).
+  bool c_trans;
   LogitStatsArgs lg;
   // Split-K workspace for Store/Accum GEMMs with fewer tiles than CUs: when
   // given (gemm_split_bytes(g) bytes), launch_gemm splits K over several
@@ -81,6 +84,13 @@ struct GemmArgs {
 };
 
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);
+// Transposed staging of hidden rows for a K-major operand over rows:
+//   dst[c*ldd + r]          = a[r*lda + c]   (r < rows)
+//   dst[c*ldd + rows + r]   = b[r*ldb + c]   (r < rows, when b is set)
+// for c < cols; ldd >= rows (or 2*rows), a multiple of 8.
+hipError_t launch_transpose_rows(const void* a, int64_t lda, const void* b, int64_t ldb,
+                                 int64_t rows, int64_t cols, void* dst, int64_t ldd, DType t,
+                                 hipStream_t stream);
 // Workspace bytes launch_gemm uses to split K for this GEMM (0: no split).
 int64_t gemm_split_bytes(const GemmArgs& g);
 int64_t gemm_stat_tiles(int64_t n);   // ceil(n/256)
