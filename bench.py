@@ -230,8 +230,8 @@ KERNEL_CLASSES = (
     # (substring of the kernel name, kernel kind)
     ("gemm_kk_logits_", "gemm_logits"),
     ("gemm_km_", "gemm_grad_hidden"),
-    ("gemm_mm_", "gemm_grad_weight"),
-    ("gemm_kk_", "gemm_nt"),
+    ("gemm_kmt_", "gemm_grad_weight"),
+    ("transpose_rows", "transpose_rows"),   # grad_W's A operand: hidden rows transposed
     ("row_pass_", "row_pass"),            # row_pass_fused_kernel, row_pass_kernel
     ("row_consts_", "row_consts"),        # the chunked row pass: per-row constants ...
     ("row_grad_", "row_grad"),            # ... and the elementwise gradient

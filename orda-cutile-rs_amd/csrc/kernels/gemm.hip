@@ -101,7 +101,6 @@ __device__ __forceinline__ int mnf_swz(int r) { return 4 * ((r >> 2) & 3); }
 constexpr int kWaitAll = 0x0070;                              // vmcnt(0) lgkmcnt(0)
 constexpr int vm_wait(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
 constexpr int kWaitTwoStages = vm_wait(2 * 2 * kXfers);     // stage s+1 landed
-constexpr int kWaitThreeStages = vm_wait(3 * 2 * kXfers);   // stage 0 landed
 constexpr int kWaitLds = 0xC07F;                              // lgkmcnt(0) only
 
 // One DMA transfer: every active lane copies the 16 bytes at sbase + voff
@@ -543,7 +542,7 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-template <typename T, bool AK, bool BK, GemmEpilogue EPI, typename LT>
+template <typename T, bool AK, bool BK, GemmEpilogue EPI, typename LT, bool CT>
 __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
   // Ring layout: A tiles of slots 0-3, then B tiles of slots 0-3 (16 KB
   // each), so every slot offset fits a DS instruction's immediate.
@@ -940,101 +939,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       }
       st_done = ns;
     } else {
-      // Single stages: iteration s (stage s in slot s%4 and register set
-      // s%2) (1) waits until stage s+1 has landed (stages s+2, s+3 may still
-      // be in flight) and every wave has finished reading stage s out of its
-      // slot; (2) reads stage s+1's fragments into the other register set;
-      // (3) DMAs stage s+4 into stage s's slot; (4) runs the 64 MFMAs of
-      // stage s, with side operation o (the stage's LDS reads first, then
-      // its eight DMA transfers) issued with MFMA pair (o * 32) / kSide.
-      // Every iteration issues the same number of DMA transfers (past the
-      // last full stage, an in-bounds dummy copy of stage 0 into a slot
-      // nobody reads again), so one constant vmcnt wait always means "stage
-      // s+1 has landed". An iteration whose stage s+1 does not exist reads a
-      // slot whose contents are never used.
-      Loader<T, AK> la;
-      LoaderB lb;
-      init_a(la);
-      init_b(lb);
-      if (nkf > 0) {
-#pragma unroll
-        for (int t = 0; t < kRing; ++t) {
-          const int src = t < nkf ? t : 0;
-          la.issue(tileA(t), src, wave, lane);
-          lb.issue(tileB(t), src, wave, lane);
-        }
-        __builtin_amdgcn_s_waitcnt(kWaitThreeStages);
-        __builtin_amdgcn_s_barrier();
-        read_stage(0, ra[0], rb[0]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      constexpr int kOpsA = FragReader<AK, AK>::kOps, kOpsB = FragReader<BK, kPaired>::kOps;
-      constexpr int kReads = kOpsA + kOpsB;
-      constexpr int kSide = kReads + 2 * kXfers;
-      constexpr int kPairDma = (kReads * 32) / kSide;   // first pair carrying a DMA
-      auto iter = [&](auto slot_c, int st, u32x4 (&rnA)[kFrag], u32x4 (&rnB)[kFrag],
-                      const u32x4 (&rcA)[kFrag], const u32x4 (&rcB)[kFrag]) {
-        constexpr int S = decltype(slot_c)::value;       // slot of stage s
-        constexpr int SN = (S + 1) % kRing;              // slot of stage s+1
-        constexpr int MA = S * kOpBytes;                 // DMA targets, from m0wave
-        constexpr int MB = (kRing + S) * kOpBytes;
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(kWaitTwoStages);
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-        uint64_t sa = 0, sb = 0;
-#pragma unroll
-        for (int pr = 0; pr < 32; ++pr) {
-          if (pr == kPairDma - 2) {
-            // DMA sources of stage s+4, computed here so the scalar work
-            // overlaps MFMAs instead of delaying the first one.
-            const int nxt = st + kRing < nkf ? st + kRing : 0;
-            sa = uniform64(la.stage_src(nxt));
-            sb = uniform64(lb.stage_src(nxt));
-          }
-#pragma unroll
-          for (int o = 0; o < kSide; ++o) {
-            if ((o * 32) / kSide != pr) continue;
-            if (o < kOpsA) {
-              fa.template read_op<SN>(o, rnA);
-            } else if (o < kReads) {
-              fb.template read_op<SN>(o - kOpsA, rnB);
-            } else {
-              switch (o - kReads) {   // 0-3: A transfers, 4-7: B transfers
-                case 0: dma16_at<MA + 0 * 4096>(sa, la.goff[0], m0wave); break;
-                case 1: dma16_at<MA + 1 * 4096>(sa, la.goff[1], m0wave); break;
-                case 2: dma16_at<MA + 2 * 4096>(sa, la.goff[2], m0wave); break;
-                case 3: dma16_at<MA + 3 * 4096>(sa, la.goff[3], m0wave); break;
-                case 4: dma16_at<MB + 0 * 4096>(sb, lb.goff[0], m0wave); break;
-                case 5: dma16_at<MB + 1 * 4096>(sb, lb.goff[1], m0wave); break;
-                case 6: dma16_at<MB + 2 * 4096>(sb, lb.goff[2], m0wave); break;
-                default: dma16_at<MB + 3 * 4096>(sb, lb.goff[3], m0wave); break;
-              }
-            }
-          }
-#pragma unroll
-          for (int q = 0; q < 2; ++q) {
-            const int mm = 2 * pr + q;
-            if constexpr (kSwapAB)
-              mfma_bf16(acc[mm & 7][mm >> 3], rcB[mm >> 3], rcA[mm & 7]);
-            else
-              mfma_bf16(acc[mm >> 3][mm & 7], rcA[mm >> 3], rcB[mm & 7]);
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      };
-      int s0 = 0;
-      for (; s0 + 3 < nkf; s0 += 4) {
-        iter(SlotC<0>{}, s0, ra[1], rb[1], ra[0], rb[0]);
-        iter(SlotC<1>{}, s0 + 1, ra[0], rb[0], ra[1], rb[1]);
-        iter(SlotC<2>{}, s0 + 2, ra[1], rb[1], ra[0], rb[0]);
-        iter(SlotC<3>{}, s0 + 3, ra[0], rb[0], ra[1], rb[1]);
-      }
-      const int rem = nkf - s0;
-      if (rem >= 1) iter(SlotC<0>{}, s0, ra[1], rb[1], ra[0], rb[0]);
-      if (rem >= 2) iter(SlotC<1>{}, s0 + 1, ra[0], rb[0], ra[1], rb[1]);
-      if (rem >= 3) iter(SlotC<2>{}, s0 + 2, ra[1], rb[1], ra[0], rb[0]);
-      st_done = nkf;
+      static_assert(AK, "the bf16 GEMMs take a K-major A");
     }
     __builtin_amdgcn_sched_barrier(0);
     mfma_drain();
@@ -1109,7 +1014,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       // acc[i][j][e] is row wm*128 + 16i + 4*lgrp + e, column wn*128 + 16j + lrow.
       const int row_w = tc.m0 + wm * 128;
       const int col_l = tc.n0 + wn * 128 + lrow;
-      if (g.c_trans) {
+      if constexpr (CT) {
         // C[n][m]: each lane holds 4 consecutive m of one n, one 16-byte
         // store where the pitch and base allow (lanes lrow + 16g write 64
         // contiguous bytes of row n).
@@ -1486,26 +1391,24 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
 
 
 // One named entry point per variant, so that profiles and the build's ISA
-// check can tell them apart: gemm_<A layout><B layout>_<epilogue>_<input>
-// [_<logits type>], layout k = K-major, m = M/N-major.
-#define ORDA_GEMM(NAME, T, AK, BK, EPI, LT) \
-  __global__ __launch_bounds__(kThreads, 1) void NAME(GemmArgs g) { gemm_body<T, AK, BK, EPI, LT>(g); }
-ORDA_GEMM(gemm_kk_logits_bf16_bf16, __bf16, true, true, GemmEpilogue::Logits, __bf16)
-ORDA_GEMM(gemm_kk_logits_bf16_f32, __bf16, true, true, GemmEpilogue::Logits, float)
-ORDA_GEMM(gemm_kk_store_bf16, __bf16, true, true, GemmEpilogue::StoreF32, float)
-ORDA_GEMM(gemm_kk_accum_bf16, __bf16, true, true, GemmEpilogue::AccumF32, float)
-ORDA_GEMM(gemm_km_store_bf16, __bf16, true, false, GemmEpilogue::StoreF32, float)
-ORDA_GEMM(gemm_km_accum_bf16, __bf16, true, false, GemmEpilogue::AccumF32, float)
-ORDA_GEMM(gemm_mm_store_bf16, __bf16, false, false, GemmEpilogue::StoreF32, float)
-ORDA_GEMM(gemm_mm_accum_bf16, __bf16, false, false, GemmEpilogue::AccumF32, float)
-ORDA_GEMM(gemm_kk_logits_f32_bf16, float, true, true, GemmEpilogue::Logits, __bf16)
-ORDA_GEMM(gemm_kk_logits_f32_f32, float, true, true, GemmEpilogue::Logits, float)
-ORDA_GEMM(gemm_kk_store_f32, float, true, true, GemmEpilogue::StoreF32, float)
-ORDA_GEMM(gemm_kk_accum_f32, float, true, true, GemmEpilogue::AccumF32, float)
-ORDA_GEMM(gemm_km_store_f32, float, true, false, GemmEpilogue::StoreF32, float)
-ORDA_GEMM(gemm_km_accum_f32, float, true, false, GemmEpilogue::AccumF32, float)
-ORDA_GEMM(gemm_mm_store_f32, float, false, false, GemmEpilogue::StoreF32, float)
-ORDA_GEMM(gemm_mm_accum_f32, float, false, false, GemmEpilogue::AccumF32, float)
+// check can tell them apart: gemm_<A layout><B layout>[t]_<epilogue>_<input>
+// [_<logits type>], layout k = K-major, m = N-major, t = C stored
+// transposed. The loss uses exactly these products: the logits (kk), the
+// hidden-row gradients (km) and grad_W computed transposed (kmt).
+#define ORDA_GEMM(NAME, T, AK, BK, EPI, LT, CT) \
+  __global__ __launch_bounds__(kThreads, 1) void NAME(GemmArgs g) { gemm_body<T, AK, BK, EPI, LT, CT>(g); }
+ORDA_GEMM(gemm_kk_logits_bf16_bf16, __bf16, true, true, GemmEpilogue::Logits, __bf16, false)
+ORDA_GEMM(gemm_kk_logits_bf16_f32, __bf16, true, true, GemmEpilogue::Logits, float, false)
+ORDA_GEMM(gemm_km_store_bf16, __bf16, true, false, GemmEpilogue::StoreF32, float, false)
+ORDA_GEMM(gemm_km_accum_bf16, __bf16, true, false, GemmEpilogue::AccumF32, float, false)
+ORDA_GEMM(gemm_kmt_store_bf16, __bf16, true, false, GemmEpilogue::StoreF32, float, true)
+ORDA_GEMM(gemm_kmt_accum_bf16, __bf16, true, false, GemmEpilogue::AccumF32, float, true)
+ORDA_GEMM(gemm_kk_logits_f32_bf16, float, true, true, GemmEpilogue::Logits, __bf16, false)
+ORDA_GEMM(gemm_kk_logits_f32_f32, float, true, true, GemmEpilogue::Logits, float, false)
+ORDA_GEMM(gemm_km_store_f32, float, true, false, GemmEpilogue::StoreF32, float, false)
+ORDA_GEMM(gemm_km_accum_f32, float, true, false, GemmEpilogue::AccumF32, float, false)
+ORDA_GEMM(gemm_kmt_store_f32, float, true, false, GemmEpilogue::StoreF32, float, true)
+ORDA_GEMM(gemm_kmt_accum_f32, float, true, false, GemmEpilogue::AccumF32, float, true)
 #undef ORDA_GEMM
 
 typedef void (*GemmKernel)(GemmArgs);
@@ -1514,18 +1417,15 @@ GemmKernel select_kernel(const GemmArgs& g) {
   using E = GemmEpilogue;
   const bool bf = g.in_type == DType::BF16;
   if (g.epi == E::Logits) {
-    if (!g.a_kmajor || !g.b_kmajor) return nullptr;
+    if (!g.a_kmajor || !g.b_kmajor || g.c_trans) return nullptr;
     if (g.logits_type == DType::BF16) return bf ? gemm_kk_logits_bf16_bf16 : gemm_kk_logits_f32_bf16;
     return bf ? gemm_kk_logits_bf16_f32 : gemm_kk_logits_f32_f32;
   }
+  if (!g.a_kmajor || g.b_kmajor) return nullptr;
   const bool st = g.epi == E::StoreF32;
-  if (g.a_kmajor && g.b_kmajor)
-    return bf ? (st ? gemm_kk_store_bf16 : gemm_kk_accum_bf16) : (st ? gemm_kk_store_f32 : gemm_kk_accum_f32);
-  if (g.a_kmajor && !g.b_kmajor)
-    return bf ? (st ? gemm_km_store_bf16 : gemm_km_accum_bf16) : (st ? gemm_km_store_f32 : gemm_km_accum_f32);
-  if (!g.a_kmajor && !g.b_kmajor)
-    return bf ? (st ? gemm_mm_store_bf16 : gemm_mm_accum_bf16) : (st ? gemm_mm_store_f32 : gemm_mm_accum_f32);
-  return nullptr;
+  if (g.c_trans)
+    return bf ? (st ? gemm_kmt_store_bf16 : gemm_kmt_accum_bf16) : (st ? gemm_kmt_store_f32 : gemm_kmt_accum_f32);
+  return bf ? (st ? gemm_km_store_bf16 : gemm_km_accum_bf16) : (st ? gemm_km_store_f32 : gemm_km_accum_f32);
 }
 
 // Split-K reduction: C = alpha * (Σ_s partial_s) (+ alpha * C when
@@ -1690,8 +1590,6 @@ int64_t gemm_split_bytes(const GemmArgs& g) {
 
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
   if (g.nprob < 1 || g.nprob > 2) return hipErrorInvalidValue;
-  if (g.c_trans && (g.epi == GemmEpilogue::Logits || !g.a_kmajor))
-    return hipErrorInvalidValue;   // only the unswapped store epilogue transposes
   if ((g.lda % 8) || (g.ldb % 8) || (g.ldc % 8 && g.epi == GemmEpilogue::Logits))
     return hipErrorInvalidValue;
   if (g.epi == GemmEpilogue::Logits && g.lg.pair_rows > 0 &&

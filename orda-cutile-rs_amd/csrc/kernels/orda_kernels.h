@@ -15,8 +15,9 @@ inline int dtype_size(DType t) { return t == DType::F32 ? 4 : 2; }
 // ---------------------------------------------------------------- GEMM
 // One launch computes up to two problems that share M, N, K and pitches:
 //   C_p[M,N] (op)= alpha * A_p · B_p
-// A is K-major ([M][lda], element (m,k) at m*lda+k) or M-major ([K][lda],
-// (m,k) at k*lda+m); likewise B is K-major ([N][ldb]) or N-major ([K][ldb]).
+// A is K-major ([M][lda], element (m,k) at m*lda+k). B is K-major ([N][ldb],
+// (n,k) at n*ldb+k) for the Logits epilogue and N-major ([K][ldb], (n,k) at
+// k*ldb+n) for Store/Accum; other layouts are rejected.
 // Pitches are in elements and must be multiples of 8; base pointers 16-byte
 // aligned. Out-of-range rows/columns/K are zero-filled on load and masked on
 // store.
