@@ -1554,11 +1554,9 @@ hipError_t launch_transpose_rows(const void* a, int64_t lda, const void* b, int6
   if (rows < 0 || cols < 0 || ldd < krows || (ldd % 8) != 0) return hipErrorInvalidValue;
   if (rows == 0 || cols == 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>((krows + 63) / 64), static_cast<unsigned>((cols + 63) / 64));
-  const int es = dtype_size(t);
   const bool vec = (lda % 8) == 0 && (b == nullptr || (ldb % 8) == 0) && (cols % 8) == 0 &&
                    (reinterpret_cast<uintptr_t>(a) % 16) == 0 &&
                    (reinterpret_cast<uintptr_t>(b) % 16) == 0;
-  (void)es;
   if (t == DType::BF16) {
     const auto* pa = static_cast<const uint16_t*>(a);
     const auto* pb = static_cast<const uint16_t*>(b);
