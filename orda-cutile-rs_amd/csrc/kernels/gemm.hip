@@ -609,10 +609,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
     for (int j = 0; j < kFrag; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   constexpr int SK = kSlab / Elem<T>::kSize;
-  // The logits epilogue, and the store epilogue of grad_W (A M-major),
-  // take swapped MFMA operands, so that each lane owns 4 consecutive columns
-  // of a row (the grad_hidden loop measured faster unswapped).
-  constexpr bool kSwapAB = EPI == GemmEpilogue::Logits || !AK;
+  // The logits epilogue takes swapped MFMA operands, so that each lane owns
+  // 4 consecutive columns of a row; the store epilogues (grad_hidden, and
+  // grad_W computed transposed) take them unswapped.
+  constexpr bool kSwapAB = EPI == GemmEpilogue::Logits;
 
   const int nkf = static_cast<int>(Kl / SK);   // full stages
   u32x4 ra[2][kFrag], rb[2][kFrag];
@@ -1010,93 +1010,59 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
   if constexpr (EPI == GemmEpilogue::StoreF32 || EPI == GemmEpilogue::AccumF32) {
     float* C = static_cast<float*>(pr.c);
     const float alpha = g.alpha_ptr != nullptr ? g.alpha * *g.alpha_ptr : g.alpha;
-    if constexpr (!kSwapAB) {
-      // acc[i][j][e] is row wm*128 + 16i + 4*lgrp + e, column wn*128 + 16j + lrow.
-      const int row_w = tc.m0 + wm * 128;
-      const int col_l = tc.n0 + wn * 128 + lrow;
-      if constexpr (CT) {
-        // C[n][m]: each lane holds 4 consecutive m of one n, one 16-byte
-        // store where the pitch and base allow (lanes lrow + 16g write 64
-        // contiguous bytes of row n).
-        const bool vec = (g.ldc % 4) == 0 && (reinterpret_cast<uintptr_t>(C) % 16) == 0;
+    static_assert(!kSwapAB, "the store epilogues take unswapped operands");
+    // acc[i][j][e] is row wm*128 + 16i + 4*lgrp + e, column wn*128 + 16j + lrow.
+    const int row_w = tc.m0 + wm * 128;
+    const int col_l = tc.n0 + wn * 128 + lrow;
+    if constexpr (CT) {
+      // C[n][m]: each lane holds 4 consecutive m of one n, one 16-byte
+      // store where the pitch and base allow (lanes lrow + 16g write 64
+      // contiguous bytes of row n).
+      const bool vec = (g.ldc % 4) == 0 && (reinterpret_cast<uintptr_t>(C) % 16) == 0;
 #pragma unroll
-        for (int j = 0; j < kFrag; ++j) {
-          const int64_t n = col_l + j * 16;
-          if (n >= g.N) continue;
-          float* cn = C + n * g.ldc;
+      for (int j = 0; j < kFrag; ++j) {
+        const int64_t n = col_l + j * 16;
+        if (n >= g.N) continue;
+        float* cn = C + n * g.ldc;
 #pragma unroll
-          for (int i = 0; i < kFrag; ++i) {
-            const int64_t m = row_w + i * 16 + lgrp * 4;
-            f32x4 v = acc[i][j];
-            if (vec && m + 4 <= g.M) {
-              f32x4* dst = reinterpret_cast<f32x4*>(cn + m);
-              if constexpr (EPI == GemmEpilogue::AccumF32) v = alpha * (*dst + v);
-              else v = alpha * v;
-              *dst = v;
-            } else {
+        for (int i = 0; i < kFrag; ++i) {
+          const int64_t m = row_w + i * 16 + lgrp * 4;
+          f32x4 v = acc[i][j];
+          if (vec && m + 4 <= g.M) {
+            f32x4* dst = reinterpret_cast<f32x4*>(cn + m);
+            if constexpr (EPI == GemmEpilogue::AccumF32) v = alpha * (*dst + v);
+            else v = alpha * v;
+            *dst = v;
+          } else {
 #pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                if (m + e < g.M) {
-                  float x = v[e];
-                  if constexpr (EPI == GemmEpilogue::AccumF32) x = alpha * (cn[m + e] + x);
-                  else x = alpha * x;
-                  cn[m + e] = x;
-                }
+            for (int e = 0; e < 4; ++e) {
+              if (m + e < g.M) {
+                float x = v[e];
+                if constexpr (EPI == GemmEpilogue::AccumF32) x = alpha * (cn[m + e] + x);
+                else x = alpha * x;
+                cn[m + e] = x;
               }
-            }
-          }
-        }
-        return;
-      }
-#pragma unroll
-      for (int i = 0; i < kFrag; ++i) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t row = row_w + i * 16 + lgrp * 4 + e;
-          if (row >= g.M) continue;
-          float* crow = C + row * g.ldc;
-#pragma unroll
-          for (int j = 0; j < kFrag; ++j) {
-            const int64_t col = col_l + j * 16;
-            if (col < g.N) {
-              float v = acc[i][j][e];
-              if constexpr (EPI == GemmEpilogue::AccumF32) v = alpha * (crow[col] + v);
-              else v = alpha * v;
-              crow[col] = v;
             }
           }
         }
       }
       return;
     }
-    // acc[i][j][e] is row wm*128 + 16i + lrow, column wn*128 + 16j + 4*lgrp + e
-    // (swapped operands): each lane writes 4 consecutive columns of a row as
-    // one 16-byte store where the pitch and base allow.
-    const bool vec = (g.ldc % 4) == 0 && (reinterpret_cast<uintptr_t>(C) % 16) == 0;
-    const int64_t col0 = static_cast<int64_t>(tc.n0) + wn * 128 + 4 * lgrp;
 #pragma unroll
     for (int i = 0; i < kFrag; ++i) {
-      const int64_t row = static_cast<int64_t>(tc.m0) + wm * 128 + i * 16 + lrow;
-      if (row >= g.M) continue;
-      float* crow = C + row * g.ldc + col0;
 #pragma unroll
-      for (int j = 0; j < kFrag; ++j) {
-        const int64_t col = col0 + j * 16;
-        f32x4 v = acc[i][j];
-        if (vec && col + 4 <= g.N) {
-          f32x4* dst = reinterpret_cast<f32x4*>(crow + j * 16);
-          if constexpr (EPI == GemmEpilogue::AccumF32) v = alpha * (*dst + v);
-          else v = alpha * v;
-          *dst = v;
-        } else {
+      for (int e = 0; e < 4; ++e) {
+        const int64_t row = row_w + i * 16 + lgrp * 4 + e;
+        if (row >= g.M) continue;
+        float* crow = C + row * g.ldc;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (col + e < g.N) {
-              float x = v[e];
-              if constexpr (EPI == GemmEpilogue::AccumF32) x = alpha * (crow[j * 16 + e] + x);
-              else x = alpha * x;
-              crow[j * 16 + e] = x;
-            }
+        for (int j = 0; j < kFrag; ++j) {
+          const int64_t col = col_l + j * 16;
+          if (col < g.N) {
+            float v = acc[i][j][e];
+            if constexpr (EPI == GemmEpilogue::AccumF32) v = alpha * (crow[col] + v);
+            else v = alpha * v;
+            crow[col] = v;
           }
         }
       }
