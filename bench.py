@@ -240,7 +240,6 @@ KERNEL_CLASSES = (
     ("quant_", "quant"),                  # quant_vec_kernel, quant_kernel
     ("mark_targets", "mark_targets"),
     ("convert_rows", "convert_rows"),
-    ("zero_pad", "zero_pad"),
 )
 COPY_KERNEL = "copyBuffer"          # HIP runtime's device-to-device copy kernel
 

@@ -179,10 +179,6 @@ struct RowStatsArgs {
 hipError_t launch_row_stats(const RowStatsArgs& a, hipStream_t stream);
 int64_t row_stats_segments(int64_t v);
 
-// Zero columns [v, ld) of rows [0, n_rows) (keeps pitch padding zero).
-hipError_t launch_zero_pad_cols(DType t, void* base, int64_t ld, int64_t n_rows, int64_t v,
-                                hipStream_t stream);
-
 // ---------------------------------------------------------------- reductions
 // Sums per-row losses into the reference's scalars (api.rs:401-405):
 // out[0..3] = loss, student_ce, teacher_ce, kl (as float).

@@ -898,15 +898,6 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(FinalizeArgs a) {
   }
 }
 
-template <typename T>
-__global__ void zero_pad_kernel(T* base, int64_t ld, int64_t n_rows, int64_t v) {
-  const int64_t w = ld - v;
-  const int64_t total = n_rows * w;
-  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    base[(i / w) * ld + v + i % w] = static_cast<T>(0.f);
-}
-
 }  // namespace
 
 hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
@@ -1007,20 +998,6 @@ hipError_t launch_row_stats(const RowStatsArgs& a, hipStream_t s) {
 
 hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(kThreads), 0, s, a);
-  return hipGetLastError();
-}
-
-hipError_t launch_zero_pad_cols(DType t, void* base, int64_t ld, int64_t n_rows, int64_t v,
-                                hipStream_t s) {
-  if (ld <= v || n_rows <= 0) return hipSuccess;
-  const int64_t total = n_rows * (ld - v);
-  const unsigned blocks = static_cast<unsigned>(total / 256 + 1 < 4096 ? total / 256 + 1 : 4096);
-  if (t == DType::BF16)
-    hipLaunchKernelGGL(zero_pad_kernel<__bf16>, dim3(blocks), dim3(256), 0, s,
-                       static_cast<__bf16*>(base), ld, n_rows, v);
-  else
-    hipLaunchKernelGGL(zero_pad_kernel<float>, dim3(blocks), dim3(256), 0, s,
-                       static_cast<float*>(base), ld, n_rows, v);
   return hipGetLastError();
 }
 
