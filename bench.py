@@ -170,7 +170,11 @@ def cpu_baseline(wl, sample_rows=(2, 4, 6)):
     and 6 rows (same H, V and options). A least-squares line through the three
     timings gives the cost per row and per chunk (the residual is reported);
     the per-call INT8 step is timed on its own so that it is not counted once
-    per chunk. Extrapolated to the full BT in the Auto plan's chunks."""
+    per chunk. Extrapolated to the full BT in the Auto plan's chunks.
+
+    The same measurement with the oracle's products, element-wise loops and
+    INT8 rows shared out over the process's cores (OMP_NUM_THREADS at most;
+    results bitwise the same) is reported beside it as `all_cores`."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle as O
@@ -191,38 +195,58 @@ def cpu_baseline(wl, sample_rows=(2, 4, 6)):
             t = H.Teacher.Precomputed(rng.standard_normal((n, v), dtype=np.float32) * 2)
         return s, y, t
     opts = options(H, wl)
-    times = []
-    for n in sample_rows:
-        s, y, t = mk(n)
-        t0 = time.perf_counter()
-        O.distillation_loss(s, w, y, t, opts)
-        times.append(time.perf_counter() - t0)
-        log(f"cpu oracle sample BT={n}: {times[-1]:.2f} s")
-    per_call = 0.0
-    if quant:
-        g = (rng.standard_normal((v, h), dtype=np.float32) * 1e-4).astype(np.float32)
-        t0 = time.perf_counter()
-        O.quant_dequant_grad_w(g, np.arange(8), -100)
-        per_call = time.perf_counter() - t0
-        log(f"cpu oracle INT8 step alone: {per_call:.2f} s")
-    x = np.array(sample_rows, np.float64)
-    tt = np.array(times, np.float64)
-    per_row, fixed = np.polyfit(x, tt, 1)
-    per_row = max(float(per_row), 1e-9)
-    resid = float(np.sqrt(np.mean((tt - (per_row * x + fixed)) ** 2)))
-    per_chunk = max(float(fixed) - per_call, 0.0)
+    samples = [mk(n) for n in sample_rows]
+    g = (rng.standard_normal((v, h), dtype=np.float32) * 1e-4).astype(np.float32) if quant else None
     plan = H.resolve_chunk_size(bt, H.ChunkSize.Auto, v, None)
-    est = bt * per_row + plan.num_chunks * per_chunk + per_call
+
+    def measure(label):
+        times = []
+        for n, (s, y, t) in zip(sample_rows, samples):
+            t0 = time.perf_counter()
+            O.distillation_loss(s, w, y, t, opts)
+            times.append(time.perf_counter() - t0)
+            log(f"cpu oracle ({label}) sample BT={n}: {times[-1]:.2f} s")
+        per_call = 0.0
+        if quant:
+            t0 = time.perf_counter()
+            O.quant_dequant_grad_w(g, np.arange(8), -100)
+            per_call = time.perf_counter() - t0
+            log(f"cpu oracle ({label}) INT8 step alone: {per_call:.2f} s")
+        x = np.array(sample_rows, np.float64)
+        tt = np.array(times, np.float64)
+        per_row, fixed = np.polyfit(x, tt, 1)
+        per_row = max(float(per_row), 1e-9)
+        resid = float(np.sqrt(np.mean((tt - (per_row * x + fixed)) ** 2)))
+        per_chunk = max(float(fixed) - per_call, 0.0)
+        est = bt * per_row + plan.num_chunks * per_chunk + per_call
+        text = (f"one chunk of {', '.join(map(str, sample_rows))} rows of this workload "
+                f"(same H, V, options; the reference's f32/f64 arithmetic), timed "
+                f"{', '.join(f'{t:.2f}' for t in times)} s; least-squares per-row "
+                f"{per_row:.3f} s and per-chunk {per_chunk:.3f} s (rms residual "
+                f"{resid:.3f} s), per-call INT8 step {per_call:.2f} s timed alone; "
+                f"extrapolated to BT={bt} in {plan.num_chunks} chunks ({est:.0f} s)")
+        return bt / est, text
+
     model, cores = cpu_info()
-    return {"value": bt / est, "unit": "rows/s", "cores": 1, "kind": "port",
-            "cpu": model, "host_cores": cores,
-            "sample": (f"oracle/liborda_oracle.so on one thread of a {cores}-core {model}: "
-                       f"one chunk of {', '.join(map(str, sample_rows))} rows of this workload "
-                       f"(same H, V, options; the reference's f32/f64 arithmetic), timed "
-                       f"{', '.join(f'{t:.2f}' for t in times)} s; least-squares per-row "
-                       f"{per_row:.3f} s and per-chunk {per_chunk:.3f} s (rms residual "
-                       f"{resid:.3f} s), per-call INT8 step {per_call:.2f} s timed alone; "
-                       f"extrapolated to BT={bt} in {plan.num_chunks} chunks ({est:.0f} s)")}
+    value, text = measure("one thread")
+    out = {"value": value, "unit": "rows/s", "cores": 1, "kind": "port",
+           "cpu": model, "host_cores": cores,
+           "sample": f"oracle/liborda_oracle.so on one thread of a {cores}-core {model}: {text}"}
+    try:
+        threads = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+    except ValueError:
+        threads = cores
+    if threads > 1:
+        O.set_threads(threads)
+        try:
+            value_n, text_n = measure(f"{threads} threads")
+        finally:
+            O.set_threads(1)
+        out["all_cores"] = {"value": value_n, "unit": "rows/s", "cores": threads,
+                            "sample": (f"the same oracle with its products, element-wise loops "
+                                       f"and INT8 rows shared out over {threads} threads "
+                                       f"(results bitwise the same): {text_n}")}
+    return out
 
 
 # ------------------------------------------------------------ profiles

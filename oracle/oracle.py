@@ -108,6 +108,8 @@ def lib():
                                                   _szp, C.c_size_t]
         L.ora_is_power_of_two.restype = C.c_int
         L.ora_is_power_of_two.argtypes = [C.c_size_t]
+        L.ora_set_threads.restype = None
+        L.ora_set_threads.argtypes = [C.c_int]
         for nm in ("ora_matmul_nt", "ora_matmul_nn", "ora_matmul_tn"):
             f = getattr(L, nm)
             f.restype = None
@@ -225,6 +227,13 @@ def is_power_of_two(v: int) -> bool:
 
 
 # ---------------------------------------------------------------- mat
+def set_threads(n: int) -> None:
+    """Threads for the three products (1, the default, is the reference's
+    single thread). Results are bitwise the same for any count: each output
+    element still accumulates its terms in the reference's order."""
+    lib().ora_set_threads(int(n))
+
+
 def matmul_nt(a, b):
     a, b = _f32(a), _f32(b)
     m, k = _shape2(a)

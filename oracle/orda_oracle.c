@@ -122,9 +122,21 @@ int ora_is_power_of_two(size_t v) { return v > 0 && (v & (v - 1)) == 0; }
  * mat.rs
  * ==================================================================== */
 
+/* Threads for the three products below and for the element-wise and
+ * row-wise loops over whole matrices (add/scale, deterministic INT8 rows);
+ * 1, the default, is the reference's single thread. With more, output rows or
+ * elements are shared out between threads; every output element still
+ * accumulates its terms in the reference's order, so the results are bitwise
+ * the same (the oracle's tests check this). Only the CPU baseline's all-core
+ * timing sets it. */
+static int g_threads = 1;
+
+void ora_set_threads(int n) { g_threads = n > 1 ? n : 1; }
+
 /* mat.rs:63-80 — out = a @ bᵀ, sequential f32 dot from 0. */
 void ora_matmul_nt(const float *a, const float *b, float *out, size_t m, size_t k,
                    size_t n) {
+#pragma omp parallel for if (g_threads > 1) num_threads(g_threads) schedule(static)
     for (size_t i = 0; i < m; i++) {
         const float *arow = a + i * k;
         float *orow = out + i * n;
@@ -141,6 +153,7 @@ void ora_matmul_nt(const float *a, const float *b, float *out, size_t m, size_t 
 void ora_matmul_nn(const float *a, const float *b, float *out, size_t m, size_t k,
                    size_t n) {
     memset(out, 0, m * n * sizeof(float));
+#pragma omp parallel for if (g_threads > 1) num_threads(g_threads) schedule(static)
     for (size_t i = 0; i < m; i++) {
         const float *arow = a + i * k;
         float *orow = out + i * n;
@@ -157,6 +170,20 @@ void ora_matmul_nn(const float *a, const float *b, float *out, size_t m, size_t 
 void ora_matmul_tn(const float *a, const float *b, float *out, size_t k, size_t m,
                    size_t n) {
     memset(out, 0, m * n * sizeof(float));
+    if (g_threads > 1) {
+        /* Output row i on one thread: its terms arrive in p order, as below. */
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+        for (size_t i = 0; i < m; i++) {
+            float *orow = out + i * n;
+            for (size_t p = 0; p < k; p++) {
+                float aip = a[p * m + i];
+                if (aip == 0.0f) continue;
+                const float *brow = b + p * n;
+                for (size_t j = 0; j < n; j++) orow[j] += aip * brow[j];
+            }
+        }
+        return;
+    }
     for (size_t p = 0; p < k; p++) {
         const float *arow = a + p * m;
         const float *brow = b + p * n;
@@ -171,11 +198,13 @@ void ora_matmul_tn(const float *a, const float *b, float *out, size_t k, size_t 
 
 /* mat.rs:133-138 */
 static void add_assign(float *dst, const float *src, size_t len) {
+#pragma omp parallel for if (g_threads > 1) num_threads(g_threads) schedule(static)
     for (size_t i = 0; i < len; i++) dst[i] += src[i];
 }
 
 /* mat.rs:141-145 */
 static void scale_assign(float *m, size_t len, float s) {
+#pragma omp parallel for if (g_threads > 1) num_threads(g_threads) schedule(static)
     for (size_t i = 0; i < len; i++) m[i] *= s;
 }
 
@@ -359,6 +388,7 @@ float ora_row_scale(const float *row, size_t cols) {
 /* quant.rs:96-117 */
 void ora_quantize_rowwise_int8(const float *m, size_t rows, size_t cols, int8_t *q,
                                float *scale) {
+#pragma omp parallel for if (g_threads > 1) num_threads(g_threads) schedule(static)
     for (size_t r = 0; r < rows; r++) {
         const float *row = m + r * cols;
         float s = ora_row_scale(row, cols);
@@ -420,6 +450,7 @@ void ora_quant_dequant_grad_w(const float *grad_w, size_t rows, size_t cols,
         ora_quantize_rowwise_int8(grad_w, rows, cols, q, scale);
     }
     /* QuantRows::dequantize (quant.rs:77-87) */
+#pragma omp parallel for if (g_threads > 1) num_threads(g_threads) schedule(static)
     for (size_t r = 0; r < rows; r++) {
         float s = scale[r];
         for (size_t c = 0; c < cols; c++) out[r * cols + c] = (float)q[r * cols + c] * s;

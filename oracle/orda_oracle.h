@@ -38,6 +38,7 @@ size_t ora_chunk_doubling_schedule(size_t bt, size_t start, size_t limit,
 int ora_is_power_of_two(size_t v);                             /* config.rs:123-125  */
 
 /* ---- mat.rs (row-major f32) ------------------------------------------- */
+void ora_set_threads(int n);   /* threads of the three products; default 1 */
 void ora_matmul_nt(const float *a, const float *b, float *out, size_t m,
                    size_t k, size_t n);                        /* mat.rs:63-80   */
 void ora_matmul_nn(const float *a, const float *b, float *out, size_t m,

@@ -297,3 +297,47 @@ def test_oracle_matches_textbook_f64(mode, alpha, kd, T, w_t, reduction):
     else:
         assert out.grad_teacher_weight is None
     assert (out.chunk_plan.chunk_size, out.chunk_plan.num_chunks) == (10, 4)
+
+
+@pytest.mark.parametrize("mode,quant", [("tied", False), ("tied", True), ("separate", False),
+                                        ("precomputed", True)])
+def test_threaded_products_are_bitwise_the_same(mode, quant):
+    """The all-core CPU baseline shares the products' output rows (and the
+    element-wise and INT8 row loops) between threads; every output element
+    keeps the reference's accumulation order, so a whole loss call must come
+    out bitwise identical."""
+    rng = np.random.default_rng(41)
+    bt, h, ht, v = 37, 29, 23, 211
+    s = rng.standard_normal((bt, h), dtype=np.float32)
+    W = (rng.standard_normal((v, h), dtype=np.float32) * 0.05).astype(np.float32)
+    y = rng.integers(0, v, bt)
+    y[::5] = -100
+    if mode == "tied":
+        t = Teacher.Tied(rng.standard_normal((bt, h), dtype=np.float32))
+    elif mode == "separate":
+        t = Teacher.Separate(rng.standard_normal((bt, ht), dtype=np.float32),
+                             (rng.standard_normal((v, ht), dtype=np.float32) * 0.05))
+    else:
+        t = Teacher.Precomputed(rng.standard_normal((bt, v), dtype=np.float32))
+    opts = LossOptions(kd_weight=0.5, temperature=1.5, label_smoothing=0.1,
+                       teacher_ce_weight=0.7 if mode != "precomputed" else None,
+                       chunk_size=ChunkSize.Fixed(10),
+                       config=KernelConfig(quantize_grad_weight=quant))
+    one = O.distillation_loss(s, W, y, t, opts)
+    try:
+        O.set_threads(4)
+        many = O.distillation_loss(s, W, y, t, opts)
+        a, b = rng.standard_normal((53, 41), dtype=np.float32), rng.standard_normal((53, 17),
+                                                                                    dtype=np.float32)
+        a[3, :] = 0.0
+        tn4 = O.matmul_tn(a, b)
+    finally:
+        O.set_threads(1)
+    assert np.array_equal(O.matmul_tn(a, b), tn4)
+    for k in ("loss", "student_ce", "teacher_ce", "kl"):
+        assert getattr(one, k) == getattr(many, k), k
+    for k in ("grad_student_hidden", "grad_weight", "grad_teacher_hidden", "grad_teacher_weight"):
+        x, z = getattr(one, k), getattr(many, k)
+        assert (x is None) == (z is None), k
+        if x is not None:
+            assert np.array_equal(x, z), k
