@@ -259,6 +259,7 @@ KERNEL_CLASSES = (
     ("row_pass_", "row_pass"),            # row_pass_fused_kernel, row_pass_kernel
     ("row_consts_", "row_consts"),        # the chunked row pass: per-row constants ...
     ("row_grad_", "row_grad"),            # ... and the elementwise gradient
+    ("row_kl_", "row_kl"),                # ... and, over fp32 logits, each row's KL
     ("row_stats_kernel", "row_stats"),
     ("finalize_kernel", "finalize"),
     ("quant_", "quant"),                  # quant_vec_kernel, quant_kernel

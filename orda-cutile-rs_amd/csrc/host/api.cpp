@@ -466,6 +466,9 @@ int64_t staged_bytes_per_row(const LossPlan& P, const Inputs& in) {
               (orda::dtype_size(lt) + (lt == P.dt ? 0 : orda::dtype_size(P.dt)));
   b += 2 * nst * 16 + 2 * 4;   // statistics, label logits
   if (paired) b += nst * 4 + 16;   // cross partials, row constants
+  // fp32 logits: row constants and the gradient blocks' KL sums
+  if (!paired && lt == orda::DType::F32)
+    b += 16 + (P.kd > 0.f ? orda::row_pass_kl_blocks(P.v) * 8 : 0);
   // hcat: the hidden rows transposed for grad_W ([h_s; h_t] with a Tied
   // teacher and teacher CE; else the student's, then the Separate teacher's).
   b += (P.mode == ORDA_TEACHER_TIED && P.w_t > 0.f ? 2 * P.h
@@ -524,7 +527,13 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   const int64_t ldh_cat = round8(tied_tce ? 2 * cap : cap);
   void* hcat = ws(c, "hcat", std::max(h, P.has_gwt ? P.ht : int64_t{0}) * ldh_cat * es);
   float* cross = paired ? static_cast<float*>(ws(c, "cross", cap * nst * 4)) : nullptr;
-  float4* rconst = paired ? static_cast<float4*>(ws(c, "rconst", cap * 16)) : nullptr;
+  // Row constants of the chunked row passes (paired bf16 logits, or fp32
+  // logits), and for fp32 logits with a KL term the per-block KL sums.
+  const bool f32_rows = !paired && lt == DType::F32;
+  float4* rconst = paired || f32_rows ? static_cast<float4*>(ws(c, "rconst", cap * 16)) : nullptr;
+  float2* klpart = f32_rows && P.kd > 0.f
+                       ? static_cast<float2*>(ws(c, "klpart", cap * row_pass_kl_blocks(v) * 8))
+                       : nullptr;
   const float inv_t = 1.0f / P.T;
 
   for (int64_t g0 = 0; g0 < nc; g0 += G) {
@@ -639,6 +648,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       r.xy_t = xy + btg;
       r.cross = cross;
       r.row_consts = rconst;
+      r.kl_part = klpart;
       r.labels = in.labels + gs;
       r.ignore_index = P.ignore;
       r.w_s = P.w_s;
@@ -936,6 +946,7 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
       ws_release(c, "dlogits");
       ws_release(c, "cross");
       ws_release(c, "rconst");
+      ws_release(c, "klpart");
       ws_release(c, "splitk");
       if (G > 1) {
         G /= 2;

@@ -128,9 +128,13 @@ struct RowPassArgs {
   // (LogitStatsArgs::cross, same pitch as the stats), or null: then the
   // pass accumulates the cross term from the logits it reads.
   const float* cross;
-  // Scratch of n_rows float4 for the chunked pass over paired bf16 logits
-  // (used when cross is set and the gradient goes in place); may be null.
+  // Scratch of n_rows float4 for the chunked passes: over paired bf16
+  // logits (cross set, gradient in place), and over fp32 logits (cross
+  // null); may be null (then the row-per-workgroup pass runs).
   float4* row_consts;
+  // fp32 chunked pass with a KL term: n_rows * row_pass_kl_blocks(v)
+  // float2, each column block's share of the row's KL sums.
+  float2* kl_part;
   // Gradient rows: written at grad_s/grad_t + r*ld in gtype. Null grad_s
   // means in place (gtype == ltype).
   void* grad_s;
@@ -150,6 +154,8 @@ struct RowPassArgs {
 };
 
 hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t stream);
+// float2 entries per row of RowPassArgs::kl_part (ceil(v/512)).
+int64_t row_pass_kl_blocks(int64_t v);
 
 // Per-row statistics of rows that were not produced by the GEMM (Precomputed
 // teacher logits, the chunk-launcher entry point). Reads src (fp32 or bf16,

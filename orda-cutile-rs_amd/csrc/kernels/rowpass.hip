@@ -1,20 +1,26 @@
-// rowpass.hip — the fused row pass of the distillation loss on gfx950.
+// rowpass.hip — the row pass of the distillation loss on gfx950.
 //
-// One workgroup owns one (student row, teacher row) pair of a logits chunk
-// (layout of src/api.rs:276-299: student rows, then teacher rows). From the
-// per-tile softmax statistics written by the logits GEMM it forms, per row,
-// lse at T=1 and at temperature T, then streams the two rows once:
+// For each (student row, teacher row) pair of a logits chunk (layout of
+// src/api.rs:276-299: student rows, then teacher rows) it forms, from the
+// per-tile softmax statistics written by the logits GEMM, lse at T=1 and at
+// temperature T, then streams the two rows once:
 //   student grad = w_s·((p_s − α/V) − [j=y](1−α)) + kd·T·(p_s^T − p_t^T)
 //                                          (cross_entropy.rs:58-71, kl.rs:83-124,
 //                                           merge api.rs:335-344)
 //   teacher grad = w_t·((p_t − α/V) − [j=y](1−α))   (api.rs:325-333)
-// overwriting both rows in place, and accumulates Σ p_t^T·(x_t − x_s) so that
-//   KL_row = Σ p_t^T (x_t − x_s)/T + (lse_s^T − lse_t^T)·Σ p_t^T
-// comes out of the same pass — unless a paired logits GEMM already formed
-// that sum per tile from its fp32 accumulators (the logits are then stored
-// in bf16 and only feed the gradient). The per-row NLL uses the fp32 label logit and
-// Σx from the GEMM epilogue and is formed in f64 like the reference.
-// Exponentials are exp2 with log2(e) folded into one FMA per element.
+// overwriting both rows in place, and the KL term
+//   KL_row = Σ p_t^T (x_t − x_s)/T + (lse_s^T − lse_t^T)·Σ p_t^T.
+// Three forms:
+//   * paired bf16 logits: the KL cross sum comes per tile from the logits
+//     GEMM's fp32 accumulators (the stored logits only feed the gradient);
+//     a per-row kernel merges the statistics, an elementwise kernel over
+//     (row, column block) writes the gradient;
+//   * large fp32 chunks: the same two kernels, the elementwise one also
+//     summing each block's share of the KL cross sum, then a per-row sum;
+//   * otherwise one workgroup per row pair, fused.
+// The per-row NLL uses the fp32 label logit and Σx from the GEMM epilogue and
+// is formed in f64 like the reference. Exponentials are exp2 with log2(e)
+// folded into one FMA per element.
 #include <math.h>
 
 #include "orda_kernels.h"
@@ -597,7 +603,10 @@ __global__ __launch_bounds__(kThreads) void row_consts_kernel(RowPassArgs a) {
   const float4* rs = a.stats_s + r * a.stats_ld;
   const bool teacher = KL || TG || a.teacher_ce;
   const float4* rt = a.stats_t + r * a.stats_ld;
-  const float* rc = KL ? a.cross + r * a.stats_ld : nullptr;
+  // Without a paired GEMM's cross partials (fp32 logits), the KL cross sums
+  // come from row_grad_f32_kernel's blocks instead.
+  const bool xk = KL && a.cross != nullptr;
+  const float* rc = xk ? a.cross + r * a.stats_ld : nullptr;
   const int64_t nt = a.stats_tiles > a.stats_tiles_t ? a.stats_tiles : a.stats_tiles_t;
   // kPer entries per lane in flight before any merge; a missing entry is
   // {-inf, 0, 0, 0}, which merges as nothing.
@@ -612,7 +621,7 @@ __global__ __launch_bounds__(kThreads) void row_consts_kernel(RowPassArgs a) {
       vs[i] = t < a.stats_tiles ? rs[t] : none;
       const bool tok = teacher && t < a.stats_tiles_t;
       vt[i] = tok ? rt[t] : none;
-      vc[i] = KL && tok ? rc[t] : 0.f;
+      vc[i] = xk && tok ? rc[t] : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
@@ -639,7 +648,11 @@ __global__ __launch_bounds__(kThreads) void row_consts_kernel(RowPassArgs a) {
     k.w = TG ? rlog2(a.w_t, fm) - lse1_t * kLog2e : 0.f;
     a.row_consts[r] = k;
     a.row_nll_s[r] = static_cast<float>(row_nll(ss, a.xy_s[r], alpha, a.v));
-    a.row_kl[r] = KL ? (rdiv(xc, st.dT, fm) * inv_t + lse_t_diff(ss, st, inv_t, fm)) * (T * T) : 0.f;
+    // Without cross partials, row_kl holds lse_s^T - lse_t^T until
+    // row_kl_kernel forms the row's KL from the gradient blocks' sums.
+    a.row_kl[r] = !KL ? 0.f
+                  : xk ? (rdiv(xc, st.dT, fm) * inv_t + lse_t_diff(ss, st, inv_t, fm)) * (T * T)
+                       : lse_t_diff(ss, st, inv_t, fm);
     a.row_nll_t[r] = a.teacher_ce ? static_cast<float>(row_nll(st, a.xy_t[r], alpha, a.v)) : 0.f;
   }
 }
@@ -731,6 +744,172 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
     elem(xs_y, xt_y, gy, ty);
     srow[y] = static_cast<__bf16>(gy - a.w_s * one_m_a);
     if (TG) trow[y] = static_cast<__bf16>(ty - a.w_t * one_m_a);
+  }
+}
+
+// The same chunked pass over fp32 logits (fp32 inputs; bf16 inputs whose
+// KL term needs fp32 logits), where the KL cross term is not available from
+// the GEMM: each (row, kF32Chunk-column) block also writes its share of the
+// two KL sums of row_pass_fused_kernel,
+//   kl_part[r * chunks + c] = {Σ kd·T·p_t^T·(x_t − x_s), Σ kd·T·p_t^T},
+// and row_kl_kernel adds a row's shares. Gradients go in place (GT float)
+// or to the separate gradient rows grad_s/grad_t; the teacher rows may have
+// their own pitch (Precomputed logits read in place). Ordinary loads and
+// stores: with the non-temporal hints of row_grad_kernel this pass measured
+// 10-20 % slower at V = 32000 and 65536 (the bf16 pass is 13 % faster with
+// them). One wave per block, one vector per thread: measured at the fp32
+// workloads (BT x V = 2048 x 32000, 4096 x 32000, 4096 x 65536) against
+// 128 and 256 threads (within 1.5 %) and 2 or 4 vectors per thread (1-5 %
+// slower).
+constexpr int kF32Threads = 64;
+constexpr int kF32Vec = 1;                                 // 8-element vectors per thread
+constexpr int kF32Chunk = kF32Threads * 8 * kF32Vec;       // columns per workgroup
+template <typename GT, bool KL, bool TG>
+__global__ __launch_bounds__(kF32Threads) void row_grad_f32_kernel(RowPassArgs a, int64_t chunks) {
+  constexpr int NV = 8;
+  __shared__ float sred[2][kF32Threads / 64];
+  const int64_t r = blockIdx.x / chunks;
+  const int64_t ci = blockIdx.x - r * chunks;
+  const int64_t c0 = ci * kF32Chunk;
+  const int tid = threadIdx.x;
+  const int64_t y = a.labels[r];
+  const int64_t v = a.v;
+  const float* srow = static_cast<const float*>(a.student) + r * a.ld;
+  const float* trow =
+      (KL || TG) ? static_cast<const float*>(a.teacher) + r * (a.ld_t ? a.ld_t : a.ld) : nullptr;
+  GT* gsrow = static_cast<GT*>(a.grad_s ? a.grad_s : a.student) + r * a.ld;
+  GT* gtrow = TG ? static_cast<GT*>(a.grad_s ? a.grad_t : a.teacher) + r * a.ld : nullptr;
+  auto col = [&](int q) { return c0 + (static_cast<int64_t>(q) * kF32Threads + tid) * NV; };
+  if (y == a.ignore_index || y < 0 || y >= v) {   // zero gradient rows, no KL
+    const float z[NV] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < kF32Vec; ++q) {
+      const int64_t j = col(q);
+      if (j < v) {
+        store8(gsrow + j, z);
+        if (TG) store8(gtrow + j, z);
+      }
+    }
+    if (KL && tid == 0) a.kl_part[r * chunks + ci] = make_float2(0.f, 0.f);
+    return;
+  }
+  const float4 k = a.row_consts[r];
+  const float it2 = kLog2e * rdiv(1.0f, a.temperature, a.fast_math);
+  const float eps = static_cast<float>(static_cast<double>(a.label_smoothing) / static_cast<double>(v));
+  const float one_m_a = 1.0f - a.label_smoothing;
+  const float sgn = a.w_s < 0.f ? -1.f : 1.f;
+  const float k0 = -a.w_s * eps, kt0 = -a.w_t * eps;
+  // Gradient of one element pair without the label term; c = kd·T·p_t^T.
+  auto elem = [&](float xs, float xt, float& g, float& gt, float& c) {
+    g = fmaf(sgn, __builtin_amdgcn_exp2f(fmaf(xs, kLog2e, k.x)), k0);
+    if (KL) {
+      c = __builtin_amdgcn_exp2f(fmaf(xt, it2, k.z));
+      g += __builtin_amdgcn_exp2f(fmaf(xs, it2, k.y)) - c;
+    }
+    if (TG) gt = __builtin_amdgcn_exp2f(fmaf(xt, kLog2e, k.w)) + kt0;
+  };
+  // The label column's logits, read by the thread that writes that column.
+  const int64_t yl = y - c0;
+  const bool owner = yl >= 0 && yl < kF32Chunk && tid == (yl / NV) % kF32Threads;
+  float xs_y = 0.f, xt_y = 0.f;
+  if (owner) {
+    xs_y = srow[y];
+    if (KL || TG) xt_y = trow[y];
+  }
+  u32x4 rs[kF32Vec][2], rt[kF32Vec][2];
+#pragma unroll
+  for (int q = 0; q < kF32Vec; ++q) {
+    const int64_t j = col(q);
+    if (j < v) {
+      rs[q][0] = reinterpret_cast<const u32x4*>(srow + j)[0];
+      rs[q][1] = reinterpret_cast<const u32x4*>(srow + j)[1];
+      if (KL || TG) {
+        rt[q][0] = reinterpret_cast<const u32x4*>(trow + j)[0];
+        rt[q][1] = reinterpret_cast<const u32x4*>(trow + j)[1];
+      }
+    }
+  }
+  float cross = 0.f, sum_c = 0.f;
+#pragma unroll
+  for (int q = 0; q < kF32Vec; ++q) {
+    const int64_t j = col(q);
+    if (j >= v) continue;
+    float g[NV], gt[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const float xs = __uint_as_float(rs[q][i >> 2][i & 3]);
+      const float xt = (KL || TG) ? __uint_as_float(rt[q][i >> 2][i & 3]) : 0.f;
+      float gi = 0.f, ti = 0.f, c = 0.f;
+      elem(xs, xt, gi, ti, c);
+      const bool valid = j + i < v;
+      if (KL) {
+        cross += valid ? c * (xt - xs) : 0.f;
+        sum_c += valid ? c : 0.f;
+      }
+      g[i] = valid ? gi : 0.f;
+      gt[i] = valid ? ti : 0.f;
+    }
+    store8(gsrow + j, g);
+    if (TG) store8(gtrow + j, gt);
+  }
+  if (owner) {   // the label term, after this thread's own store of that column
+    float gy = 0.f, ty = 0.f, c = 0.f;
+    elem(xs_y, xt_y, gy, ty, c);
+    gsrow[y] = static_cast<GT>(gy - a.w_s * one_m_a);
+    if (TG) gtrow[y] = static_cast<GT>(ty - a.w_t * one_m_a);
+  }
+  if (KL) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      cross += __shfl_xor(cross, o);
+      sum_c += __shfl_xor(sum_c, o);
+    }
+    if ((tid & 63) == 0) {
+      sred[0][tid >> 6] = cross;
+      sred[1][tid >> 6] = sum_c;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      float x = 0.f, sm = 0.f;
+#pragma unroll
+      for (int w = 0; w < kF32Threads / 64; ++w) {
+        x += sred[0][w];
+        sm += sred[1][w];
+      }
+      a.kl_part[r * chunks + ci] = make_float2(x, sm);
+    }
+  }
+}
+
+// KL_row·T² of every non-ignored row from its gradient blocks' sums and
+// lse_s^T - lse_t^T (left in row_kl by row_consts_kernel), as in
+// row_pass_fused_kernel:
+//   KL_row = Σ p_t^T (x_t − x_s)/T + (lse_s^T − lse_t^T)·Σ p_t^T.
+// One wave per row: lanes take every 64th block, then a butterfly.
+__global__ __launch_bounds__(kThreads) void row_kl_kernel(RowPassArgs a, int64_t chunks) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+  if (r >= a.n_rows) return;
+  const int64_t y = a.labels[r];
+  if (y == a.ignore_index || y < 0 || y >= a.v) return;   // row_kl is already 0
+  const float2* p = a.kl_part + r * chunks;
+  float x = 0.f, s = 0.f;
+  for (int64_t c = lane; c < chunks; c += 64) {
+    const float2 q = p[c];
+    x += q.x;
+    s += q.y;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    x += __shfl_xor(x, o);
+    s += __shfl_xor(s, o);
+  }
+  if (lane == 0) {
+    const bool fm = a.fast_math;
+    const float T = a.temperature;
+    const float inv_t = rdiv(1.0f, T, fm);
+    const float gsc = a.kd * T;   // kl.rs:85
+    a.row_kl[r] = (rdiv(x, gsc, fm) * inv_t + a.row_kl[r] * rdiv(s, gsc, fm)) * (T * T);
   }
 }
 
@@ -945,6 +1124,42 @@ hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
     }
     return hipGetLastError();
   }
+  // The chunked fp32 pass costs two more launches (~12 us) and streams ~8 %
+  // faster: the row-per-workgroup kernel serves small chunks (measured 16.5
+  // against 27 us at 256 rows x V = 8192).
+  const bool big = a.n_rows * a.v >= (int64_t{1} << 25);
+  if (big && a.ltype == DType::F32 && a.cross == nullptr && a.row_consts != nullptr &&
+      (a.kl_part != nullptr || !kl) && (!(kl || tg || a.teacher_ce) || has_t)) {
+    // fp32 logits: per-row constants, the chunked elementwise gradient with
+    // per-block KL sums, then each row's KL from those sums.
+    const int64_t chunks = row_pass_kl_blocks(a.v);
+    const int64_t blocks = a.n_rows * chunks;
+    const dim3 cgrid(static_cast<unsigned>((a.n_rows + kThreads / 64 - 1) / (kThreads / 64)));
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 bgrid(static_cast<unsigned>(blocks));
+#define ORDA_ROWGRAD_F32(GT)                                                                          \
+  if (kl && tg) {                                                                                     \
+    hipLaunchKernelGGL((row_consts_kernel<true, true>), cgrid, dim3(kThreads), 0, s, a);              \
+    hipLaunchKernelGGL((row_grad_f32_kernel<GT, true, true>), bgrid, dim3(kF32Threads), 0, s, a, chunks); \
+  } else if (kl) {                                                                                    \
+    hipLaunchKernelGGL((row_consts_kernel<true, false>), cgrid, dim3(kThreads), 0, s, a);             \
+    hipLaunchKernelGGL((row_grad_f32_kernel<GT, true, false>), bgrid, dim3(kF32Threads), 0, s, a, chunks); \
+  } else if (tg) {                                                                                    \
+    hipLaunchKernelGGL((row_consts_kernel<false, true>), cgrid, dim3(kThreads), 0, s, a);             \
+    hipLaunchKernelGGL((row_grad_f32_kernel<GT, false, true>), bgrid, dim3(kF32Threads), 0, s, a, chunks); \
+  } else {                                                                                            \
+    hipLaunchKernelGGL((row_consts_kernel<false, false>), cgrid, dim3(kThreads), 0, s, a);            \
+    hipLaunchKernelGGL((row_grad_f32_kernel<GT, false, false>), bgrid, dim3(kF32Threads), 0, s, a, chunks); \
+  }
+    if (gt == DType::F32) {
+      ORDA_ROWGRAD_F32(float)
+    } else {
+      ORDA_ROWGRAD_F32(__bf16)
+    }
+#undef ORDA_ROWGRAD_F32
+    if (kl) hipLaunchKernelGGL(row_kl_kernel, cgrid, dim3(kThreads), 0, s, a, chunks);
+    return hipGetLastError();
+  }
 #define ORDA_ROWPASS(LT, GT)                                                                          \
   if (kl && tg) hipLaunchKernelGGL((row_pass_fused_kernel<LT, GT, true, true>), grid, dim3(kThreads), 0, s, a);   \
   else if (kl) hipLaunchKernelGGL((row_pass_fused_kernel<LT, GT, true, false>), grid, dim3(kThreads), 0, s, a);  \
@@ -964,6 +1179,8 @@ hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
 }
 
 int64_t row_stats_segments(int64_t v) { return (v + kSegCols - 1) / kSegCols; }
+
+int64_t row_pass_kl_blocks(int64_t v) { return (v + kF32Chunk - 1) / kF32Chunk; }
 
 hipError_t launch_row_stats(const RowStatsArgs& a, hipStream_t s) {
   if (a.n_rows <= 0) return hipSuccess;
