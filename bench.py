@@ -249,6 +249,65 @@ def cpu_baseline(wl, sample_rows=(2, 4, 6)):
     return out
 
 
+def vendor_gemms(torch, wl, dev, s, w, t, reps):
+    """The loss's three products on the same inputs' shapes, timed with the
+    vendor library (hipBLASLt through torch: F.linear / torch.mm in the compute
+    dtype, fp32 accumulation, output in the compute dtype, no fused epilogue),
+    on this GPU in this run: a reference for what a tuned library reaches on
+    these shapes here. Operands: the workload's hidden rows and weights, and a
+    random gradient-like matrix (N(0, 1e-5^2)) in place of the row pass's
+    output. Products as the library runs them: logits = hidden · Wᵀ,
+    grad_hidden = dlogits · W, grad_W computed transposed = hiddenᵀ · dlogits.
+    Separate teachers are not covered (two weights)."""
+    import torch.nn.functional as F
+    teacher, bt, h, ht, v, _, kd, T, alpha, w_t, quant = wl[:11]
+    if teacher == "separate":
+        return None
+    dt = compute_dtype(wl)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    hid = s.to(tdt)
+    if teacher == "tied" and (w_t is None or w_t > 0 or kd > 0):
+        hid = torch.cat([hid, t[1].to(tdt)], 0)
+    wt = w.to(tdt)
+    rows = hid.shape[0]
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    dl = torch.empty((rows, v), device=dev, dtype=torch.float32)
+    dl.normal_(0.0, 1e-5, generator=g)
+    dl = dl.to(tdt)
+    hid_t = hid.t().contiguous()
+    products = {
+        "gemm_logits": lambda: F.linear(hid, wt),
+        "gemm_grad_hidden": lambda: torch.mm(dl, wt),
+        "gemm_grad_weight": lambda: torch.mm(hid_t, dl),
+    }
+    flops = 2.0 * rows * h * v
+    out = {"library": "hipBLASLt via torch (F.linear / torch.mm), "
+                      f"{dt} in and out, fp32 accumulation, no fused epilogue",
+           "peak_tflops": PEAK_MFMA_TFLOPS[dt]}
+    for kind, fn in products.items():
+        r = fn()
+        torch.cuda.synchronize()
+        del r
+        times = []
+        for _ in range(max(3, min(reps, 5))):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            r = fn()
+            e1.record()
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1))
+            del r
+        ms = sorted(times)[len(times) // 2]
+        tf = flops / (ms * 1e-3) / 1e12
+        out[kind] = {"ms": round(ms, 4), "achieved": round(tf, 2),
+                     "frac": round(tf / PEAK_MFMA_TFLOPS[dt], 4)}
+        log(f"vendor {kind}: {ms:.3f} ms ({tf:.1f} TFLOP/s)")
+    del dl, hid, hid_t, wt
+    return out
+
+
 # ------------------------------------------------------------ profiles
 KERNEL_CLASSES = (
     # (substring of the kernel name, kernel kind)
@@ -404,6 +463,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-vendor", action="store_true",
+                    help="skip timing the same products with hipBLASLt (torch.mm)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="before the timed steps, run one device-to-device copy of BYTES "
                          "(reference kernel for HBM counter calibration)")
@@ -508,8 +569,13 @@ def main():
         "row_pass_gbs": kernels.get("row_pass", {}).get("achieved"),
         "other_ms_per_step": round(ms_other / args.steps, 4),
     }
-    del s, w, y, t, teacher, out, outputs
+    del out, outputs
     ctx.close()
+    torch.cuda.empty_cache()
+    if not args.no_vendor:
+        log("timing the same products with the vendor library")
+        line["vendor_gemm"] = vendor_gemms(torch, wl, dev, s, w, t, args.steps)
+    del s, w, y, t, teacher
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         log("timing the CPU oracle on a bounded sample")
