@@ -12,7 +12,8 @@ cores; results bitwise the same as one thread):
   teacher weight), Precomputed logits read in place, also at a pitch wider
   than V;
 * bf16 inputs whose KL term needs fp32 logits (Separate, Precomputed): the
-  gradient rows then go to a separate bf16 buffer.
+  gradient rows then go to a separate bf16 buffer;
+* two staging groups in one call, which reuse the per-block KL buffer.
 Tolerances as in tests/parity.py (loss terms 1e-4 relative; gradients 1e-3
 for fp32 inputs, 2e-2 for bf16 inputs with the oracle fed the rounded values).
 """
@@ -112,3 +113,29 @@ def test_f32_row_pass_against_oracle(torch_dev, name):
     got = H.distillation_loss(dev_t(s), dev_t(w), torch.from_numpy(y).to(dev), t_gpu, opts)
     ref = O.distillation_loss(s, w, y, t_ref, opts)
     check_output(got, ref, kind="bf16" if dtype == "bf16" else "f32")
+
+
+@pytest.mark.parametrize("teacher_ce", [True, False])
+def test_f32_row_pass_two_staging_groups(torch_dev, teacher_ce):
+    """Two staging groups of 256 rows (256 x 131072 logits per block, the
+    chunked fp32 pass in each): the per-block KL shares are reused from one
+    group to the next, and every row's KL, NLLs and gradients must still
+    match the oracle's, with the reference's per-chunk KL rounding."""
+    torch, dev = torch_dev
+    bt, h, v = 512, 16, 131072
+    s, th = normal((bt, h), 11), normal((bt, h), 12)
+    w = normal((v, h), 13, 0.2)
+    y = edge_labels(bt, v, 14, ignore_every=5)
+    opts = LossOptions(kd_weight=0.6, temperature=1.5, label_smoothing=0.1,
+                       teacher_ce_weight=0.5 if teacher_ce else 0.0,
+                       chunk_size=H.ChunkSize.Fixed(256))
+    ctx = H.Context(0)
+    ctx.set_staging_budget(1)   # one chunk per group
+    ctx.set_timing(True)
+    dt = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    got = H.distillation_loss(dt(s), dt(w), dt(y), Teacher.Tied(dt(th)), opts, ctx=ctx)
+    _, n = ctx.kernel_time("gemm_logits")
+    assert n == 2, f"expected two logits launches (two groups), got {n}"
+    ref = O.distillation_loss(s, w, y, Teacher.Tied(th), opts)
+    check_output(got, ref)
+    ctx.close()
