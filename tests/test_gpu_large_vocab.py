@@ -1,0 +1,75 @@
+"""GPU parity at ragged large vocabularies, against the oracle.
+
+The chunked row passes (paired bf16 logits: 1024-column blocks; fp32 logits
+above 2^25 logits per block: 512-column blocks) and the logits GEMM's last,
+partial 256-column tile meet a vocabulary that is a multiple of none of them
+(nor of 8, so the logits pitch is padded), with labels in the last columns
+and ignored rows. Small hidden widths keep the oracle's products cheap (run on
+the host's cores; results bitwise the same as one thread). Tolerances as in
+tests/parity.py.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import bf16_round, normal, uniform_labels
+from parity import check_output
+
+import orda_hip as H
+from orda_hip import LossOptions, Teacher
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a visible GPU"
+    assert H.is_available(), "liborda_hip.so does not see a gfx950 device"
+    O.set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    yield torch, torch.device("cuda:0")
+    O.set_threads(1)
+
+
+CASES = {
+    # name: (mode, dtype, bt, h, ht, v, options)
+    "tied-bf16-paired": ("tied", "bf16", 301, 40, 40, 100003,
+                         dict(kd_weight=0.4, temperature=1.5, label_smoothing=0.1)),
+    "tied-bf16-paired-kd-only": ("tied", "bf16", 257, 24, 24, 70001,
+                                 dict(kd_weight=1.0, temperature=3.0, teacher_ce_weight=0.0)),
+    "tied-f32": ("tied", "f32", 333, 24, 24, 101011,
+                 dict(kd_weight=0.5, temperature=0.5, label_smoothing=0.1)),
+    "separate-bf16": ("separate", "bf16", 290, 24, 56, 116001,
+                      dict(kd_weight=0.5, temperature=2.0, teacher_ce_weight=0.3)),
+}
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_ragged_large_vocab(torch_dev, name):
+    torch, dev = torch_dev
+    mode, dtype, bt, h, ht, v, kw = CASES[name]
+    s = normal((bt, h), 21)
+    w = normal((v, h), 22, 0.2)
+    y = uniform_labels(bt, v, 23)
+    y[1::9] = v - 1 - (np.arange(len(y[1::9])) % 7)     # the last columns
+    y[::6] = -100
+    th = normal((bt, ht), 24)
+    tw = normal((v, ht), 25, 0.15) if mode == "separate" else None
+    if dtype == "bf16":
+        s, w, th = bf16_round(s), bf16_round(w), bf16_round(th)
+        tw = None if tw is None else bf16_round(tw)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+
+    def dev_t(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(tdt)
+
+    if mode == "tied":
+        t_ref, t_gpu = Teacher.Tied(th), Teacher.Tied(dev_t(th))
+    else:
+        t_ref, t_gpu = Teacher.Separate(th, tw), Teacher.Separate(dev_t(th), dev_t(tw))
+    opts = LossOptions(**kw)
+    got = H.distillation_loss(dev_t(s), dev_t(w), torch.from_numpy(y).to(dev), t_gpu, opts)
+    ref = O.distillation_loss(s, w, y, t_ref, opts)
+    check_output(got, ref, kind="bf16" if dtype == "bf16" else "f32")
