@@ -150,15 +150,31 @@ def work_per_step(wl, plan):
 
 
 def cpu_info():
-    """(model name, usable cores) of the host."""
-    model = "unknown"
+    """(model description, usable cores) of the host: the model name with the
+    CPU family / model / stepping, clock and whether it runs under a
+    hypervisor, as /proc/cpuinfo states them for the first processor."""
+    fields = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
+            if not line.strip():
                 break
+            k, _, val = line.partition(":")
+            fields[k.strip()] = val.strip()
     except OSError:
         pass
+    model = fields.get("model name", "unknown")
+    extra = []
+    if "cpu family" in fields:
+        fam = fields["cpu family"]
+        famx = f" (0x{int(fam):X})" if fam.isdigit() else ""
+        extra.append(f"family {fam}{famx} model {fields.get('model', '?')} "
+                     f"stepping {fields.get('stepping', '?')}")
+    if "cpu MHz" in fields:
+        extra.append(f"{float(fields['cpu MHz']):.0f} MHz")
+    if "hypervisor" in fields.get("flags", "").split():
+        extra.append("virtual machine")
+    if extra:
+        model = f"{model} ({', '.join(extra)})"
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
