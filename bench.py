@@ -332,6 +332,7 @@ KERNEL_CLASSES = (
     ("gemm_kk_logits_", "gemm_logits"),
     ("gemm_km_", "gemm_grad_hidden"),
     ("gemm_kmt_", "gemm_grad_weight"),
+    ("splitk_reduce", "splitk_reduce"),   # split-K: ordered sum of the partials
     ("transpose_rows", "transpose_rows"),   # grad_W's A operand: hidden rows transposed
     ("row_pass_", "row_pass"),            # row_pass_fused_kernel, row_pass_kernel
     ("row_consts_", "row_consts"),        # the chunked row pass: per-row constants ...

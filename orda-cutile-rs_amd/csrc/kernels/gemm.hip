@@ -1395,23 +1395,39 @@ GemmKernel select_kernel(const GemmArgs& g) {
 }
 
 // Split-K reduction: C = alpha * (Σ_s partial_s) (+ alpha * C when
-// accumulating), the partials summed in split order.
-__global__ void splitk_reduce_kernel(const float* ws, int64_t stride, int splits, int64_t M,
-                                     int64_t N, int64_t ldp, float* c0, float* c1, int64_t ldc,
-                                     float alpha0, const float* alpha_ptr, bool accum, bool trans) {
+// accumulating), the partials summed in split order. The partials are laid
+// out like C (rows x cols, row pitch ldp, a multiple of 4; transposed
+// products store them transposed), so each thread sums 4 consecutive
+// columns of one row with 16-byte loads, and stores them with one 16-byte
+// store where C's pitch and base allow. The split loop is unrolled so that
+// its loads are in flight together; the additions stay in split order.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(
+    const float* ws, int64_t stride, int splits, int64_t rows, int64_t cols, int64_t ldp,
+    float* c0, float* c1, int64_t ldc, float alpha0, const float* alpha_ptr, bool accum) {
   const float alpha = alpha_ptr != nullptr ? alpha0 * *alpha_ptr : alpha0;
-  const int64_t per = M * N;
+  const int64_t quads = (cols + 3) / 4;
+  const int64_t per = rows * quads;
   const int64_t total = per * (c1 ? 2 : 1);
+  const bool vec = (ldc % 4) == 0 && (reinterpret_cast<uintptr_t>(c0) % 16) == 0 &&
+                   (c1 == nullptr || (reinterpret_cast<uintptr_t>(c1) % 16) == 0);
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int p = i >= per ? 1 : 0;
     const int64_t e = i - p * per;
-    const int64_t m = e / N, n = e - m * N;
-    const float* src = ws + p * M * ldp + m * ldp + n;
-    float v = 0.f;
-    for (int s = 0; s < splits; ++s) v += src[s * stride];
-    float* dst = (p ? c1 : c0) + (trans ? n * ldc + m : m * ldc + n);
-    *dst = accum ? alpha * (*dst + v) : alpha * v;
+    const int64_t r = e / quads;
+    const int64_t q = (e - r * quads) * 4;
+    const f32x4* src = reinterpret_cast<const f32x4*>(ws + p * rows * ldp + r * ldp + q);
+    const int64_t sq = stride / 4;
+    f32x4 v = src[0];
+#pragma unroll 8
+    for (int s = 1; s < splits; ++s) v += src[s * sq];
+    float* dst = (p ? c1 : c0) + r * ldc + q;
+    if (vec && q + 4 <= cols) {
+      f32x4* d4 = reinterpret_cast<f32x4*>(dst);
+      *d4 = accum ? alpha * (*d4 + v) : alpha * v;
+    } else {
+      for (int k = 0; k < 4 && q + k < cols; ++k) dst[k] = accum ? alpha * (dst[k] + v[k]) : alpha * v[k];
+    }
   }
 }
 
@@ -1484,18 +1500,21 @@ struct SplitPlan {
 };
 
 // Split K when the tiles cannot fill the CUs: about 256 workgroups in all,
-// each split at least 512 elements of K (a multiple of 64), at most 64
-// splits and 256 MB of partials.
+// each split at least 128 elements of K (a multiple of 64), at most 64
+// splits and 256 MB of partials. (At BT=256, H=512, V=8192 fp32 a 512
+// minimum left grad_hidden on 64 workgroups and grad_W unsplit: 0.152 and
+// 0.141 ms against 0.072 and 0.070 ms with 128, reductions included; 64
+// measured the same as 128.)
 SplitPlan plan_split(const GemmArgs& g) {
   SplitPlan sp{1, g.K, 0, 0, 0};
   if (g.epi == GemmEpilogue::Logits || g.M <= 0 || g.N <= 0 || g.K <= 0) return sp;
   const int64_t tiles = ((g.M + kTile - 1) / kTile) * ((g.N + kTile - 1) / kTile) * g.nprob;
   if (tiles >= 192) return sp;
   int64_t s = (256 + tiles - 1) / tiles;
-  const int64_t by_k = g.K / 512;
+  const int64_t by_k = g.K / 128;
   if (s > by_k) s = by_k;
   if (s > 64) s = 64;
-  const int64_t per_split = g.nprob * g.M * ((g.N + 3) / 4 * 4) * 4;
+  const int64_t per_split = g.nprob * (g.c_trans ? g.N * ((g.M + 3) / 4 * 4) : g.M * ((g.N + 3) / 4 * 4)) * 4;
   if (s > (int64_t{256} << 20) / per_split) s = (int64_t{256} << 20) / per_split;
   if (s <= 1) return sp;
   const int64_t len = ((g.K + s - 1) / s + 63) / 64 * 64;
@@ -1503,8 +1522,9 @@ SplitPlan plan_split(const GemmArgs& g) {
   if (s <= 1) return sp;
   sp.splits = static_cast<int>(s);
   sp.len = len;
-  sp.ldp = (g.N + 3) / 4 * 4;
-  sp.stride = g.nprob * g.M * sp.ldp;
+  // partials in C's orientation: rows x ldp, transposed when C is
+  sp.ldp = ((g.c_trans ? g.M : g.N) + 3) / 4 * 4;
+  sp.stride = g.nprob * (g.c_trans ? g.N : g.M) * sp.ldp;
   sp.bytes = s * sp.stride * 4;
   return sp;
 }
@@ -1564,28 +1584,28 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
   const int64_t tiles = ((g.M + kTile - 1) / kTile) * ((g.N + kTile - 1) / kTile) * g.nprob;
   const SplitPlan sp = plan_split(g);
   if (sp.splits > 1 && g.split_ws != nullptr && g.split_ws_bytes >= sp.bytes) {
-    // Partials of every split with the Store epilogue (alpha 1), then one
-    // reduction applying the requested epilogue.
+    // Partials of every split with the Store epilogue (alpha 1), in C's
+    // orientation, then one reduction applying the requested epilogue.
     GemmArgs s = g;
     s.epi = GemmEpilogue::StoreF32;
     s.alpha = 1.f;
     s.alpha_ptr = nullptr;
-    s.c_trans = false;
     s.ldc = sp.ldp;
     s.split_k = sp.splits;
     s.split_len = sp.len;
     s.split_stride = sp.stride;
-    for (int p = 0; p < g.nprob; ++p) s.prob[p].c = g.split_ws + p * g.M * sp.ldp;
+    const int64_t rows = g.c_trans ? g.N : g.M, cols = g.c_trans ? g.M : g.N;
+    for (int p = 0; p < g.nprob; ++p) s.prob[p].c = g.split_ws + p * rows * sp.ldp;
     const GemmKernel k = select_kernel(s);
     if (k == nullptr) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(tiles * sp.splits)), dim3(kThreads), 0,
                        stream, s);
-    const int64_t total = g.M * g.N * g.nprob;
+    const int64_t total = rows * ((cols + 3) / 4) * g.nprob;
     const unsigned blocks = static_cast<unsigned>((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, g.split_ws,
-                       sp.stride, sp.splits, g.M, g.N, sp.ldp, static_cast<float*>(g.prob[0].c),
+                       sp.stride, sp.splits, rows, cols, sp.ldp, static_cast<float*>(g.prob[0].c),
                        g.nprob > 1 ? static_cast<float*>(g.prob[1].c) : nullptr, g.ldc, g.alpha,
-                       g.alpha_ptr, g.epi == GemmEpilogue::AccumF32, g.c_trans);
+                       g.alpha_ptr, g.epi == GemmEpilogue::AccumF32);
     return hipGetLastError();
   }
   GemmArgs one = g;

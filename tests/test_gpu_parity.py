@@ -467,6 +467,25 @@ def _tied_f32_row_bytes(h, v):
     return 2 * pitch * 4 + 2 * ((v + 255) // 256) * 16 + 2 * 4 + 2 * ((h + 7) // 8 * 8) * 4
 
 
+def _split_k_bytes(m, n, k, nprob, trans=False):
+    """fp32 partial bytes of a backward GEMM that splits K (the library's
+    policy: about 256 workgroups, at least 128 elements of K per split, at most
+    64 splits and 256 MB; partials in C's orientation, rows padded to 4), or 0
+    when it does not split."""
+    cdiv = lambda a, b: -(-a // b)
+    rows, cols = (n, m) if trans else (m, n)
+    ldp = cdiv(cols, 4) * 4
+    tiles = cdiv(m, 256) * cdiv(n, 256) * nprob
+    if tiles >= 192:
+        return 0
+    s = min(cdiv(256, tiles), k // 128, 64, (256 << 20) // (nprob * rows * ldp * 4))
+    if s <= 1:
+        return 0
+    length = cdiv(cdiv(k, s), 64) * 64
+    s = cdiv(k, length)
+    return s * nprob * rows * ldp * 4 if s > 1 else 0
+
+
 def test_oom_retry_walks_the_doubling_schedule(torch_dev):
     """A memory limit that one chunk of 1024 rows exceeds and two chunks of
     512 rows fit: the retry takes the next entry of chunk_doubling_schedule
@@ -507,7 +526,10 @@ def test_oom_retry_halves_the_staging_group(torch_dev):
     y = uniform_labels(bt, v, 74)
     opts = LossOptions(kd_weight=0.4, temperature=1.5, chunk_size=ChunkSize.Fixed(128))
     row = _tied_f32_row_bytes(h, v)
-    limit = int(1.25 * 256 * row) + (4 << 20)
+    # two chunks (256 rows) per group plus the split-K partials of their
+    # backward GEMMs (one buffer, sized for the larger of the two)
+    split = max(_split_k_bytes(256, h, v, 2), _split_k_bytes(h, v, 2 * 256, 1, trans=True))
+    limit = int(1.25 * 256 * row) + (4 << 20) + split
     assert limit < 512 * row
     ctx = H.Context(0)
     ctx.set_memory_limit(limit)
