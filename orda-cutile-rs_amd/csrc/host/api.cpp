@@ -683,6 +683,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       d.alpha = 1.f;
       d.alpha_ptr = ms_dev;
       d.group_m = 4;
+      d.share_rounds = true;
       d.nprob = 1;
       d.prob[0] = {Gs, in.W.p, in.gh.p + gs * in.gh.ld};
       const bool fuse = P.has_ght && P.mode == ORDA_TEACHER_TIED && in.ght.ld == in.gh.ld;

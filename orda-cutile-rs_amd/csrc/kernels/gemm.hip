@@ -32,7 +32,9 @@
 // bf16 uses v_mfma_f32_16x16x32_bf16, fp32 v_mfma_f32_16x16x4_f32 (four per
 // 16-byte k-group); accumulation is fp32 in both. Workgroups are rastered in
 // groups of M-tiles and each XCD receives a contiguous range, so tiles that
-// share an operand strip share that XCD's L2.
+// share an operand strip share that XCD's L2; products with few N-tiles
+// (grad_hidden) instead run rounds that all XCDs spend on the same operand
+// strips (map_tile).
 //
 // The Logits epilogue fuses the statistics the row pass needs: for every row
 // and every 256-column tile it writes {max, Σe^(x-max), Σe^((x-max)/T), Σx}
@@ -510,11 +512,41 @@ struct TileCoord {
   int p, m0, n0, ntile;
 };
 
+__device__ __forceinline__ TileCoord tile_at(int64_t pm, int64_t pn, int64_t Mt) {
+  TileCoord c;
+  c.p = static_cast<int>(pm / Mt);
+  c.m0 = static_cast<int>((pm % Mt) * kTile);
+  c.n0 = static_cast<int>(pn * kTile);
+  c.ntile = static_cast<int>(pn);
+  return c;
+}
+
 __device__ __forceinline__ TileCoord map_tile(const GemmArgs& g, int64_t t) {
   const int64_t Mt = (g.M + kTile - 1) / kTile;
   const int64_t Nt = (g.N + kTile - 1) / kTile;
-  const int64_t Mv = Mt * g.nprob;
-  const int64_t T = Mv * Nt;
+  int64_t Mv = Mt * g.nprob;
+  int64_t T = Mv * Nt;
+  int64_t mfirst = 0;   // first M-tile of the grouped raster below
+  // Shared rounds (few N-tiles, long K: grad_hidden). Each round of 256
+  // workgroups, one per CU, covers 8*xm M-tiles x all Nt N-tiles: xn = Nt/4
+  // XCDs side by side in N, xm = 8/xn in M, each XCD 8 M x 4 N (12 operand
+  // strips per stage in its L2, as in the grouped raster). The XCDs of a
+  // round read the same strips at the same time, so the MALL serves the
+  // repeats and each strip is fetched from HBM once per round (the grouped
+  // raster walks an XCD's M-tiles over two rounds of N and fetches them
+  // twice). Tiles past the last whole round take the grouped raster.
+  if (g.share_rounds && (Nt == 4 || Nt == 8 || Nt == 16 || Nt == 32)) {
+    const int64_t xn = Nt / 4, xm = 8 / xn, rm = 8 * xm;
+    const int64_t full = Mv / rm * rm * Nt;   // a multiple of 256
+    if (t < full) {
+      const int64_t x = t % 8, l = t / 8, k = l / 32, j = l % 32;
+      return tile_at(k * rm + (x / xn) * 8 + j % 8, (x % xn) * 4 + j / 8, Mt);
+    }
+    t -= full;
+    T -= full;
+    mfirst = Mv / rm * rm;
+    Mv -= mfirst;
+  }
   // Consecutive workgroups land on consecutive XCDs; give each XCD a
   // contiguous range of the raster so tiles sharing operands share an L2.
   const int64_t per = T / 8;
@@ -525,14 +557,7 @@ __device__ __forceinline__ TileCoord map_tile(const GemmArgs& g, int64_t t) {
   const int64_t first = gid * gm;
   const int64_t gsize = (Mv - first) < gm ? (Mv - first) : gm;
   const int64_t r = t % in_group;
-  const int64_t pm = first + r % gsize;
-  const int64_t pn = r / gsize;
-  TileCoord c;
-  c.p = static_cast<int>(pm / Mt);
-  c.m0 = static_cast<int>((pm % Mt) * kTile);
-  c.n0 = static_cast<int>(pn * kTile);
-  c.ntile = static_cast<int>(pn);
-  return c;
+  return tile_at(mfirst + first + r % gsize, r / gsize, Mt);
 }
 
 // Two floats as packed bf16 (round to nearest even), low half first.

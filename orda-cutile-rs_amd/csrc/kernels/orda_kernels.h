@@ -69,6 +69,9 @@ struct GemmArgs {
   // the deferred mean computed on the device by launch_label_check).
   const float* alpha_ptr;
   int group_m;            // M-tiles per raster group (L2 reuse of B)
+  // Rounds of 256 workgroups spanning all N-tiles, the XCDs of a round
+  // on the same operand strips (N of 4-32 tiles; other N: ignored).
+  bool share_rounds;
   // Store/Accum only: C is stored transposed, element (m, n) of the
   // product at C[n*ldc + m] (C is [N][ldc]).
   bool c_trans;
