@@ -143,6 +143,11 @@ def work_per_step(wl, plan):
     t_stats = (-(-v // 8192) if teacher == "precomputed" else nst) if rows_read > bt else 0
     paired = teacher == "tied" and dt == "bf16" and (kd > 0 or wt > 0)
     rowpass += bt * (nst * 16 + t_stats * 16 + (nst * 4 if paired else 0) + 8)
+    # bf16 logits are stored relative to their 128-column half-tile maxima:
+    # 4 bytes per half and row of the logits GEMM (Precomputed teacher rows
+    # are stored as they are)
+    if ls == 2:
+        rowpass += bt * nst * 8 * (2 if rows_read > bt and teacher != "precomputed" else 1)
     quant_b = v * h * 8 if quant else 0
     return {"gemm_logits": ("mfma", fwd), "gemm_grad_hidden": ("mfma", dgrad),
             "gemm_grad_weight": ("mfma", wgrad), "row_pass": ("hbm", rowpass),

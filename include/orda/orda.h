@@ -183,8 +183,10 @@ int32_t orda_ctx_set_memory_limit(orda_ctx *ctx, int64_t bytes);
 /* Bytes of logits staging the context may use per group of chunks
  * (default 16 GiB). Consecutive chunks up to this size share one logits
  * GEMM, row pass and backward GEMMs; a smaller budget runs more groups, each
- * accumulating into grad_W. No counterpart in the reference, which runs one
- * chunk at a time (src/api.rs:263-378). */
+ * accumulating into grad_W. The split-K partials of backward GEMMs with
+ * fewer output tiles than CUs (at most 256 MB) come on top of it. No
+ * counterpart in the reference, which runs one chunk at a time
+ * (src/api.rs:263-378). */
 int32_t orda_ctx_set_staging_budget(orda_ctx *ctx, int64_t bytes);
 /* Release the cached workspace. */
 int32_t orda_ctx_trim(orda_ctx *ctx);

@@ -466,6 +466,7 @@ int64_t staged_bytes_per_row(const LossPlan& P, const Inputs& in) {
               (orda::dtype_size(lt) + (lt == P.dt ? 0 : orda::dtype_size(P.dt)));
   b += 2 * nst * 16 + 2 * 4;   // statistics, label logits
   if (paired) b += nst * 4 + 16;   // cross partials, row constants
+  if (lt == orda::DType::BF16) b += 4 * nst * 4;   // half-tile maxima of both rows
   // fp32 logits: row constants and the gradient blocks' KL sums
   if (!paired && lt == orda::DType::F32)
     b += 16 + (P.kd > 0.f ? orda::row_pass_kl_blocks(P.v) * 8 : 0);
@@ -527,6 +528,11 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   const int64_t ldh_cat = round8(tied_tce ? 2 * cap : cap);
   void* hcat = ws(c, "hcat", std::max(h, P.has_gwt ? P.ht : int64_t{0}) * ldh_cat * es);
   float* cross = paired ? static_cast<float*>(ws(c, "cross", cap * nst * 4)) : nullptr;
+  // bf16 logits are stored relative to their half-tile maxima: per row
+  // pair and 128-column half, the student's and the teacher's maximum side
+  // by side (LogitStatsArgs::hmax).
+  const int64_t hld = 4 * nst;
+  float* hmax = lt == DType::BF16 ? static_cast<float*>(ws(c, "hmax", cap * hld * 4)) : nullptr;
   // Row constants of the chunked row passes (paired bf16 logits, or fp32
   // logits), and for fp32 logits with a KL term the per-block KL sums.
   const bool f32_rows = !paired && lt == DType::F32;
@@ -574,6 +580,8 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
     f.lg.labels = in.labels + gs;
     f.lg.ignore_index = P.ignore;
     f.lg.inv_t = inv_t;
+    f.lg.hmax = hmax;
+    f.lg.hmax_ld = hld;
     f.nprob = 1;
     f.prob[0] = {at(in.hs.p, gs * in.hs.ld, dt), in.W.p, Ls};
     const bool fuse_t = P.need_teacher && P.mode == ORDA_TEACHER_TIED && in.th.ld == in.hs.ld;
@@ -622,6 +630,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
         t.prob[0] = {at(in.th.p, gs * in.th.ld, dt), sep ? in.tw.p : in.W.p, Lt};
         t.lg.stats = stats + btg * nst;
         t.lg.xy = xy + btg;
+        t.lg.hmax = hmax ? hmax + 1 : nullptr;   // the teacher side
         timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_gemm(t, c->stream); });
       }
     }
@@ -647,6 +656,11 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       r.xy_s = xy;
       r.xy_t = xy + btg;
       r.cross = cross;
+      // Rows of the logits GEMM in bf16 are relative to their half-tile
+      // maxima; Precomputed teacher rows (converted or in place) are not.
+      r.hmax_s = hmax;
+      r.hmax_t = hmax && P.need_teacher && P.mode != ORDA_TEACHER_PRECOMPUTED ? hmax + 1 : nullptr;
+      r.hmax_ld = hld;
       r.row_consts = rconst;
       r.kl_part = klpart;
       r.labels = in.labels + gs;
@@ -942,6 +956,7 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
       (void)hipGetLastError();
       ws_release(c, "logits");
       ws_release(c, "hcat");
+      ws_release(c, "hmax");
       ws_release(c, "stats");
       ws_release(c, "xy");
       ws_release(c, "dlogits");

@@ -43,7 +43,10 @@
 // teacher rows interleaved in blocks of 16) it also writes the tile's KL
 // cross term Σ e^((t-max_t)/T)·(t - s), so that every loss term comes from
 // fp32 accumulators and the stored logits (then bf16) only feed the
-// gradient. Each lane stores its 4 consecutive columns directly.
+// gradient. Each lane stores its 4 consecutive columns directly. bf16 logits
+// are stored relative to the maximum of their 128-column half tile, in log2
+// units, with those maxima beside the statistics: their rounding error then
+// follows their distance below the maximum, not their magnitude.
 #include <float.h>
 #include <math.h>
 
@@ -1176,6 +1179,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         __builtin_nontemporal_store(w[jp / 2], reinterpret_cast<u32x4*>(rowbase + 16 * jp + c0));
     };
     constexpr bool kSwapStore = Elem<LT>::kSize == 2;
+    // bf16 logits are stored as t = (x - m)·log2(e), m the row's maximum over
+    // this wave's 128 columns (written to hmax after the merge below): the
+    // first exponent's argument, so e^((x-m)/T) = 2^(t/T) costs no more.
+    constexpr bool kRel = Elem<LT>::kSize == 2;
+    const float inv_t = g.lg.inv_t;
     // The label's logit, if this lane holds its column (16j + e == yl):
     // select e, then j.
     auto pick = [&](const f32x4 (&v)[kFrag], int yl) {
@@ -1225,14 +1233,27 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         mx = quad_max(mx);
         // exp((x - mx)) and exp((x - mx)/T) as exp2 of one fma each.
         const float o1 = -mx * kLog2e, oT = -mx * it2;
+        const bool hit = yl >= 0 && (yl & 12) == 0;
+        float xyv = 0.f;   // the label's fp32 logit, before av holds t
+        if constexpr (kRel) {
+          if (hit) xyv = pick(av, yl);
+        }
         float d1 = 0.f, dT = 0.f, sx = 0.f;
 #pragma unroll
         for (int j = 0; j < kFrag; ++j) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float x = av[j][e];
-            const float a1 = __builtin_amdgcn_exp2f(fmaf(x, kLog2e, o1));
-            const float aT = __builtin_amdgcn_exp2f(fmaf(x, it2, oT));
+            float a1, aT;
+            if constexpr (kRel) {
+              const float t = fmaf(x, kLog2e, o1);
+              a1 = __builtin_amdgcn_exp2f(t);
+              aT = __builtin_amdgcn_exp2f(t * inv_t);
+              av[j][e] = t;
+            } else {
+              a1 = __builtin_amdgcn_exp2f(fmaf(x, kLog2e, o1));
+              aT = __builtin_amdgcn_exp2f(fmaf(x, it2, oT));
+            }
             if (kFull || j * 16 + e < ncol) {
               d1 += a1;
               dT += aT;
@@ -1240,7 +1261,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
             }
           }
         }
-        const bool hit = yl >= 0 && (yl & 12) == 0;
         d1 = quad_sum(d1);
         dT = quad_sum(dT);
         sx = quad_sum(sx);
@@ -1248,7 +1268,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         u32x4 aw[kFrag / 2];
         if constexpr (kSwapStore && kFull) swap_rows(av, aw);
         if (row < g.M) {
-          if (hit) g.lg.xy[tc.p * g.M + row] = pick(av, yl);
+          if (hit) g.lg.xy[tc.p * g.M + row] = kRel ? xyv : pick(av, yl);
           if constexpr (kSwapStore && kFull)
             store_swapped(C + row * g.ldc + (colw - 4 * lgrp), aw);
           else
@@ -1288,16 +1308,35 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         mt = quad_max(mt);
         const float o1s = -ms * kLog2e, oTs = -ms * it2;
         const float o1t = -mt * kLog2e, oTt = -mt * it2;
+        const bool hit = yl >= 0 && (yl & 12) == 0;
+        float xys = 0.f, xyt = 0.f;   // the label's fp32 logits, before as/at hold t
+        if constexpr (kRel) {
+          if (hit) {
+            xys = pick(as, yl);
+            xyt = pick(at, yl);
+          }
+        }
         float d1s = 0.f, dTs = 0.f, sxs = 0.f, d1t = 0.f, dTt = 0.f, sxt = 0.f, cx = 0.f;
 #pragma unroll
         for (int j = 0; j < kFrag; ++j) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float xs = as[j][e], xt = at[j][e];
-            const float a1s = __builtin_amdgcn_exp2f(fmaf(xs, kLog2e, o1s));
-            const float aTs = __builtin_amdgcn_exp2f(fmaf(xs, it2, oTs));
-            const float a1t = __builtin_amdgcn_exp2f(fmaf(xt, kLog2e, o1t));
-            const float aTt = __builtin_amdgcn_exp2f(fmaf(xt, it2, oTt));
+            float a1s, aTs, a1t, aTt;
+            if constexpr (kRel) {
+              const float ts = fmaf(xs, kLog2e, o1s), tt = fmaf(xt, kLog2e, o1t);
+              a1s = __builtin_amdgcn_exp2f(ts);
+              aTs = __builtin_amdgcn_exp2f(ts * inv_t);
+              a1t = __builtin_amdgcn_exp2f(tt);
+              aTt = __builtin_amdgcn_exp2f(tt * inv_t);
+              as[j][e] = ts;
+              at[j][e] = tt;
+            } else {
+              a1s = __builtin_amdgcn_exp2f(fmaf(xs, kLog2e, o1s));
+              aTs = __builtin_amdgcn_exp2f(fmaf(xs, it2, oTs));
+              a1t = __builtin_amdgcn_exp2f(fmaf(xt, kLog2e, o1t));
+              aTt = __builtin_amdgcn_exp2f(fmaf(xt, it2, oTt));
+            }
             if (kFull || j * 16 + e < ncol) {
               d1s += a1s;
               dTs += aTs;
@@ -1309,7 +1348,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
             }
           }
         }
-        const bool hit = yl >= 0 && (yl & 12) == 0;
         d1s = quad_sum(d1s);
         dTs = quad_sum(dTs);
         sxs = quad_sum(sxs);
@@ -1329,8 +1367,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         }
         if (row < prs) {
           if (hit) {   // one lane of a row at most, for one column tile
-            g.lg.xy[row] = pick(as, yl);
-            g.lg.xy[prs + row] = pick(at, yl);
+            g.lg.xy[row] = kRel ? xys : pick(as, yl);
+            g.lg.xy[prs + row] = kRel ? xyt : pick(at, yl);
           }
           if constexpr (kSwapStore && kFull) {
             store_swapped(C + row * g.ldc + (colw - 4 * lgrp), sw);
@@ -1374,6 +1412,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
           cx = xpart[tid] * fa + xpart[256 + tid] * fb;
         }
         g.lg.stats[orow * g.lg.stats_ld + tc.ntile] = s;
+        if constexpr (kRel) {   // the two halves' maxima, beside the other block's
+          const int64_t hrow = prs > 0 ? (teacher ? orow - prs : orow) : tc.m0 + tid;
+          const int side = prs > 0 ? (teacher ? 1 : 0) : tc.p;
+          float* hp = g.lg.hmax + hrow * g.lg.hmax_ld + 4 * tc.ntile + side;
+          hp[0] = a.x;
+          hp[2] = b.x;
+        }
         if (teacher) g.lg.cross[(orow - prs) * g.lg.stats_ld + tc.ntile] = cx;
       }
     }
@@ -1604,6 +1649,9 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
   if (g.epi == GemmEpilogue::Logits && g.lg.pair_rows > 0 &&
       (g.nprob != 1 || g.lg.cross == nullptr || g.lg.pair_teacher == nullptr ||
        g.in_type != DType::BF16 || g.M != 2 * ((g.lg.pair_rows + 15) / 16 * 16)))
+    return hipErrorInvalidValue;
+  if (g.epi == GemmEpilogue::Logits && g.logits_type == DType::BF16 &&
+      (g.lg.hmax == nullptr || g.lg.hmax_ld % 2 || g.lg.hmax_ld < 4 * ((g.N + kTile - 1) / kTile)))
     return hipErrorInvalidValue;
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
   const int64_t tiles = ((g.M + kTile - 1) / kTile) * ((g.N + kTile - 1) / kTile) * g.nprob;

@@ -53,6 +53,17 @@ struct LogitStatsArgs {
   int64_t pair_rows;
   float* cross;
   const void* pair_teacher;
+  // bf16 logits (required then): each logit is stored relative to the
+  // maximum m of its 128-column half tile k (k = 2*n_tile + h), in log2
+  // units, C = bf16((x - m) * log2(e)), so the bf16 rounding error of a
+  // stored logit scales with its distance below that maximum, not with its
+  // magnitude. m goes to hmax[r * hmax_ld + 2*k + side], r the row within
+  // its block (student rows side 0, teacher rows side 1: the paired rows,
+  // or problem p as side p; a teacher-only launch passes hmax + 1), so a
+  // row pair's two maxima of one half are adjacent. hmax_ld >= 4*ceil(N/256),
+  // even. fp32 logits are stored as they are.
+  float* hmax;
+  int64_t hmax_ld;
 };
 
 struct GemmArgs {
@@ -138,6 +149,16 @@ struct RowPassArgs {
   // fp32 chunked pass with a KL term: n_rows * row_pass_kl_blocks(v)
   // float2, each column block's share of the row's KL sums.
   float2* kl_part;
+  // bf16 logits stored relative to their half-tile maxima by the logits
+  // GEMM (LogitStatsArgs::hmax): half k of row r has its maximum at
+  // hmax_s[r*hmax_ld + 2*k] (student) and hmax_t[r*hmax_ld + 2*k]
+  // (teacher, hmax_s + 1 for the GEMM's paired layout), or null for rows
+  // stored as they are (Precomputed teacher logits, the chunk-launcher
+  // entry point). The chunked pass over paired bf16 rows runs only with
+  // them, interleaved.
+  const float* hmax_s;
+  const float* hmax_t;
+  int64_t hmax_ld;
   // Gradient rows: written at grad_s/grad_t + r*ld in gtype. Null grad_s
   // means in place (gtype == ltype).
   void* grad_s;

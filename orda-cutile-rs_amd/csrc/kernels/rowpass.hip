@@ -375,6 +375,21 @@ __device__ __forceinline__ void store8_nt(__bf16* p, const float (&g)[8]) {
   __builtin_nontemporal_store(Vec<__bf16>::pack(g), reinterpret_cast<u32x4*>(p));
 }
 
+// The half-tile maxima of one row pair (RowPassArgs::hmax_s / hmax_t), or
+// 0 where the rows are stored as they are.
+struct HalfRel {
+  const float* ps;
+  const float* pt;
+  bool rs, rt;
+  __device__ HalfRel(const RowPassArgs& a, int64_t r, bool teacher)
+      : ps(a.hmax_s ? a.hmax_s + r * a.hmax_ld : nullptr),
+        pt(teacher && a.hmax_t ? a.hmax_t + r * a.hmax_ld : nullptr),
+        rs(a.hmax_s != nullptr),
+        rt(teacher && a.hmax_t != nullptr) {}
+  __device__ float s(int64_t col) const { return rs ? ps[2 * (col >> 7)] : 0.f; }
+  __device__ float t(int64_t col) const { return rt ? pt[2 * (col >> 7)] : 0.f; }
+};
+
 // The row pass of distillation_loss, specialised on the logits type LT, the
 // gradient type GT and whether the KL term (KL) and the teacher CE gradient
 // (TG) are present. Same results as row_pass_kernel<LT, false>, with the
@@ -388,8 +403,9 @@ __device__ __forceinline__ void store8_nt(__bf16* p, const float (&g)[8]) {
 //  * two 8-element groups per row and thread are in flight per iteration;
 //  * an ignored row is a zero fill.
 // Logits are read in LT (fp32, or bf16 only when the inputs are bf16 and
-// the loss terms do not need fp32 logits) and gradients written in GT, in
-// place when grad_s is null.
+// the loss terms do not need fp32 logits; bf16 rows of the logits GEMM are
+// relative to their half-tile maxima) and gradients written in GT, in place
+// when grad_s is null.
 template <typename LT, typename GT, bool KL, bool TG>
 __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a) {
   __shared__ Stat sstat[kThreads / 64];
@@ -459,26 +475,38 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
   const float cd = TG ? rlog2(wt, fm) - lse1_t * kLog2e : 0.f;    // w_t·p_t
   const float k0 = -ws * eps, kt0 = -wt * eps;
   const float ky = ws * one_m_a, kyt = wt * one_m_a;
+  // bf16 rows stored relative to their half-tile maxima (log2 units; the
+  // launcher keeps such rows away from the KL cross term below, which needs
+  // the logits themselves): scale 1 (1/T) instead of log2(e) (log2(e)/T),
+  // and each 128-column half's maximum folded into the offsets.
+  const HalfRel hr(a, r, HT);
+  const float e1s = hr.rs ? 1.f : kLog2e, eTs = hr.rs ? inv_t : it2;
+  const float e1t = hr.rt ? 1.f : kLog2e, eTt = hr.rt ? inv_t : it2;
+  auto offs = [&](float hs, float ht) {
+    return float4{fmaf(hs, kLog2e, ca), fmaf(hs, it2, cb), fmaf(ht, it2, cc), fmaf(ht, kLog2e, cd)};
+  };
 
   float cross = 0.f, sum_c = 0.f;
   // Gradient of one element pair, without the label term.
-  auto elem = [&](float xs, float xt, float& g, float& gt, float& cx, float& c) {
-    g = fmaf(sgn, __builtin_amdgcn_exp2f(fmaf(xs, kLog2e, ca)), k0);
+  auto elem = [&](float xs, float xt, const float4& o, float& g, float& gt, float& cx, float& c) {
+    g = fmaf(sgn, __builtin_amdgcn_exp2f(fmaf(xs, e1s, o.x)), k0);
     if (KL) {
-      const float b = __builtin_amdgcn_exp2f(fmaf(xs, it2, cb));
-      c = __builtin_amdgcn_exp2f(fmaf(xt, it2, cc));
+      const float b = __builtin_amdgcn_exp2f(fmaf(xs, eTs, o.y));
+      c = __builtin_amdgcn_exp2f(fmaf(xt, eTt, o.z));
       g += b - c;
       cx = c * (xt - xs);
     }
-    if (TG) gt = __builtin_amdgcn_exp2f(fmaf(xt, kLog2e, cd)) + kt0;
+    if (TG) gt = __builtin_amdgcn_exp2f(fmaf(xt, e1t, o.w)) + kt0;
   };
-  auto compute = [&](int j0, const float (&xs)[NV], const float (&xt)[NV], bool full) {
+  auto compute = [&](int j0, const float (&xs)[NV], const float (&xt)[NV], float hs, float ht,
+                     bool full) {
     float g[NV], gt[NV];
+    const float4 o = offs(hs, ht);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const bool valid = full || j0 + i < v;
       float gi = 0.f, ti = 0.f, cx = 0.f, c = 0.f;
-      elem(xs[i], xt[i], gi, ti, cx, c);
+      elem(xs[i], xt[i], o, gi, ti, cx, c);
       if (KL) {
         cross += valid ? cx : 0.f;
         sum_c += valid ? c : 0.f;
@@ -513,22 +541,28 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
     const int jb0 = nk > 1 ? j + kStep : j;
     load8(srow + j, as);
     if (HT) load8(trow + j, at);
+    float ahs = hr.s(j), aht = hr.t(j);
     load8(srow + jb0, bs);
     if (HT) load8(trow + jb0, bt);
+    float bhs = hr.s(jb0), bht = hr.t(jb0);
     int k = 0;
     for (; k + 1 < nk; k += 2) {
-      compute(j, as, at, true);
+      compute(j, as, at, ahs, aht, true);
       const int ja = k + 2 < nk ? j + 2 * kStep : j;   // re-read when past the end
       load8(srow + ja, as);
       if (HT) load8(trow + ja, at);
-      compute(j + kStep, bs, bt, true);
+      ahs = hr.s(ja);
+      aht = hr.t(ja);
+      compute(j + kStep, bs, bt, bhs, bht, true);
       const int jb = k + 3 < nk ? j + 3 * kStep : j;
       load8(srow + jb, bs);
       if (HT) load8(trow + jb, bt);
+      bhs = hr.s(jb);
+      bht = hr.t(jb);
       j += 2 * kStep;
     }
     if (k < nk) {
-      compute(j, as, at, true);
+      compute(j, as, at, ahs, aht, true);
       j += kStep;
     }
   }
@@ -536,14 +570,15 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
     float s0[NV], t0[NV];
     load8(srow + j, s0);
     if (HT) load8(trow + j, t0);
-    if (j < jfull) compute(j, s0, t0, true);
-    else compute(j, s0, t0, false);
+    const float hs0 = hr.s(j), ht0 = hr.t(j);
+    if (j < jfull) compute(j, s0, t0, hs0, ht0, true);
+    else compute(j, s0, t0, hs0, ht0, false);
   }
   // The label column: its owner (the thread that wrote it, so in program
   // order) rewrites it with the −(1−α)·w term included.
   if (owner) {
     float gy = 0.f, ty = 0.f, cx = 0.f, c = 0.f;
-    elem(xs_y, xt_y, gy, ty, cx, c);
+    elem(xs_y, xt_y, offs(hr.s(y), hr.t(y)), gy, ty, cx, c);
     gsrow[y] = static_cast<GT>(gy - ky);
     if (TG) gtrow[y] = static_cast<GT>(ty - kyt);
   }
@@ -692,15 +727,22 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
     return;
   }
   const float4 k = a.row_consts[r];
-  const float it2 = kLog2e * rdiv(1.0f, a.temperature, a.fast_math);
+  const float inv_t = rdiv(1.0f, a.temperature, a.fast_math);
+  const float it2 = kLog2e * inv_t;
   const float eps = static_cast<float>(static_cast<double>(a.label_smoothing) / static_cast<double>(v));
   const float one_m_a = 1.0f - a.label_smoothing;
   const float sgn = a.w_s < 0.f ? -1.f : 1.f;
   const float k0 = -a.w_s * eps, kt0 = -a.w_t * eps;
-  auto elem = [&](float xs, float xt, float& g, float& gt) {
-    g = fmaf(sgn, __builtin_amdgcn_exp2f(fmaf(xs, kLog2e, k.x)), k0);
-    if (KL) g += __builtin_amdgcn_exp2f(fmaf(xs, it2, k.y)) - __builtin_amdgcn_exp2f(fmaf(xt, it2, k.z));
-    if (TG) gt = __builtin_amdgcn_exp2f(fmaf(xt, kLog2e, k.w)) + kt0;
+  // Both rows are stored relative to their half-tile maxima, in log2 units
+  // (LogitStatsArgs::hmax): each 128-column half's maximum is folded into
+  // the exponent offsets, and the T terms scale by 1/T.
+  auto offs = [&](float hs, float ht) {
+    return float4{fmaf(hs, kLog2e, k.x), fmaf(hs, it2, k.y), fmaf(ht, it2, k.z), fmaf(ht, kLog2e, k.w)};
+  };
+  auto elem = [&](float xs, float xt, const float4& o, float& g, float& gt) {
+    g = fmaf(sgn, __builtin_amdgcn_exp2f(xs + o.x), k0);
+    if (KL) g += __builtin_amdgcn_exp2f(fmaf(xs, inv_t, o.y)) - __builtin_amdgcn_exp2f(fmaf(xt, inv_t, o.z));
+    if (TG) gt = __builtin_amdgcn_exp2f(xt + o.w) + kt0;
   };
   // The label column's logits, read by the thread that writes that column.
   const int64_t yl = y - c0;
@@ -709,6 +751,19 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
   if (owner) {
     xs_y = static_cast<float>(srow[y]);
     if (KL || TG) xt_y = static_cast<float>(trow[y]);
+  }
+  // Half-tile maxima, loaded first (ahead of the logits, so that no wait
+  // comes between): the student's and the teacher's maxima of a half are
+  // adjacent, one float2 per lane (lanes of one half share it). A lane past
+  // the row's end reads the row's last half, which it does not use.
+  float hs[kChunkVec], ht[kChunkVec];
+#pragma unroll
+  for (int q = 0; q < kChunkVec; ++q) {
+    const int64_t hk = (c0 + (static_cast<int64_t>(q) * kGradThreads + tid) * NV) >> 7;
+    const int64_t hl = (v - 1) >> 7;
+    const float2 m = *reinterpret_cast<const float2*>(a.hmax_s + r * a.hmax_ld + 2 * (hk < hl ? hk : hl));
+    hs[q] = m.x;
+    ht[q] = m.y;
   }
   // The loads stay packed (bf16 pairs) until their group is computed.
   u32x4 rs[kChunkVec], rt[kChunkVec];
@@ -728,10 +783,11 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
     Vec<__bf16>::unpack(rs[q], xs);
     if (KL || TG) Vec<__bf16>::unpack(rt[q], xt);
     float g[NV], gt[NV];
+    const float4 o = offs(hs[q], ht[q]);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       float gi = 0.f, ti = 0.f;
-      elem(xs[i], xt[i], gi, ti);
+      elem(xs[i], xt[i], o, gi, ti);
       const bool valid = j + i < v;
       g[i] = valid ? gi : 0.f;
       gt[i] = valid ? ti : 0.f;
@@ -741,7 +797,7 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
   }
   if (owner) {   // the label term, after this thread's own store of that column
     float gy = 0.f, ty = 0.f;
-    elem(xs_y, xt_y, gy, ty);
+    elem(xs_y, xt_y, offs(hs[0], ht[0]), gy, ty);   // column y is in this thread's vector
     srow[y] = static_cast<__bf16>(gy - a.w_s * one_m_a);
     if (TG) trow[y] = static_cast<__bf16>(ty - a.w_t * one_m_a);
   }
@@ -1081,6 +1137,12 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(FinalizeArgs a) {
 
 hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
   if (a.n_rows <= 0) return hipSuccess;
+  // Half-tile-relative rows: bf16 logits of the logits GEMM only, and never
+  // where the KL cross term is formed from the stored logits.
+  if ((a.hmax_s != nullptr || a.hmax_t != nullptr) &&
+      (a.split || a.ltype != DType::BF16 || (a.kl && a.cross == nullptr) ||
+       a.hmax_ld < 4 * ((a.v + 255) / 256)))
+    return hipErrorInvalidValue;
   dim3 grid(static_cast<unsigned>(a.n_rows));
   if (a.split) {   // any pitch and alignment
     if (a.ltype == DType::BF16)
@@ -1098,9 +1160,11 @@ hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
   if (a.grad_s && (tg && a.grad_t == nullptr)) return hipErrorInvalidValue;
   if (a.ld_t && ((a.ld_t % 8) || (tg && a.grad_s == nullptr))) return hipErrorInvalidValue;
   if (a.cross != nullptr && a.row_consts != nullptr && a.ltype == DType::BF16 &&
-      a.grad_s == nullptr && a.ld_t == 0 && (!(kl || tg || a.teacher_ce) || has_t)) {
-    // Paired layout, bf16 in place: per-row constants, then the chunked
-    // elementwise gradient.
+      a.grad_s == nullptr && a.ld_t == 0 && (!(kl || tg || a.teacher_ce) || has_t) &&
+      a.hmax_s != nullptr && a.hmax_t == a.hmax_s + 1 && a.hmax_ld % 2 == 0 &&
+      reinterpret_cast<uintptr_t>(a.hmax_s) % 8 == 0) {
+    // Paired layout, bf16 in place (rows relative to their half-tile
+    // maxima): per-row constants, then the chunked elementwise gradient.
     const int64_t chunks = (a.v + kChunk - 1) / kChunk;
     const int64_t blocks = a.n_rows * chunks;
     const dim3 cgrid(static_cast<unsigned>((a.n_rows + kThreads / 64 - 1) / (kThreads / 64)));

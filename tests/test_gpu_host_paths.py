@@ -263,9 +263,10 @@ def test_staging_budget_bounds_the_group(torch_dev):
     """The group of chunks staged together is sized so that its device
     buffers fit the context's staging budget, counting every per-row buffer:
     bf16 logits of both rows, tile statistics, label logits, KL cross
-    partials and row constants, and the [h_s; h_t] rows grad_W multiplies.
-    Bytes per row at H=4096, V=8192 (pitch 8256): 2*8256*2 + 2*32*16 + 2*4
-    + 32*4 + 16 + 2*4096*2 = 50584. With a budget of 2.5 chunks of 1024 rows,
+    partials and row constants, the half-tile maxima of both rows, and the
+    [h_s; h_t] rows grad_W multiplies. Bytes per row at H=4096, V=8192
+    (pitch 8256): 2*8256*2 + 2*32*16 + 2*4 + 32*4 + 16 + 2*64*4 + 2*4096*2
+    = 51096. With a budget of 2.5 chunks of 1024 rows,
     two chunks are staged at a time (two logits GEMMs; the groups are large
     enough that no backward GEMM splits K) and the workspace stays within
     the budget (plus the per-call row losses)."""
@@ -277,7 +278,7 @@ def test_staging_budget_bounds_the_group(torch_dev):
     ht = torch.randn(bt, h, generator=g, device=dev).to(torch.bfloat16)
     w = (torch.randn(v, h, generator=g, device=dev) * 0.02).to(torch.bfloat16)
     y = torch.randint(0, v, (bt,), generator=g, device=dev)
-    row = 2 * 8256 * 2 + 2 * 32 * 16 + 2 * 4 + 32 * 4 + 16 + 2 * 4096 * 2
+    row = 2 * 8256 * 2 + 2 * 32 * 16 + 2 * 4 + 32 * 4 + 16 + 2 * 64 * 4 + 2 * 4096 * 2
     budget = int(2.5 * cs * row)
     ctx = H.Context(0)
     ctx.set_staging_budget(budget)
