@@ -1096,6 +1096,9 @@ __global__ __launch_bounds__(kThreads) void row_stats_seg_kernel(RowStatsArgs a,
 __global__ __launch_bounds__(kThreads) void finalize_kernel(FinalizeArgs a) {
   __shared__ double red[3][kThreads];
   double s_nll = 0.0, t_nll = 0.0, kl = 0.0;
+  // Unrolled so that a thread's loads are in flight together; the
+  // additions keep their order.
+#pragma unroll 8
   for (int64_t i = threadIdx.x; i < a.bt; i += kThreads) {
     s_nll += static_cast<double>(a.row_nll_s[i]);
     t_nll += static_cast<double>(a.row_nll_t[i]);
@@ -1107,6 +1110,7 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(FinalizeArgs a) {
   for (int64_t c = threadIdx.x >> 6; c < nc; c += kThreads / 64) {
     const int64_t e = (c + 1) * a.chunk_size < a.bt ? (c + 1) * a.chunk_size : a.bt;
     double k = 0.0;
+#pragma unroll 8
     for (int64_t i = c * a.chunk_size + lane; i < e; i += 64) k += static_cast<double>(a.row_kl[i]);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) k += __shfl_xor(k, o);
