@@ -2,7 +2,8 @@
 
 The library is built in place by ``__graft_entry__.build()`` (or
 ``make -C orda-cutile-rs_amd``). Loading fails loudly when it is missing:
-there is no CPU fallback.
+there is no CPU fallback. ``ORDA_HIP_LIB`` names another build of the same
+library to load instead (the sanitizer build of the host code).
 """
 from __future__ import annotations
 
@@ -10,7 +11,7 @@ import ctypes as C
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "liborda_hip.so")
+LIB_PATH = os.environ.get("ORDA_HIP_LIB") or os.path.join(_HERE, "liborda_hip.so")
 
 ORDA_OK = 0
 ORDA_ERR_INVALID = 1
