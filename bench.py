@@ -335,6 +335,7 @@ def vendor_gemms(torch, wl, dev, s, w, t, reps):
 KERNEL_CLASSES = (
     # (substring of the kernel name, kernel kind)
     ("gemm_kk_logits_", "gemm_logits"),
+    ("gemm_kk_store_", "gemm_logits"),      # small fp32 problems: logits split over K
     ("gemm_km_", "gemm_grad_hidden"),
     ("gemm_kmt_", "gemm_grad_weight"),
     ("splitk_reduce", "splitk_reduce"),   # split-K: ordered sum of the partials
@@ -343,7 +344,7 @@ KERNEL_CLASSES = (
     ("row_consts_", "row_consts"),        # the chunked row pass: per-row constants ...
     ("row_grad_", "row_grad"),            # ... and the elementwise gradient
     ("row_kl_", "row_kl"),                # ... and, over fp32 logits, each row's KL
-    ("row_stats_kernel", "row_stats"),
+    ("row_stats_", "row_stats"),          # row_stats_kernel, row_stats_seg_kernel
     ("finalize_kernel", "finalize"),
     ("quant_", "quant"),                  # quant_vec_kernel, quant_kernel
     ("mark_targets", "mark_targets"),

@@ -599,7 +599,44 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       f.prob[1] = {at(in.th.p, gs * in.th.ld, dt), in.W.p, Lt};
     }
     f.group_m = 8;
-    timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_gemm(f, c->stream); });
+    // fp32 logits of fp32 inputs, for a product with fewer output tiles than
+    // CUs (small BT·V):
+    // stored plainly with K split over the CUs (launch_gemm's ordered split
+    // K), then each row's statistics and label logit from the stored rows,
+    // per 8192-column segment. The statistics epilogue needs all of K in one
+    // workgroup, so it cannot split. Returns whether that path ran.
+    auto logits_gemm = [&](const GemmArgs& g) {
+      GemmArgs sg = g;
+      sg.epi = GemmEpilogue::StoreF32;
+      sg.lg = LogitStatsArgs{};
+      if (lt != DType::F32 || g.in_type != DType::F32 || paired || gemm_split_bytes(sg) <= 0) {
+        timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_gemm(g, c->stream); });
+        return false;
+      }
+      attach_split_ws(c, sg);
+      timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_gemm(sg, c->stream); });
+      for (int p = 0; p < g.nprob; ++p) {
+        RowStatsArgs r{};
+        r.src_type = DType::F32;
+        r.src = g.prob[p].c;
+        r.lds = g.ldc;
+        r.dst_type = DType::F32;
+        r.ldd = g.ldc;
+        r.n_rows = g.M;
+        r.v = g.N;
+        r.stats = g.lg.stats + p * g.M * g.lg.stats_ld;
+        r.stats_ld = g.lg.stats_ld;
+        r.xy = g.lg.xy + p * g.M;
+        r.labels = g.lg.labels;
+        r.ignore_index = g.lg.ignore_index;
+        r.inv_t = g.lg.inv_t;
+        r.segmented = true;
+        timed(c, ORDA_KERNEL_OTHER, [&] { return launch_row_stats(r, c->stream); });
+      }
+      return true;
+    };
+    const bool seg_s = logits_gemm(f);
+    bool seg_t = fuse_t && seg_s;
     if (P.need_teacher && !fuse_t) {
       if (P.mode == ORDA_TEACHER_PRECOMPUTED) {
         RowStatsArgs r{};
@@ -631,7 +668,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
         t.lg.stats = stats + btg * nst;
         t.lg.xy = xy + btg;
         t.lg.hmax = hmax ? hmax + 1 : nullptr;   // the teacher side
-        timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_gemm(t, c->stream); });
+        seg_t = logits_gemm(t);
       }
     }
 
@@ -651,8 +688,9 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       r.stats_s = stats;
       r.stats_t = stats + btg * nst;
       r.stats_ld = nst;
-      r.stats_tiles = nst;
-      r.stats_tiles_t = P.mode != ORDA_TEACHER_PRECOMPUTED ? nst : P.online ? 1 : row_stats_segments(v);
+      const int64_t nseg = row_stats_segments(v);
+      r.stats_tiles = seg_s ? nseg : nst;
+      r.stats_tiles_t = P.mode == ORDA_TEACHER_PRECOMPUTED ? (P.online ? 1 : nseg) : seg_t ? nseg : nst;
       r.xy_s = xy;
       r.xy_t = xy + btg;
       r.cross = cross;

@@ -1430,7 +1430,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
 // check can tell them apart: gemm_<A layout><B layout>[t]_<epilogue>_<input>
 // [_<logits type>], layout k = K-major, m = N-major, t = C stored
 // transposed. The loss uses exactly these products: the logits (kk), the
-// hidden-row gradients (km) and grad_W computed transposed (kmt).
+// hidden-row gradients (km), grad_W computed transposed (kmt), and the fp32
+// logits of small problems stored plainly so that K can be split (kk_store).
 #define ORDA_GEMM(NAME, T, AK, BK, EPI, LT, CT) \
   __global__ __launch_bounds__(kThreads, 1) void NAME(GemmArgs g) { gemm_body<T, AK, BK, EPI, LT, CT>(g); }
 ORDA_GEMM(gemm_kk_logits_bf16_bf16, __bf16, true, true, GemmEpilogue::Logits, __bf16, false)
@@ -1445,6 +1446,9 @@ ORDA_GEMM(gemm_km_store_f32, float, true, false, GemmEpilogue::StoreF32, float, 
 ORDA_GEMM(gemm_km_accum_f32, float, true, false, GemmEpilogue::AccumF32, float, false)
 ORDA_GEMM(gemm_kmt_store_f32, float, true, false, GemmEpilogue::StoreF32, float, true)
 ORDA_GEMM(gemm_kmt_accum_f32, float, true, false, GemmEpilogue::AccumF32, float, true)
+// fp32 logits of small problems, stored plainly and split over K (the row
+// statistics then come from a separate pass over the stored logits).
+ORDA_GEMM(gemm_kk_store_f32, float, true, true, GemmEpilogue::StoreF32, float, false)
 #undef ORDA_GEMM
 
 typedef void (*GemmKernel)(GemmArgs);
@@ -1457,8 +1461,9 @@ GemmKernel select_kernel(const GemmArgs& g) {
     if (g.logits_type == DType::BF16) return bf ? gemm_kk_logits_bf16_bf16 : gemm_kk_logits_f32_bf16;
     return bf ? gemm_kk_logits_bf16_f32 : gemm_kk_logits_f32_f32;
   }
-  if (!g.a_kmajor || g.b_kmajor) return nullptr;
   const bool st = g.epi == E::StoreF32;
+  if (g.a_kmajor && g.b_kmajor && st && !g.c_trans && !bf) return gemm_kk_store_f32;
+  if (!g.a_kmajor || g.b_kmajor) return nullptr;
   if (g.c_trans)
     return bf ? (st ? gemm_kmt_store_bf16 : gemm_kmt_accum_bf16) : (st ? gemm_kmt_store_f32 : gemm_kmt_accum_f32);
   return bf ? (st ? gemm_km_store_bf16 : gemm_km_accum_bf16) : (st ? gemm_km_store_f32 : gemm_km_accum_f32);
