@@ -458,11 +458,11 @@ def test_validation_errors_match_reference(torch_dev):
 
 
 # Device bytes one staged chunk row takes at this fp32 Tied shape with teacher
-# CE: student and teacher logits rows (pitch 20000), the per-256-column tile
+# CE: student and teacher logits rows (pitch 20032), the per-256-column tile
 # statistics and label logits of both rows, and the two hidden rows that
 # grad_W multiplies ([h_s; h_t]).
 def _tied_f32_row_bytes(h, v):
-    pitch = (v + 7) // 8 * 8
+    pitch = (v + 63) // 64 * 64
     pitch += 64 if pitch % 1024 == 0 else 0
     return 2 * pitch * 4 + 2 * ((v + 255) // 256) * 16 + 2 * 4 + 2 * ((h + 7) // 8 * 8) * 4
 
