@@ -530,24 +530,25 @@ __device__ __forceinline__ TileCoord map_tile(const GemmArgs& g, int64_t t) {
   int64_t Mv = Mt * g.nprob;
   int64_t T = Mv * Nt;
   int64_t mfirst = 0;   // first M-tile of the grouped raster below
-  // Shared rounds (few N-tiles, long K: grad_hidden). Each round of 256
-  // workgroups, one per CU, covers 8*xm M-tiles x all Nt N-tiles: xn = Nt/4
-  // XCDs side by side in N, xm = 8/xn in M, each XCD 8 M x 4 N (12 operand
-  // strips per stage in its L2, as in the grouped raster). The XCDs of a
-  // round read the same strips at the same time, so the MALL serves the
-  // repeats and each strip is fetched from HBM once per round (the grouped
-  // raster walks an XCD's M-tiles over two rounds of N and fetches them
-  // twice). Tiles past the last whole round take the grouped raster.
-  if (g.share_rounds && (Nt == 4 || Nt == 8 || Nt == 16 || Nt == 32)) {
-    const int64_t xn = Nt / 4, xm = 8 / xn, rm = 8 * xm;
-    const int64_t full = Mv / rm * rm * Nt;   // a multiple of 256
+  // Shared rounds (few N-tiles, long K: grad_hidden). Each round covers a
+  // band of a*xm M-tiles x all Nt N-tiles: xn XCDs side by side in N (b =
+  // Nt/xn N-tiles each), xm = 8/xn in M (a M-tiles each), a*b <= 32 tiles
+  // per XCD (launch_gemm picks them: at Nt = 16, 8 x 4, the same 12 operand
+  // strips per stage in each L2 as the grouped raster). The XCDs of a round
+  // read the same strips at the same time, so the MALL serves the repeats
+  // and each strip is fetched from HBM once per band (the grouped raster
+  // walks an XCD's M-tiles over two passes of N and fetches them twice).
+  // Tiles past the last whole band take the grouped raster.
+  if (g.sh_a > 0) {
+    const int64_t a = g.sh_a, b = g.sh_b, xn = g.sh_xn, bm = a * (8 / xn), per = a * b;
+    const int64_t full = Mv / bm * bm * Nt;   // 8 * per tiles per band
     if (t < full) {
-      const int64_t x = t % 8, l = t / 8, k = l / 32, j = l % 32;
-      return tile_at(k * rm + (x / xn) * 8 + j % 8, (x % xn) * 4 + j / 8, Mt);
+      const int64_t x = t % 8, l = t / 8, k = l / per, j = l % per;
+      return tile_at(k * bm + (x / xn) * a + j % a, (x % xn) * b + j / a, Mt);
     }
     t -= full;
     T -= full;
-    mfirst = Mv / rm * rm;
+    mfirst = Mv / bm * bm;
     Mv -= mfirst;
   }
   // Consecutive workgroups land on consecutive XCDs; give each XCD a
@@ -1580,6 +1581,35 @@ struct SplitPlan {
 // minimum left grad_hidden on 64 workgroups and grad_W unsplit: 0.152 and
 // 0.141 ms against 0.072 and 0.070 ms with 128, reductions included; 64
 // measured the same as 128.)
+// Shared-round blocks (map_tile) for a product with share_rounds set: xn in
+// {1, 2, 4, 8} dividing the N-tiles, b = Nt/xn, a = 32/b; the most tiles per
+// XCD (at least 24), then the fewest operand strips per stage (a + b), then
+// the larger a (8 x 4 measured faster than 4 x 8 at Nt = 16). The band must
+// fit in the M-tiles at least once.
+void set_share_blocks(GemmArgs& g) {
+  g.sh_a = g.sh_b = g.sh_xn = 0;
+  if (!g.share_rounds) return;
+  const int64_t Nt = (g.N + kTile - 1) / kTile;
+  const int64_t Mv = ((g.M + kTile - 1) / kTile) * g.nprob;
+  int64_t best_a = 0, best_b = 0, best_xn = 0;
+  for (int64_t xn = 1; xn <= 8; xn *= 2) {
+    if (Nt % xn != 0) continue;
+    const int64_t b = Nt / xn, a = 32 / b;
+    if (a < 1 || a * b < 24 || a * (8 / xn) > Mv) continue;
+    const bool better = best_a == 0 || a * b > best_a * best_b ||
+                        (a * b == best_a * best_b &&
+                         (a + b < best_a + best_b || (a + b == best_a + best_b && a > best_a)));
+    if (better) {
+      best_a = a;
+      best_b = b;
+      best_xn = xn;
+    }
+  }
+  g.sh_a = static_cast<int>(best_a);
+  g.sh_b = static_cast<int>(best_b);
+  g.sh_xn = static_cast<int>(best_xn);
+}
+
 SplitPlan plan_split(const GemmArgs& g) {
   SplitPlan sp{1, g.K, 0, 0, 0};
   if (g.epi == GemmEpilogue::Logits || g.M <= 0 || g.N <= 0 || g.K <= 0) return sp;
@@ -1660,11 +1690,13 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
     return hipErrorInvalidValue;
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
   const int64_t tiles = ((g.M + kTile - 1) / kTile) * ((g.N + kTile - 1) / kTile) * g.nprob;
+  GemmArgs gr = g;
+  set_share_blocks(gr);
   const SplitPlan sp = plan_split(g);
   if (sp.splits > 1 && g.split_ws != nullptr && g.split_ws_bytes >= sp.bytes) {
     // Partials of every split with the Store epilogue (alpha 1), in C's
     // orientation, then one reduction applying the requested epilogue.
-    GemmArgs s = g;
+    GemmArgs s = gr;
     s.epi = GemmEpilogue::StoreF32;
     s.alpha = 1.f;
     s.alpha_ptr = nullptr;
@@ -1686,7 +1718,7 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
                        g.alpha_ptr, g.epi == GemmEpilogue::AccumF32);
     return hipGetLastError();
   }
-  GemmArgs one = g;
+  GemmArgs one = gr;
   one.split_k = 1;
   const GemmKernel k = select_kernel(one);
   if (k == nullptr) return hipErrorInvalidValue;

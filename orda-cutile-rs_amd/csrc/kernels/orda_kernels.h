@@ -80,9 +80,12 @@ struct GemmArgs {
   // the deferred mean computed on the device by launch_label_check).
   const float* alpha_ptr;
   int group_m;            // M-tiles per raster group (L2 reuse of B)
-  // Rounds of 256 workgroups spanning all N-tiles, the XCDs of a round
-  // on the same operand strips (N of 4-32 tiles; other N: ignored).
+  // Rounds spanning all N-tiles, the XCDs of a round on the same operand
+  // strips (launch_gemm picks the blocks; shapes it cannot fill: ignored).
   bool share_rounds;
+  // Set by launch_gemm when share_rounds applies: each XCD takes an
+  // sh_a (M) x sh_b (N) block of a round, sh_xn XCDs side by side in N.
+  int sh_a, sh_b, sh_xn;
   // Store/Accum only: C is stored transposed, element (m, n) of the
   // product at C[n*ldc + m] (C is [N][ldc]).
   bool c_trans;
