@@ -14,6 +14,8 @@ passes. Tolerances as in tests/parity.py: loss terms 1e-4 relative,
 gradients 1e-3 (fp32) or 2e-2 (bf16, the oracle fed the same bf16-rounded
 values), chunk plans bit-exact.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -26,7 +28,9 @@ from orda_hip import ChunkSize, LossOptions, Reduction, Teacher
 
 pytestmark = pytest.mark.gpu
 
-N_SMALL, N_MEDIUM = 64, 24
+# ORDA_SWEEP_SMALL / ORDA_SWEEP_MEDIUM draw more cases from the same generator.
+N_SMALL = int(os.environ.get("ORDA_SWEEP_SMALL", 64))
+N_MEDIUM = int(os.environ.get("ORDA_SWEEP_MEDIUM", 24))
 
 
 def draw_case(k, medium=False):
