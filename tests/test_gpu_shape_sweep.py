@@ -29,8 +29,8 @@ from orda_hip import ChunkSize, LossOptions, Reduction, Teacher
 pytestmark = pytest.mark.gpu
 
 # ORDA_SWEEP_SMALL / ORDA_SWEEP_MEDIUM draw more cases from the same generator.
-N_SMALL = int(os.environ.get("ORDA_SWEEP_SMALL", 64))
-N_MEDIUM = int(os.environ.get("ORDA_SWEEP_MEDIUM", 24))
+N_SMALL = int(os.environ.get("ORDA_SWEEP_SMALL", 128))
+N_MEDIUM = int(os.environ.get("ORDA_SWEEP_MEDIUM", 48))
 
 
 def draw_case(k, medium=False):
