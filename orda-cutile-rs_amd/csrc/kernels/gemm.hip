@@ -1672,8 +1672,45 @@ hipError_t launch_transpose_rows(const void* a, int64_t lda, const void* b, int6
   return hipGetLastError();
 }
 
+namespace {
+
+// The product over columns n0.. of g (B and C advanced by n0 columns).
+GemmArgs tail_args(const GemmArgs& g, int64_t n0) {
+  GemmArgs t = g;
+  t.N = g.N - n0;
+  const int64_t es = g.in_type == DType::BF16 ? 2 : 4;
+  for (int p = 0; p < g.nprob; ++p) {
+    t.prob[p].b = static_cast<const unsigned char*>(g.prob[p].b) + (g.b_kmajor ? n0 * g.ldb : n0) * es;
+    t.prob[p].c = static_cast<float*>(g.prob[p].c) + (g.c_trans ? n0 * g.ldc : n0);
+  }
+  return t;
+}
+
+// Whole rounds and a tail. A Store/Accum product whose tiles leave a last
+// round of fewer than 192 workgroups (for 256 CUs) runs its whole rounds as
+// one launch over the first n0 columns and the remaining columns as a second
+// product, which then splits K over the CUs (plan_split): the tail costs a
+// fraction of a round instead of a whole one. Applies when the whole rounds
+// end on a column-tile boundary (256·rounds divisible by the M-tiles, e.g.
+// grad_W computed transposed with its 16 M-tiles at H = 4096). Returns n0, or
+// 0 when the product runs as one launch.
+int64_t tail_columns(const GemmArgs& g) {
+  if (g.epi == GemmEpilogue::Logits || g.split_k > 1 || g.M <= 0 || g.N <= 0) return 0;
+  const int64_t Mv = ((g.M + kTile - 1) / kTile) * g.nprob;
+  const int64_t Nt = (g.N + kTile - 1) / kTile;
+  const int64_t T = Mv * Nt, q = T / 256, r = T % 256;
+  if (q < 1 || r == 0 || r >= 192 || (256 * q) % Mv != 0) return 0;
+  const int64_t n0t = 256 * q / Mv;
+  if (n0t >= Nt) return 0;
+  // only when the tail does split K (else it would cost a whole round anyway)
+  return plan_split(tail_args(g, n0t * kTile)).splits > 1 ? n0t * kTile : 0;
+}
+
+}  // namespace
+
 int64_t gemm_split_bytes(const GemmArgs& g) {
-  const SplitPlan sp = plan_split(g);
+  const int64_t n0 = tail_columns(g);
+  const SplitPlan sp = plan_split(n0 > 0 ? tail_args(g, n0) : g);
   return sp.splits > 1 ? sp.bytes : 0;
 }
 
@@ -1689,6 +1726,16 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
       (g.lg.hmax == nullptr || g.lg.hmax_ld % 2 || g.lg.hmax_ld < 4 * ((g.N + kTile - 1) / kTile)))
     return hipErrorInvalidValue;
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
+  if (g.split_ws != nullptr) {
+    const int64_t n0 = tail_columns(g);
+    if (n0 > 0) {   // whole rounds, then the tail with K split
+      GemmArgs m = g;
+      m.N = n0;
+      const hipError_t e = launch_gemm(m, stream);
+      if (e != hipSuccess) return e;
+      return launch_gemm(tail_args(g, n0), stream);
+    }
+  }
   const int64_t tiles = ((g.M + kTile - 1) / kTile) * ((g.N + kTile - 1) / kTile) * g.nprob;
   GemmArgs gr = g;
   set_share_blocks(gr);
