@@ -301,6 +301,10 @@ def vendor_gemms(torch, wl, dev, s, w, t, reps):
     hid_t = hid.t().contiguous()
     products = {
         "gemm_logits": lambda: F.linear(hid, wt),
+        # the plain product followed by one of the statistics the library's
+        # logits epilogue forms (each row's logsumexp, one more pass over the
+        # logits): a lower bound for the unfused form of that GEMM
+        "gemm_logits_then_logsumexp": lambda: torch.logsumexp(F.linear(hid, wt), dim=1),
         "gemm_grad_hidden": lambda: torch.mm(dl, wt),
         "gemm_grad_weight": lambda: torch.mm(hid_t, dl),
     }
