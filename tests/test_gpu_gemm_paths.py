@@ -9,6 +9,11 @@ shapes, against the oracle:
   second group's grad_W accumulate (the Accum epilogue through both launches
   and the split reduction), with K = 512 per group.
 
+* grad_hidden in shared raster rounds at 12 N-tiles (H = 3072: blocks of
+  5 M x 6 N tiles per XCD, bands of 20 M-tiles) with a grouped tail: BT =
+  2860 gives 24 M-tiles over the student and teacher problems, one band and
+  4 M-tiles after it.
+
 fp32 (the oracle's tolerance 1e-3 on gradients) and bf16 inputs (2e-2, the
 oracle fed the same bf16-rounded values).
 """
@@ -59,5 +64,23 @@ def test_grad_w_tail_split_accumulated_over_groups(torch_dev, dtype):
     _, n = ctx.kernel_time("gemm_logits")
     ctx.close()
     assert n == 2, f"expected two staging groups, got {n} logits launches"
+    ref = O.distillation_loss(s, w, y, Teacher.Tied(th), opts)
+    check_output(got, ref, kind=dtype)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_grad_hidden_shared_rounds_twelve_column_tiles(torch_dev, dtype):
+    torch, dev = torch_dev
+    bt, h, v = 2860, 3072, 301
+    s, th = normal((bt, h), 91), normal((bt, h), 92)
+    w = normal((v, h), 93, 0.02)   # logits spread ~1.1
+    y = uniform_labels(bt, v, 94)
+    y[::8] = -100
+    if dtype == "bf16":
+        s, th, w = bf16_round(s), bf16_round(th), bf16_round(w)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    dt = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(tdt)
+    opts = LossOptions(kd_weight=0.4, temperature=1.5, label_smoothing=0.1)
+    got = H.distillation_loss(dt(s), dt(w), torch.from_numpy(y).to(dev), Teacher.Tied(dt(th)), opts)
     ref = O.distillation_loss(s, w, y, Teacher.Tied(th), opts)
     check_output(got, ref, kind=dtype)
