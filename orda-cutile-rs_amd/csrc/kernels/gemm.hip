@@ -1674,43 +1674,65 @@ hipError_t launch_transpose_rows(const void* a, int64_t lda, const void* b, int6
 
 namespace {
 
-// The product over columns n0.. of g (B and C advanced by n0 columns).
-GemmArgs tail_args(const GemmArgs& g, int64_t n0) {
+// The part of g over columns [c0, c1) and rows [r0, r1) of C (operands and
+// C advanced to them).
+GemmArgs sub_product(const GemmArgs& g, int64_t r0, int64_t r1, int64_t c0, int64_t c1) {
   GemmArgs t = g;
-  t.N = g.N - n0;
+  t.M = r1 - r0;
+  t.N = c1 - c0;
   const int64_t es = g.in_type == DType::BF16 ? 2 : 4;
   for (int p = 0; p < g.nprob; ++p) {
-    t.prob[p].b = static_cast<const unsigned char*>(g.prob[p].b) + (g.b_kmajor ? n0 * g.ldb : n0) * es;
-    t.prob[p].c = static_cast<float*>(g.prob[p].c) + (g.c_trans ? n0 * g.ldc : n0);
+    t.prob[p].a = static_cast<const unsigned char*>(g.prob[p].a) + (g.a_kmajor ? r0 * g.lda : r0) * es;
+    t.prob[p].b = static_cast<const unsigned char*>(g.prob[p].b) + (g.b_kmajor ? c0 * g.ldb : c0) * es;
+    t.prob[p].c = static_cast<float*>(g.prob[p].c) +
+                  (g.c_trans ? c0 * g.ldc + r0 : r0 * g.ldc + c0);
   }
   return t;
 }
 
 // Whole rounds and a tail. A Store/Accum product whose tiles leave a last
 // round of fewer than 192 workgroups (for 256 CUs) runs its whole rounds as
-// one launch over the first n0 columns and the remaining columns as a second
-// product, which then splits K over the CUs (plan_split): the tail costs a
-// fraction of a round instead of a whole one. Applies when the whole rounds
-// end on a column-tile boundary (256·rounds divisible by the M-tiles, e.g.
-// grad_W computed transposed with its 16 M-tiles at H = 4096). Returns n0, or
-// 0 when the product runs as one launch.
-int64_t tail_columns(const GemmArgs& g) {
-  if (g.epi == GemmEpilogue::Logits || g.split_k > 1 || g.M <= 0 || g.N <= 0) return 0;
-  const int64_t Mv = ((g.M + kTile - 1) / kTile) * g.nprob;
-  const int64_t Nt = (g.N + kTile - 1) / kTile;
+// one launch and the rest as a second product, which then splits K over the
+// CUs (plan_split): the tail costs a fraction of a round instead of a whole
+// one. The whole rounds must end on a tile boundary: in the columns (256 x
+// rounds divisible by the M-tiles, e.g. grad_W computed transposed with its
+// 16 M-tiles at H = 4096), else in the rows of every problem (by the
+// N-tiles x problems, e.g. grad_hidden at H = 4096 and BT = 5000); and the
+// tail must split. Returns the split point (a multiple of 256) as a column
+// (cols = true) or a row, or 0 when the product runs as one launch.
+struct TailSplit {
+  int64_t at;
+  bool cols;
+};
+TailSplit plan_tail(const GemmArgs& g) {
+  const TailSplit none{0, false};
+  if (g.epi == GemmEpilogue::Logits || g.split_k > 1 || g.M <= 0 || g.N <= 0) return none;
+  const int64_t Mt = (g.M + kTile - 1) / kTile, Nt = (g.N + kTile - 1) / kTile;
+  const int64_t Mv = Mt * g.nprob;
   const int64_t T = Mv * Nt, q = T / 256, r = T % 256;
-  if (q < 1 || r == 0 || r >= 192 || (256 * q) % Mv != 0) return 0;
-  const int64_t n0t = 256 * q / Mv;
-  if (n0t >= Nt) return 0;
-  // only when the tail does split K (else it would cost a whole round anyway)
-  return plan_split(tail_args(g, n0t * kTile)).splits > 1 ? n0t * kTile : 0;
+  if (q < 1 || r == 0 || r >= 192) return none;
+  if ((256 * q) % Mv == 0) {
+    const int64_t n0 = 256 * q / Mv * kTile;
+    if (n0 < g.N && plan_split(sub_product(g, 0, g.M, n0, g.N)).splits > 1) return {n0, true};
+  }
+  if ((256 * q) % (Nt * g.nprob) == 0) {
+    const int64_t m0 = 256 * q / (Nt * g.nprob) * kTile;
+    if (m0 < g.M && plan_split(sub_product(g, m0, g.M, 0, g.N)).splits > 1) return {m0, false};
+  }
+  return none;
+}
+
+// The two launches of a tail split: whole rounds first, then the tail.
+GemmArgs tail_part(const GemmArgs& g, const TailSplit& ts, bool tail) {
+  if (ts.cols) return tail ? sub_product(g, 0, g.M, ts.at, g.N) : sub_product(g, 0, g.M, 0, ts.at);
+  return tail ? sub_product(g, ts.at, g.M, 0, g.N) : sub_product(g, 0, ts.at, 0, g.N);
 }
 
 }  // namespace
 
 int64_t gemm_split_bytes(const GemmArgs& g) {
-  const int64_t n0 = tail_columns(g);
-  const SplitPlan sp = plan_split(n0 > 0 ? tail_args(g, n0) : g);
+  const TailSplit ts = plan_tail(g);
+  const SplitPlan sp = plan_split(ts.at > 0 ? tail_part(g, ts, true) : g);
   return sp.splits > 1 ? sp.bytes : 0;
 }
 
@@ -1727,13 +1749,11 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
     return hipErrorInvalidValue;
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
   if (g.split_ws != nullptr) {
-    const int64_t n0 = tail_columns(g);
-    if (n0 > 0) {   // whole rounds, then the tail with K split
-      GemmArgs m = g;
-      m.N = n0;
-      const hipError_t e = launch_gemm(m, stream);
+    const TailSplit ts = plan_tail(g);
+    if (ts.at > 0) {   // whole rounds, then the tail with K split
+      const hipError_t e = launch_gemm(tail_part(g, ts, false), stream);
       if (e != hipSuccess) return e;
-      return launch_gemm(tail_args(g, n0), stream);
+      return launch_gemm(tail_part(g, ts, true), stream);
     }
   }
   const int64_t tiles = ((g.M + kTile - 1) / kTile) * ((g.N + kTile - 1) / kTile) * g.nprob;

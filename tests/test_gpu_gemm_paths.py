@@ -14,6 +14,11 @@ shapes, against the oracle:
   2860 gives 24 M-tiles over the student and teacher problems, one band and
   4 M-tiles after it.
 
+* grad_hidden as whole rounds over its first rows plus a tail of rows with
+  K split: H = 512 (2 N-tiles) and BT = 17000 give 67 M-tiles per problem,
+  268 tiles over student and teacher rows, one round over the first 16384
+  rows and a 12-tile tail (V = 320: K split in two).
+
 fp32 (the oracle's tolerance 1e-3 on gradients) and bf16 inputs (2e-2, the
 oracle fed the same bf16-rounded values).
 """
@@ -81,6 +86,25 @@ def test_grad_hidden_shared_rounds_twelve_column_tiles(torch_dev, dtype):
     tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
     dt = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(tdt)
     opts = LossOptions(kd_weight=0.4, temperature=1.5, label_smoothing=0.1)
+    got = H.distillation_loss(dt(s), dt(w), torch.from_numpy(y).to(dev), Teacher.Tied(dt(th)), opts)
+    ref = O.distillation_loss(s, w, y, Teacher.Tied(th), opts)
+    check_output(got, ref, kind=dtype)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_grad_hidden_tail_rows_split(torch_dev, dtype):
+    torch, dev = torch_dev
+    bt, h, v = 17000, 512, 320
+    s, th = normal((bt, h), 101), normal((bt, h), 102)
+    w = normal((v, h), 103, 0.05)
+    y = uniform_labels(bt, v, 104)
+    y[::10] = -100
+    if dtype == "bf16":
+        s, th, w = bf16_round(s), bf16_round(th), bf16_round(w)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    dt = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(tdt)
+    opts = LossOptions(kd_weight=0.4, temperature=2.0, label_smoothing=0.1,
+                       chunk_size=ChunkSize.Fixed(bt))
     got = H.distillation_loss(dt(s), dt(w), torch.from_numpy(y).to(dev), Teacher.Tied(dt(th)), opts)
     ref = O.distillation_loss(s, w, y, Teacher.Tied(th), opts)
     check_output(got, ref, kind=dtype)
