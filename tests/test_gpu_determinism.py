@@ -7,7 +7,8 @@ floating-point atomics.
 
 The cases reach the paths whose reductions could differ: split K in both
 backward GEMMs (small shapes), grad_hidden in shared raster rounds with a
-grouped tail, the paired bf16 row pass with INT8 grad_W (deterministic and
+grouped tail, grad_hidden as one whole round plus a tail of rows with K
+split, the paired bf16 row pass with INT8 grad_W (deterministic and
 stochastic rounding), several staging groups accumulating into grad_W, a
 Separate teacher, Precomputed logits through the chunked fp32 row pass, and
 the fp32 inputs under Profile.Fast.
@@ -45,6 +46,10 @@ CASES = {
                          dict(kd_weight=0.4, temperature=1.5)),
     "tied-bf16-shared-rounds": ("tied", "bf16", 8492, 800, 800, 301, 0.04,
                                 dict(kd_weight=0.5, temperature=1.5, label_smoothing=0.1)),
+    # grad_hidden: 20 x 16 tiles, one whole round of 256 and a tail of rows
+    # 4096-4999 with K split
+    "tied-bf16-tail-split": ("tied", "bf16", 5000, 4096, 4096, 1024, 0.04,
+                             dict(kd_weight=0.4, temperature=1.5)),
     "separate-bf16": ("separate", "bf16", 500, 256, 384, 20000, 0.05,
                       dict(kd_weight=0.5, temperature=2.0, teacher_ce_weight=0.3)),
     "precomputed-f32-chunked": ("precomputed", "f32", 300, 64, 0, 120000, 0.1,
