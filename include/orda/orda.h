@@ -67,21 +67,23 @@ typedef struct {
 /* KernelConfig (src/config.rs:45-63). Option<T> fields carry has_* flags.
  * The reference's CPU path ignores the tuning fields (src/config.rs:3-7); on
  * this GPU path they act as follows:
- *   fast_math       (Profile::Fast) fp32 inputs are rounded to bf16 once and
- *                   run the bf16 MFMA pipeline with bf16 logits storage
- *                   (upstream's half-precision logits, docs/BLOCKERS.md:
- *                   129-131); per-row logs and divisions use the hardware
- *                   approximations. Gradients match the reference on the
- *                   bf16-rounded inputs to the bf16 tolerance.
+ *   fast_math       (Profile::Fast, src/config.rs:37-40,93-103) the per-row
+ *                   logs and divisions of the row pass use the hardware
+ *                   approximations (v_log_f32, v_rcp_f32 then a multiply);
+ *                   exponentials are the hardware exp2 in every profile.
+ *                   Inputs keep their dtype: fp32 inputs run the fp32 GEMMs,
+ *                   and the result matches the reference to the fp32
+ *                   tolerance.
  *   profile         ORDA_PROFILE_DEBUG (the precise preset): bf16 inputs are
  *                   widened to fp32 and run the fp32 pipeline (fp32 logits,
  *                   fp32 GEMMs), matching the reference to the fp32
  *                   tolerance. Set by orda_kernel_config_from_profile; the
  *                   reference records the preset only through the fields
  *                   it sets, so this one field is new.
- *   online_softmax  row statistics of logits the GEMM did not produce
- *                   (Precomputed teacher logits, the chunk-launcher slot) in
- *                   one online pass instead of a max pass and a sum pass.
+ *   online_softmax  row statistics of Precomputed teacher logits (logits
+ *                   the GEMM did not produce) in one online pass instead of
+ *                   a max pass and a sum pass. (The chunk-launcher slot takes
+ *                   no KernelConfig; it always uses the two passes.)
  *   fp32_grad_weight_accumulation, max_fused_size: accepted and validated;
  *                   grad_W always accumulates in fp32 (the reference's
  *                   output is f32) and the tile widths are fixed. */
@@ -249,7 +251,11 @@ int32_t orda_kl_ce_on_logits_chunk(orda_ctx *ctx, const orda_tensor *logits_chun
  * required; every tensor and the targets must be on the device; n_rows is at
  * most 32768 (ORDA_ERR_INVALID beyond). The per-row scratch is one 1.75 MiB
  * array per GPU held until the process ends and shared by every call on that
- * GPU: calls that overlap on one GPU race. */
+ * GPU: calls that overlap on one GPU race. On a stream under HIP graph
+ * capture (the context's stream, orda_ctx_set_stream) the call records its
+ * kernels and returns without waiting or timing; every replay of the graph
+ * uses the same per-GPU scratch, so a replay overlapping another call or
+ * replay on that GPU races too. Otherwise the call is synchronous. */
 int32_t orda_kl_ce_on_logits_chunk_noalloc(orda_ctx *ctx, const orda_tensor *logits_chunk,
                                            const int32_t *targets, int32_t targets_location,
                                            int64_t n_rows, float inv_t, float kl_grad_scale,

@@ -381,12 +381,12 @@ void config_validate(const orda_kernel_config& k) {
     fail(ORDA_ERR_INVALID, "unknown profile %d", k.profile);
 }
 
-// The dtype the GEMMs and the logits run in: the inputs' own, except fp32
-// inputs under fast_math (bf16, half-precision storage) and bf16 inputs
-// under the Debug profile (fp32, the precise preset).
+// The dtype the GEMMs and the logits run in: the inputs' own, except bf16
+// inputs under the Debug profile (fp32, the precise preset). fast_math
+// (Profile::Fast) changes only how the row pass forms its per-row logs and
+// divisions (src/config.rs:37-40,93-103), never the inputs.
 DType compute_dtype(const orda_kernel_config& k, DType in) {
   if (k.profile == ORDA_PROFILE_DEBUG) return DType::F32;
-  if (k.fast_math && in == DType::F32) return DType::BF16;
   return in;
 }
 
@@ -470,11 +470,11 @@ int64_t staged_bytes_per_row(const LossPlan& P, const Inputs& in) {
   int64_t b = blocks * logits_pitch(P.v) *
               (orda::dtype_size(lt) + (lt == P.dt ? 0 : orda::dtype_size(P.dt)));
   b += 2 * nst * 16 + 2 * 4;   // statistics, label logits
-  if (paired) b += nst * 4 + 16;   // cross partials, row constants
+  if (paired) b += nst * 8 + 16;   // KL partials, row constants
   if (lt == orda::DType::BF16) b += 4 * nst * 4;   // half-tile maxima of both rows
   // fp32 logits: row constants and the gradient blocks' KL sums
   if (!paired && lt == orda::DType::F32)
-    b += 16 + (P.kd > 0.f ? orda::row_pass_kl_blocks(P.v) * 8 : 0);
+    b += 16 + (P.kd > 0.f ? orda::row_pass_kl_blocks(P.v) * 16 : 0);
   // hcat: the hidden rows transposed for grad_W ([h_s; h_t] with a Tied
   // teacher and teacher CE; else the student's, then the Separate teacher's).
   b += (P.mode == ORDA_TEACHER_TIED && P.w_t > 0.f ? 2 * P.h
@@ -532,7 +532,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   // the K-major A operand of grad_Wᵀ.
   const int64_t ldh_cat = round64(tied_tce ? 2 * cap : cap);   // rows on 128-byte lines
   void* hcat = ws(c, "hcat", std::max(h, P.has_gwt ? P.ht : int64_t{0}) * ldh_cat * es);
-  float* cross = paired ? static_cast<float*>(ws(c, "cross", cap * nst * 4)) : nullptr;
+  float2* cross = paired ? static_cast<float2*>(ws(c, "cross", cap * nst * 8)) : nullptr;
   // bf16 logits are stored relative to their half-tile maxima: per row
   // pair and 128-column half, the student's and the teacher's maximum side
   // by side (LogitStatsArgs::hmax).
@@ -542,8 +542,8 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   // logits), and for fp32 logits with a KL term the per-block KL sums.
   const bool f32_rows = !paired && lt == DType::F32;
   float4* rconst = paired || f32_rows ? static_cast<float4*>(ws(c, "rconst", cap * 16)) : nullptr;
-  float2* klpart = f32_rows && P.kd > 0.f
-                       ? static_cast<float2*>(ws(c, "klpart", cap * row_pass_kl_blocks(v) * 8))
+  float4* klpart = f32_rows && P.kd > 0.f
+                       ? static_cast<float4*>(ws(c, "klpart", cap * row_pass_kl_blocks(v) * 16))
                        : nullptr;
   const float inv_t = 1.0f / P.T;
 
@@ -958,7 +958,7 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
       check_labels_host(host_labels(c, labels, n_labels, lab_loc), v, o->ignore_index);
     throw;
   }
-  // ---- compute dtype (KernelConfig::fast_math, Profile::Debug)
+  // ---- compute dtype (Profile::Debug)
   {
     const DType ct = compute_dtype(o->config, P.dt);
     if (ct != P.dt) {
@@ -1164,6 +1164,23 @@ void kl_ce_slot(orda_ctx* c, const orda_tensor* logits_chunk, const int32_t* tar
       fail(ORDA_ERR_INVALID, "the no-allocation entry point takes device targets only");
   }
   hip_check(hipSetDevice(c->device), "hipSetDevice");
+  // Under HIP graph capture (the no-allocation form only: every tensor is on
+  // the device, so nothing is copied back) the call records its kernels and
+  // returns without waiting: a synchronize would invalidate the capture.
+  // Per-kernel timing is skipped then too (its events would be replayed
+  // with the graph, not read).
+  bool capturing = false;
+  if (sc) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hip_check(hipStreamIsCapturing(c->stream, &cs), "hipStreamIsCapturing");
+    capturing = cs != hipStreamCaptureStatusNone;
+  }
+  auto launch = [&](int kind, auto&& f) {
+    if (capturing)
+      hip_check(f(), "kernel launch");
+    else
+      timed(c, kind, f);
+  };
   DMat L;
   if (logits_chunk->location == ORDA_DEVICE) {
     L.p = logits_chunk->data;
@@ -1222,7 +1239,7 @@ void kl_ce_slot(orda_ctx* c, const orda_tensor* logits_chunk, const int32_t* tar
     r.labels = lab;
     r.ignore_index = ignore_index;
     r.inv_t = inv_t;
-    timed(c, ORDA_KERNEL_OTHER, [&] { return launch_row_stats(r, c->stream); });
+    launch(ORDA_KERNEL_OTHER, [&] { return launch_row_stats(r, c->stream); });
   }
   RowPassArgs a{};
   a.ltype = L.t;
@@ -1257,11 +1274,12 @@ void kl_ce_slot(orda_ctx* c, const orda_tensor* logits_chunk, const int32_t* tar
   a.t_sq = t_sq;
   a.inv_t = inv_t;
   a.student_only = student_only != 0;
-  timed(c, ORDA_KERNEL_ROW_PASS, [&] { return launch_row_pass(a, c->stream); });
+  launch(ORDA_KERNEL_ROW_PASS, [&] { return launch_row_pass(a, c->stream); });
   download(c, gk);
   download(c, gc);
   download(c, kr);
   download(c, cl);
+  if (capturing) return;
   hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
   collect_timing(c);
 }

@@ -41,15 +41,21 @@
 // from the fp32 accumulators, plus the fp32 logit at the row's label, so the
 // row pass reads each logit exactly once. With paired rows (student and
 // teacher rows interleaved in blocks of 16) it also writes the tile's KL
-// cross term Σ e^((t-max_t)/T)·(t - s), so that every loss term comes from
-// fp32 accumulators and the stored logits (then bf16) only feed the
-// gradient. Each lane stores its 4 consecutive columns directly. bf16 logits
+// KL sums Σ e^((t-max_t)/T)·((t - max_t) - (s - max_s)) and
+// Σ (e^((s-max_s)/T) - e^((t-max_t)/T)), each element's terms taken
+// relative to its own row's maximum and its difference formed before it is
+// summed (with log1p of the second over Σe^((t-max_t)/T), the row pass gets
+// lse_s^T - lse_t^T without the cancellation of two separately rounded
+// sums, and a constant offset between the rows cancels element by element),
+// so that every loss term comes from fp32 accumulators and the stored
+// logits (then bf16) only feed the gradient. Each lane stores its 4 consecutive columns directly. bf16 logits
 // are stored relative to the maximum of their 128-column half tile, in log2
 // units, with those maxima beside the statistics: their rounding error then
 // follows their distance below the maximum, not their magnitude.
 #include <float.h>
 #include <math.h>
 
+#include "kl_sums.h"
 #include "orda_kernels.h"
 
 namespace orda {
@@ -1108,7 +1114,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
     LT* C = static_cast<LT*>(pr.c);
     int64_t* lab = reinterpret_cast<int64_t*>(epi);                      // [256]
     float4* part = reinterpret_cast<float4*>(epi + 2048);                // [2][256]
-    float* xpart = reinterpret_cast<float*>(epi + 10240);                // [2][256]
+    float2* xpart = reinterpret_cast<float2*>(epi + 10240);              // [2][256]
     const int64_t prs = g.lg.pair_rows;
     // Tile row rl as (output row, teacher?, valid): stats / xy / C row index.
     auto out_row = [&](int rl, bool& teacher, bool& valid) -> int64_t {
@@ -1307,8 +1313,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         }
         ms = quad_max(ms);
         mt = quad_max(mt);
-        const float o1s = -ms * kLog2e, oTs = -ms * it2;
-        const float o1t = -mt * kLog2e, oTt = -mt * it2;
+        const float o1s = -ms * kLog2e, o1t = -mt * kLog2e;
         const bool hit = yl >= 0 && (yl & 12) == 0;
         float xys = 0.f, xyt = 0.f;   // the label's fp32 logits, before as/at hold t
         if constexpr (kRel) {
@@ -1317,49 +1322,48 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
             xyt = pick(at, yl);
           }
         }
-        float d1s = 0.f, dTs = 0.f, sxs = 0.f, d1t = 0.f, dTt = 0.f, sxt = 0.f, cx = 0.f;
+        // Per element pair, in log2 units relative to the rows' own half
+        // maxima: ts, tt (the stored values), e^((x-m)/T) = 2^(t/T). The KL
+        // sums take (tt - ts) and (aTs - aTt), so a constant offset between
+        // the two rows cancels in each element; Σ aTs = dd + Σ aTt.
+        float d1s = 0.f, sxs = 0.f, d1t = 0.f, dTt = 0.f, sxt = 0.f, cx = 0.f, dd = 0.f;
 #pragma unroll
         for (int j = 0; j < kFrag; ++j) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float xs = as[j][e], xt = at[j][e];
-            float a1s, aTs, a1t, aTt;
+            const float ts = fmaf(xs, kLog2e, o1s), tt = fmaf(xt, kLog2e, o1t);
+            const float a1s = __builtin_amdgcn_exp2f(ts);
+            const float aTs = __builtin_amdgcn_exp2f(ts * inv_t);
+            const float a1t = __builtin_amdgcn_exp2f(tt);
+            const float aTt = __builtin_amdgcn_exp2f(tt * inv_t);
             if constexpr (kRel) {
-              const float ts = fmaf(xs, kLog2e, o1s), tt = fmaf(xt, kLog2e, o1t);
-              a1s = __builtin_amdgcn_exp2f(ts);
-              aTs = __builtin_amdgcn_exp2f(ts * inv_t);
-              a1t = __builtin_amdgcn_exp2f(tt);
-              aTt = __builtin_amdgcn_exp2f(tt * inv_t);
               as[j][e] = ts;
               at[j][e] = tt;
-            } else {
-              a1s = __builtin_amdgcn_exp2f(fmaf(xs, kLog2e, o1s));
-              aTs = __builtin_amdgcn_exp2f(fmaf(xs, it2, oTs));
-              a1t = __builtin_amdgcn_exp2f(fmaf(xt, kLog2e, o1t));
-              aTt = __builtin_amdgcn_exp2f(fmaf(xt, it2, oTt));
             }
             if (kFull || j * 16 + e < ncol) {
               d1s += a1s;
-              dTs += aTs;
+              dd += aTs - aTt;
               sxs += xs;
               d1t += a1t;
               dTt += aTt;
               sxt += xt;
-              cx = fmaf(aTt, xt - xs, cx);
+              cx = fmaf(aTt, tt - ts, cx);
             }
           }
         }
         d1s = quad_sum(d1s);
-        dTs = quad_sum(dTs);
+        dd = quad_sum(dd);
         sxs = quad_sum(sxs);
         d1t = quad_sum(d1t);
         dTt = quad_sum(dTt);
         sxt = quad_sum(sxt);
         cx = quad_sum(cx);
+        const float dTs = dd + dTt;
         if (lgrp == 0) {
           part[wn * 256 + rs] = make_float4(ms, d1s, dTs, sxs);
           part[wn * 256 + rt] = make_float4(mt, d1t, dTt, sxt);
-          xpart[wn * 256 + rt] = cx;
+          xpart[wn * 256 + rt] = make_float2(cx, dd);
         }
         u32x4 sw[kFrag / 2], tw[kFrag / 2];
         if constexpr (kSwapStore && kFull) {
@@ -1399,18 +1403,26 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         float4 s;
         s.x = m;
         s.w = a.w + b.w;
-        float cx = 0.f;
+        float2 cx = make_float2(0.f, 0.f);
         if (m == -INFINITY) {
           s.y = 0.f;
           s.z = 0.f;
-        } else {
+        } else if (teacher) {
+          // the KL sums of the two halves relative to the tile's maxima; the
+          // student row of this pair is tile row tid - 16
+          const float4 sa = part[tid - 16], sb = part[256 + tid - 16];
+          const float ms = fmaxf(sa.x, sb.x);
+          const float2 xa = kl_rebase(xpart[tid], sa.x, a.x, sa.z, a.z, ms, m, g.lg.inv_t);
+          const float2 xb = kl_rebase(xpart[256 + tid], sb.x, b.x, sb.z, b.z, ms, m, g.lg.inv_t);
+          cx = make_float2(xa.x + xb.x, xa.y + xb.y);
+        }
+        if (m != -INFINITY) {
           const float ea = __builtin_amdgcn_exp2f((a.x - m) * kLog2e);
           const float eb = __builtin_amdgcn_exp2f((b.x - m) * kLog2e);
           const float fa = __builtin_amdgcn_exp2f((a.x - m) * it2);
           const float fb = __builtin_amdgcn_exp2f((b.x - m) * it2);
           s.y = a.y * ea + b.y * eb;
           s.z = a.z * fa + b.z * fb;
-          cx = xpart[tid] * fa + xpart[256 + tid] * fb;
         }
         g.lg.stats[orow * g.lg.stats_ld + tc.ntile] = s;
         if constexpr (kRel) {   // the two halves' maxima, beside the other block's

@@ -48,10 +48,14 @@ struct LogitStatsArgs {
   // M = 2*round16(pair_rows), read in place: student rows from prob[0].a,
   // teacher rows from pair_teacher, both with pitch lda. Student row r is
   // stored as row r of C / stats / xy, teacher row r as row pair_rows + r, and
-  //   cross[r * stats_ld + n_tile] = Σ e^((t_j - max_t)/T) · (t_j - s_j)
-  // over the tile's columns, max_t being the teacher row's tile maximum.
+  //   cross[r * stats_ld + n_tile] = {Σ e^((t_j - max_t)/T) · (t_j - s_j),
+  //                                  Σ (e^((s_j - max_t)/T) - e^((t_j - max_t)/T))}
+  // over the tile's columns, max_t being the teacher row's tile maximum; the
+  // second sum forms each element's difference before adding it (NaN where
+  // the student's maximum exceeds the teacher's by more than 64·T·ln 2 in a
+  // half tile: the row pass then uses the two rows' own sums).
   int64_t pair_rows;
-  float* cross;
+  float2* cross;
   const void* pair_teacher;
   // bf16 logits (required then): each logit is stored relative to the
   // maximum m of its 128-column half tile k (k = 2*n_tile + h), in log2
@@ -141,17 +145,17 @@ struct RowPassArgs {
   float* row_nll_s;        // [n_rows] outputs (never null)
   float* row_nll_t;
   float* row_kl;           // KL_row * T^2 (T^2 in f32), 0 when ignored
-  // Per-tile KL cross partials of the teacher rows from a paired logits GEMM
+  // Per-tile KL partials of the teacher rows from a paired logits GEMM
   // (LogitStatsArgs::cross, same pitch as the stats), or null: then the
-  // pass accumulates the cross term from the logits it reads.
-  const float* cross;
+  // pass accumulates the KL sums from the logits it reads.
+  const float2* cross;
   // Scratch of n_rows float4 for the chunked passes: over paired bf16
   // logits (cross set, gradient in place), and over fp32 logits (cross
   // null); may be null (then the row-per-workgroup pass runs).
   float4* row_consts;
   // fp32 chunked pass with a KL term: n_rows * row_pass_kl_blocks(v)
-  // float2, each column block's share of the row's KL sums.
-  float2* kl_part;
+  // float4, each column block's share of the row's three KL sums.
+  float4* kl_part;
   // bf16 logits stored relative to their half-tile maxima by the logits
   // GEMM (LogitStatsArgs::hmax): half k of row r has its maximum at
   // hmax_s[r*hmax_ld + 2*k] (student) and hmax_t[r*hmax_ld + 2*k]
@@ -181,7 +185,7 @@ struct RowPassArgs {
 };
 
 hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t stream);
-// float2 entries per row of RowPassArgs::kl_part (ceil(v/512)).
+// float4 entries per row of RowPassArgs::kl_part (ceil(v/512)).
 int64_t row_pass_kl_blocks(int64_t v);
 
 // Per-row statistics of rows that were not produced by the GEMM (Precomputed

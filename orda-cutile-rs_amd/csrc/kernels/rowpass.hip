@@ -9,7 +9,12 @@
 //                                           merge api.rs:335-344)
 //   teacher grad = w_t·((p_t − α/V) − [j=y](1−α))   (api.rs:325-333)
 // overwriting both rows in place, and the KL term
-//   KL_row = Σ p_t^T (x_t − x_s)/T + (lse_s^T − lse_t^T)·Σ p_t^T.
+//   KL_row = Σ p_t^T (x_t − x_s)/T + lse_s^T − lse_t^T,
+// where lse_s^T − lse_t^T = log(Σ e^(x_s/T) / Σ e^(x_t/T)) is formed as
+// log1p(D/S) from a sum D of per-element differences of the two rows'
+// terms (each difference rounded once) over the teacher's sum S: for nearly
+// equal rows, two separately rounded sums of V terms would leave an error of
+// a few 1e-7 in a KL that may itself be that small.
 // Three forms:
 //   * paired bf16 logits: the KL cross sum comes per tile from the logits
 //     GEMM's fp32 accumulators (the stored logits only feed the gradient);
@@ -23,6 +28,7 @@
 // folded into one FMA per element.
 #include <math.h>
 
+#include "kl_sums.h"
 #include "orda_kernels.h"
 
 namespace orda {
@@ -74,27 +80,6 @@ __device__ __forceinline__ Stat shfl_xor_stat(Stat s, int o) {
   r.dT = __shfl_xor(s.dT, o);
   r.sx = __shfl_xor(s.sx, o);
   return r;
-}
-
-// merge() of teacher statistics that also carries x, a sum of terms
-// c·e^((x_j - m)/T) relative to the statistics' maximum m (the KL cross
-// partials): rescaled by the same factors as dT.
-__device__ __forceinline__ void merge_cross(Stat& a, float& ax, Stat b, float bx, float it2) {
-  const float m = fmaxf(a.m, b.m);
-  a.sx += b.sx;
-  if (m == -INFINITY) {
-    a.m = m;
-    a.d1 = 0.f;
-    a.dT = 0.f;
-    ax = 0.f;
-    return;
-  }
-  const float fa = __builtin_amdgcn_exp2f((a.m - m) * it2), fb = __builtin_amdgcn_exp2f((b.m - m) * it2);
-  a.d1 = a.d1 * __builtin_amdgcn_exp2f((a.m - m) * kLog2e) +
-         b.d1 * __builtin_amdgcn_exp2f((b.m - m) * kLog2e);
-  a.dT = a.dT * fa + b.dT * fb;
-  ax = ax * fa + bx * fb;
-  a.m = m;
 }
 
 // Block-wide merge of per-thread partial stats; every thread gets the result.
@@ -175,14 +160,30 @@ struct Vec<__bf16> {
   }
 };
 
-// lse_s^T - lse_t^T of two rows from their merged statistics, as
-// (m_s - m_t)/T + log(dT_s / dT_t): the maxima are logits, so their
-// difference is exact when they are close, and the log of a ratio near 1
-// keeps the small KL of nearly equal rows (where lse_s^T and lse_t^T agree
-// to many digits) from being swamped by the rounding of two O(|lse|) logs.
-__device__ __forceinline__ float lse_t_diff(const Stat& s, const Stat& t, float inv_t,
-                                            bool fast = false) {
-  return (s.m - t.m) * inv_t + rlog(rdiv(s.dT, t.dT, fast), fast);
+// KL_row (without T²) of a row pair from its merged statistics s, t and the
+// paired GEMM's merged KL sums x (kl_sums.h): the mean of the centred
+// difference under p_t^T plus log1p(x.y / t.dT) = lse_s^T - lse_t^T (with
+// the shift between the two maxima taken out of both). Precise log1p and
+// division of the sums in every profile (they carry the small-KL
+// precision; one per row). Should x.y / t.dT not lie in (-1, inf), the two
+// rows' own sums instead.
+__device__ __forceinline__ float kl_paired(float2 x, const Stat& s, const Stat& t, float inv_t,
+                                           bool fast) {
+  const float z = x.y / t.dT;
+  const float lr = isfinite(z) && z > -1.f ? log1pf(z) : rlog(rdiv(s.dT, t.dT, fast), fast);
+  return rdiv(x.x, t.dT, fast) * (kLn2 * inv_t) + lr;
+}
+
+// KL_row (without T²) from the sums of a pass that forms p_s^T and p_t^T
+// itself as 2^(x·log2(e)/T − o) (scaled by the same factor g in both):
+// cross = g·Σ p_t^T (x_t − x_s), sum_t = g·Σ p_t^T, sum_d = g·Σ (p_s^T − p_t^T)
+// (each difference formed before it is summed), and do = o_s − o_t, the
+// difference of the two exponent offsets as the pass used them (log2
+// units). Exact in those terms: KL = E_t[x_t − x_s]/T + (lse_s^T − lse_t^T),
+// with lse_s^T − lse_t^T = do·ln2 + log(Σ p_s^T / Σ p_t^T).
+__device__ __forceinline__ float kl_from_sums(float cross, float sum_t, float sum_d, float d_off,
+                                              float inv_t, bool fast) {
+  return rdiv(cross, sum_t, fast) * inv_t + d_off * kLn2 + log1pf(sum_d / sum_t);
 }
 
 // nll of cross_entropy.rs:46-56 from merged stats, in f64.
@@ -239,7 +240,7 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(RowPassArgs a) {
 
   using VT = Vec<LT>;
   constexpr int NV = VT::N;
-  float cross = 0.f, sum_pt = 0.f;
+  float cross = 0.f, sum_pt = 0.f, sum_d = 0.f;
   const int64_t vpad = (a.v + NV - 1) / NV * NV;
   // Rows are read where they are, at any pitch: 16-byte vectors where the
   // row is 16-byte aligned and the vector lies inside the row, single
@@ -273,9 +274,11 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(RowPassArgs a) {
         if (do_kl) {
           const float ps = __builtin_amdgcn_exp2f(fmaf(xs[i], it2, -oTs));
           const float pt = __builtin_amdgcn_exp2f(fmaf(xt[i], it2, -oTt));
-          gkv = gsc * (ps - pt);
+          const float d = ps - pt;
+          gkv = gsc * d;
           cross = fmaf(pt, xt[i] - xs[i], cross);
           sum_pt += pt;
+          sum_d += d;
         }
         if (do_tgrad) {
           const float q = __builtin_amdgcn_exp2f(fmaf(xt[i], kLog2e, -o1t));
@@ -316,6 +319,7 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(RowPassArgs a) {
   if (do_kl) {
     cross = block_sum(cross, ssum);
     sum_pt = block_sum(sum_pt, ssum);
+    sum_d = block_sum(sum_d, ssum);
   }
   if (tid == 0) {
     const float xy_s = ignored ? 0.f : a.xy_s[r];
@@ -323,7 +327,7 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(RowPassArgs a) {
     float kl_row = 0.f;
     if (do_kl && !ignored) {
       const float t_sq = SPLIT ? a.t_sq : T * T;   // kl.rs:86
-      kl_row = (cross * inv_t + lse_t_diff(ss, st, inv_t) * sum_pt) * t_sq;
+      kl_row = kl_from_sums(cross, sum_pt, sum_d, oTs - oTt, inv_t, false) * t_sq;
     }
     double nll_t = 0.0;
     const bool tce = SPLIT ? (!a.student_only && has_t) : (a.teacher_ce && has_t);
@@ -446,16 +450,22 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
   const Stat ss = load_row_stats(a.stats_s + r * a.stats_ld, a.stats_tiles, it2, sstat);
   Stat st{-INFINITY, 0.f, 0.f, 0.f};
   if (HT || a.teacher_ce) st = load_row_stats(a.stats_t + r * a.stats_ld, a.stats_tiles_t, it2, sstat);
-  // KL cross term from a paired logits GEMM: Σ_tiles e^((m_tile - M_t)/T)·x_tile
-  // = Σ_j e^((t_j - M_t)/T)·(t_j - s_j), formed from the fp32 accumulators.
-  float xc = 0.f;
+  // KL sums from a paired logits GEMM (kl_sums.h), each tile's taken to
+  // the row's merged maxima and added.
+  float2 xc = make_float2(0.f, 0.f);
   if (KL && a.cross != nullptr) {
+    const float4* srow_s = a.stats_s + r * a.stats_ld;
     const float4* srow_t = a.stats_t + r * a.stats_ld;
-    const float* crow = a.cross + r * a.stats_ld;
-    float part = 0.f;
-    for (int64_t t = tid; t < a.stats_tiles_t; t += kThreads)
-      part = fmaf(crow[t], __builtin_amdgcn_exp2f((srow_t[t].x - st.m) * it2), part);
-    xc = block_sum(part, ssum);
+    const float2* crow = a.cross + r * a.stats_ld;
+    float px = 0.f, pd = 0.f;
+    for (int64_t t = tid; t < a.stats_tiles_t; t += kThreads) {
+      const float4 vs = srow_s[t], vt = srow_t[t];
+      const float2 c = kl_rebase(crow[t], vs.x, vt.x, vs.z, vt.z, ss.m, st.m, inv_t);
+      px += c.x;
+      pd += c.y;
+    }
+    xc.x = block_sum(px, ssum);
+    xc.y = block_sum(pd, ssum);
   }
 
   const double alpha = static_cast<double>(a.label_smoothing);
@@ -486,14 +496,16 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
     return float4{fmaf(hs, kLog2e, ca), fmaf(hs, it2, cb), fmaf(ht, it2, cc), fmaf(ht, kLog2e, cd)};
   };
 
-  float cross = 0.f, sum_c = 0.f;
+  float cross = 0.f, sum_c = 0.f, sum_d = 0.f;
   // Gradient of one element pair, without the label term.
-  auto elem = [&](float xs, float xt, const float4& o, float& g, float& gt, float& cx, float& c) {
+  auto elem = [&](float xs, float xt, const float4& o, float& g, float& gt, float& cx, float& c,
+                  float& d) {
     g = fmaf(sgn, __builtin_amdgcn_exp2f(fmaf(xs, e1s, o.x)), k0);
     if (KL) {
       const float b = __builtin_amdgcn_exp2f(fmaf(xs, eTs, o.y));
       c = __builtin_amdgcn_exp2f(fmaf(xt, eTt, o.z));
-      g += b - c;
+      d = b - c;
+      g += d;
       cx = c * (xt - xs);
     }
     if (TG) gt = __builtin_amdgcn_exp2f(fmaf(xt, e1t, o.w)) + kt0;
@@ -505,11 +517,12 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const bool valid = full || j0 + i < v;
-      float gi = 0.f, ti = 0.f, cx = 0.f, c = 0.f;
-      elem(xs[i], xt[i], o, gi, ti, cx, c);
+      float gi = 0.f, ti = 0.f, cx = 0.f, c = 0.f, d = 0.f;
+      elem(xs[i], xt[i], o, gi, ti, cx, c, d);
       if (KL) {
         cross += valid ? cx : 0.f;
         sum_c += valid ? c : 0.f;
+        sum_d += valid ? d : 0.f;
       }
       g[i] = valid ? gi : 0.f;
       gt[i] = valid ? ti : 0.f;
@@ -577,24 +590,24 @@ __global__ __launch_bounds__(kThreads) void row_pass_fused_kernel(RowPassArgs a)
   // The label column: its owner (the thread that wrote it, so in program
   // order) rewrites it with the −(1−α)·w term included.
   if (owner) {
-    float gy = 0.f, ty = 0.f, cx = 0.f, c = 0.f;
-    elem(xs_y, xt_y, offs(hr.s(y), hr.t(y)), gy, ty, cx, c);
+    float gy = 0.f, ty = 0.f, cx = 0.f, c = 0.f, d = 0.f;
+    elem(xs_y, xt_y, offs(hr.s(y), hr.t(y)), gy, ty, cx, c, d);
     gsrow[y] = static_cast<GT>(gy - ky);
     if (TG) gtrow[y] = static_cast<GT>(ty - kyt);
   }
 
-  if (KL) {
+  if (KL && a.cross == nullptr) {
     cross = block_sum(cross, ssum);
     sum_c = block_sum(sum_c, ssum);
+    sum_d = block_sum(sum_d, ssum);
   }
   if (tid == 0) {
     a.row_nll_s[r] = static_cast<float>(row_nll(ss, a.xy_s[r], alpha, v));
     float kl_row = 0.f;
     if (KL && a.cross != nullptr)
-      kl_row = (rdiv(xc, st.dT, fm) * inv_t + lse_t_diff(ss, st, inv_t, fm)) * (T * T);
-    else if (KL)
-      kl_row = (rdiv(cross, gsc, fm) * inv_t + lse_t_diff(ss, st, inv_t, fm) * rdiv(sum_c, gsc, fm)) *
-               (T * T);
+      kl_row = kl_paired(xc, ss, st, inv_t, fm) * (T * T);
+    else if (KL)   // offsets as used: p_s^T·kd·T = 2^(x·eTs + cb + ...), p_t^T likewise with cc
+      kl_row = kl_from_sums(cross, sum_c, sum_d, cc - cb, inv_t, fm) * (T * T);
     a.row_kl[r] = kl_row;
     a.row_nll_t[r] = a.teacher_ce ? static_cast<float>(row_nll(st, a.xy_t[r], alpha, v)) : 0.f;
   }
@@ -634,40 +647,84 @@ __global__ __launch_bounds__(kThreads) void row_consts_kernel(RowPassArgs a) {
   const float inv_t = rdiv(1.0f, T, fm);
   const float it2 = inv_t * kLog2e;
   Stat ss{-INFINITY, 0.f, 0.f, 0.f}, st{-INFINITY, 0.f, 0.f, 0.f};
-  float xc = 0.f;
+  float2 xc = make_float2(0.f, 0.f);
   const float4* rs = a.stats_s + r * a.stats_ld;
   const bool teacher = KL || TG || a.teacher_ce;
   const float4* rt = a.stats_t + r * a.stats_ld;
   // Without a paired GEMM's cross partials (fp32 logits), the KL cross sums
   // come from row_grad_f32_kernel's blocks instead.
   const bool xk = KL && a.cross != nullptr;
-  const float* rc = xk ? a.cross + r * a.stats_ld : nullptr;
+  const float2* rc = xk ? a.cross + r * a.stats_ld : nullptr;
   const int64_t nt = a.stats_tiles > a.stats_tiles_t ? a.stats_tiles : a.stats_tiles_t;
-  // kPer entries per lane in flight before any merge; a missing entry is
-  // {-inf, 0, 0, 0}, which merges as nothing.
+  // The row's two maxima first, then every tile's entries taken to them once
+  // and added (no pairwise merges). kPer entries per lane are loaded at a
+  // time; a missing entry is {-inf, 0, 0, 0}, which adds nothing. Rows of up
+  // to 64·kPer tiles (V <= 131072) keep their entries in registers between
+  // the two steps; longer rows read them again.
   constexpr int kPer = 8;
   const float4 none = make_float4(-INFINITY, 0.f, 0.f, 0.f);
-  for (int64_t t0 = 0; t0 < nt; t0 += 64 * kPer) {
-    float4 vs[kPer], vt[kPer];
-    float vc[kPer];
+  float4 vs[kPer], vt[kPer];
+  float2 vc[kPer];
+  auto load = [&](int64_t t0) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int64_t t = t0 + i * 64 + lane;
       vs[i] = t < a.stats_tiles ? rs[t] : none;
       const bool tok = teacher && t < a.stats_tiles_t;
       vt[i] = tok ? rt[t] : none;
-      vc[i] = xk && tok ? rc[t] : 0.f;
+      vc[i] = xk && tok ? rc[t] : make_float2(0.f, 0.f);
     }
+  };
+  const bool one = nt <= 64 * kPer;
+  float ms = -INFINITY, mt = -INFINITY;
+  for (int64_t t0 = 0; t0 < nt; t0 += 64 * kPer) {
+    load(t0);
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      ss = merge(ss, Stat{vs[i].x, vs[i].y, vs[i].z, vs[i].w}, it2);
-      merge_cross(st, xc, Stat{vt[i].x, vt[i].y, vt[i].z, vt[i].w}, vc[i], it2);
+      ms = fmaxf(ms, vs[i].x);
+      mt = fmaxf(mt, vt[i].x);
     }
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
-    ss = merge(ss, shfl_xor_stat(ss, o), it2);
-    merge_cross(st, xc, shfl_xor_stat(st, o), __shfl_xor(xc, o), it2);
+    ms = fmaxf(ms, __shfl_xor(ms, o));
+    mt = fmaxf(mt, __shfl_xor(mt, o));
+  }
+  ss.m = ms;
+  st.m = mt;
+  for (int64_t t0 = 0; t0 < nt; t0 += 64 * kPer) {
+    if (!one) load(t0);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      if (vs[i].x != -INFINITY) {
+        ss.d1 = fmaf(vs[i].y, __builtin_amdgcn_exp2f((vs[i].x - ms) * kLog2e), ss.d1);
+        ss.dT = fmaf(vs[i].z, __builtin_amdgcn_exp2f((vs[i].x - ms) * it2), ss.dT);
+        ss.sx += vs[i].w;
+      }
+      if (vt[i].x != -INFINITY) {
+        st.d1 = fmaf(vt[i].y, __builtin_amdgcn_exp2f((vt[i].x - mt) * kLog2e), st.d1);
+        st.dT = fmaf(vt[i].z, __builtin_amdgcn_exp2f((vt[i].x - mt) * it2), st.dT);
+        st.sx += vt[i].w;
+      }
+      if (xk) {
+        const float2 c = kl_rebase(vc[i], vs[i].x, vt[i].x, vs[i].z, vt[i].z, ms, mt, inv_t);
+        xc.x += c.x;
+        xc.y += c.y;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    ss.d1 += __shfl_xor(ss.d1, o);
+    ss.dT += __shfl_xor(ss.dT, o);
+    ss.sx += __shfl_xor(ss.sx, o);
+    st.d1 += __shfl_xor(st.d1, o);
+    st.dT += __shfl_xor(st.dT, o);
+    st.sx += __shfl_xor(st.sx, o);
+    if (xk) {
+      xc.x += __shfl_xor(xc.x, o);
+      xc.y += __shfl_xor(xc.y, o);
+    }
   }
   if (lane == 0) {
     const double alpha = static_cast<double>(a.label_smoothing);
@@ -683,11 +740,9 @@ __global__ __launch_bounds__(kThreads) void row_consts_kernel(RowPassArgs a) {
     k.w = TG ? rlog2(a.w_t, fm) - lse1_t * kLog2e : 0.f;
     a.row_consts[r] = k;
     a.row_nll_s[r] = static_cast<float>(row_nll(ss, a.xy_s[r], alpha, a.v));
-    // Without cross partials, row_kl holds lse_s^T - lse_t^T until
-    // row_kl_kernel forms the row's KL from the gradient blocks' sums.
-    a.row_kl[r] = !KL ? 0.f
-                  : xk ? (rdiv(xc, st.dT, fm) * inv_t + lse_t_diff(ss, st, inv_t, fm)) * (T * T)
-                       : lse_t_diff(ss, st, inv_t, fm);
+    // Without the GEMM's KL partials, row_kl_kernel forms the row's KL
+    // from the gradient blocks' sums and these constants.
+    a.row_kl[r] = xk ? kl_paired(xc, ss, st, inv_t, fm) * (T * T) : 0.f;
     a.row_nll_t[r] = a.teacher_ce ? static_cast<float>(row_nll(st, a.xy_t[r], alpha, a.v)) : 0.f;
   }
 }
@@ -806,8 +861,9 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
 // The same chunked pass over fp32 logits (fp32 inputs; bf16 inputs whose
 // KL term needs fp32 logits), where the KL cross term is not available from
 // the GEMM: each (row, kF32Chunk-column) block also writes its share of the
-// two KL sums of row_pass_fused_kernel,
-//   kl_part[r * chunks + c] = {Σ kd·T·p_t^T·(x_t − x_s), Σ kd·T·p_t^T},
+// three KL sums of row_pass_fused_kernel,
+//   kl_part[r * chunks + c] = {Σ kd·T·p_t^T·(x_t − x_s), Σ kd·T·p_t^T,
+//                              Σ kd·T·(p_s^T − p_t^T), 0},
 // and row_kl_kernel adds a row's shares. Gradients go in place (GT float)
 // or to the separate gradient rows grad_s/grad_t; the teacher rows may have
 // their own pitch (Precomputed logits read in place). Ordinary loads and
@@ -823,7 +879,7 @@ constexpr int kF32Chunk = kF32Threads * 8 * kF32Vec;       // columns per workgr
 template <typename GT, bool KL, bool TG>
 __global__ __launch_bounds__(kF32Threads) void row_grad_f32_kernel(RowPassArgs a, int64_t chunks) {
   constexpr int NV = 8;
-  __shared__ float sred[2][kF32Threads / 64];
+  __shared__ float sred[3][kF32Threads / 64];
   const int64_t r = blockIdx.x / chunks;
   const int64_t ci = blockIdx.x - r * chunks;
   const int64_t c0 = ci * kF32Chunk;
@@ -846,7 +902,7 @@ __global__ __launch_bounds__(kF32Threads) void row_grad_f32_kernel(RowPassArgs a
         if (TG) store8(gtrow + j, z);
       }
     }
-    if (KL && tid == 0) a.kl_part[r * chunks + ci] = make_float2(0.f, 0.f);
+    if (KL && tid == 0) a.kl_part[r * chunks + ci] = make_float4(0.f, 0.f, 0.f, 0.f);
     return;
   }
   const float4 k = a.row_consts[r];
@@ -855,12 +911,14 @@ __global__ __launch_bounds__(kF32Threads) void row_grad_f32_kernel(RowPassArgs a
   const float one_m_a = 1.0f - a.label_smoothing;
   const float sgn = a.w_s < 0.f ? -1.f : 1.f;
   const float k0 = -a.w_s * eps, kt0 = -a.w_t * eps;
-  // Gradient of one element pair without the label term; c = kd·T·p_t^T.
-  auto elem = [&](float xs, float xt, float& g, float& gt, float& c) {
+  // Gradient of one element pair without the label term; c = kd·T·p_t^T,
+  // d = kd·T·(p_s^T − p_t^T).
+  auto elem = [&](float xs, float xt, float& g, float& gt, float& c, float& d) {
     g = fmaf(sgn, __builtin_amdgcn_exp2f(fmaf(xs, kLog2e, k.x)), k0);
     if (KL) {
       c = __builtin_amdgcn_exp2f(fmaf(xt, it2, k.z));
-      g += __builtin_amdgcn_exp2f(fmaf(xs, it2, k.y)) - c;
+      d = __builtin_amdgcn_exp2f(fmaf(xs, it2, k.y)) - c;
+      g += d;
     }
     if (TG) gt = __builtin_amdgcn_exp2f(fmaf(xt, kLog2e, k.w)) + kt0;
   };
@@ -885,7 +943,7 @@ __global__ __launch_bounds__(kF32Threads) void row_grad_f32_kernel(RowPassArgs a
       }
     }
   }
-  float cross = 0.f, sum_c = 0.f;
+  float cross = 0.f, sum_c = 0.f, sum_d = 0.f;
 #pragma unroll
   for (int q = 0; q < kF32Vec; ++q) {
     const int64_t j = col(q);
@@ -895,12 +953,13 @@ __global__ __launch_bounds__(kF32Threads) void row_grad_f32_kernel(RowPassArgs a
     for (int i = 0; i < NV; ++i) {
       const float xs = __uint_as_float(rs[q][i >> 2][i & 3]);
       const float xt = (KL || TG) ? __uint_as_float(rt[q][i >> 2][i & 3]) : 0.f;
-      float gi = 0.f, ti = 0.f, c = 0.f;
-      elem(xs, xt, gi, ti, c);
+      float gi = 0.f, ti = 0.f, c = 0.f, d = 0.f;
+      elem(xs, xt, gi, ti, c, d);
       const bool valid = j + i < v;
       if (KL) {
         cross += valid ? c * (xt - xs) : 0.f;
         sum_c += valid ? c : 0.f;
+        sum_d += valid ? d : 0.f;
       }
       g[i] = valid ? gi : 0.f;
       gt[i] = valid ? ti : 0.f;
@@ -909,8 +968,8 @@ __global__ __launch_bounds__(kF32Threads) void row_grad_f32_kernel(RowPassArgs a
     if (TG) store8(gtrow + j, gt);
   }
   if (owner) {   // the label term, after this thread's own store of that column
-    float gy = 0.f, ty = 0.f, c = 0.f;
-    elem(xs_y, xt_y, gy, ty, c);
+    float gy = 0.f, ty = 0.f, c = 0.f, d = 0.f;
+    elem(xs_y, xt_y, gy, ty, c, d);
     gsrow[y] = static_cast<GT>(gy - a.w_s * one_m_a);
     if (TG) gtrow[y] = static_cast<GT>(ty - a.w_t * one_m_a);
   }
@@ -919,53 +978,59 @@ __global__ __launch_bounds__(kF32Threads) void row_grad_f32_kernel(RowPassArgs a
     for (int o = 32; o >= 1; o >>= 1) {
       cross += __shfl_xor(cross, o);
       sum_c += __shfl_xor(sum_c, o);
+      sum_d += __shfl_xor(sum_d, o);
     }
     if ((tid & 63) == 0) {
       sred[0][tid >> 6] = cross;
       sred[1][tid >> 6] = sum_c;
+      sred[2][tid >> 6] = sum_d;
     }
     __syncthreads();
     if (tid == 0) {
-      float x = 0.f, sm = 0.f;
+      float x = 0.f, sm = 0.f, sd = 0.f;
 #pragma unroll
       for (int w = 0; w < kF32Threads / 64; ++w) {
         x += sred[0][w];
         sm += sred[1][w];
+        sd += sred[2][w];
       }
-      a.kl_part[r * chunks + ci] = make_float2(x, sm);
+      a.kl_part[r * chunks + ci] = make_float4(x, sm, sd, 0.f);
     }
   }
 }
 
-// KL_row·T² of every non-ignored row from its gradient blocks' sums and
-// lse_s^T - lse_t^T (left in row_kl by row_consts_kernel), as in
-// row_pass_fused_kernel:
-//   KL_row = Σ p_t^T (x_t − x_s)/T + (lse_s^T − lse_t^T)·Σ p_t^T.
-// One wave per row: lanes take every 64th block, then a butterfly.
+// KL_row·T² of every non-ignored row from its gradient blocks' sums and the
+// exponent offsets of row_consts_kernel (kl_from_sums, as in
+// row_pass_fused_kernel). One wave per row: lanes take every 64th block,
+// then a butterfly.
 __global__ __launch_bounds__(kThreads) void row_kl_kernel(RowPassArgs a, int64_t chunks) {
   const int lane = threadIdx.x & 63;
   const int64_t r = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
   if (r >= a.n_rows) return;
   const int64_t y = a.labels[r];
   if (y == a.ignore_index || y < 0 || y >= a.v) return;   // row_kl is already 0
-  const float2* p = a.kl_part + r * chunks;
-  float x = 0.f, s = 0.f;
+  const float4* p = a.kl_part + r * chunks;
+  float x = 0.f, s = 0.f, d = 0.f;
   for (int64_t c = lane; c < chunks; c += 64) {
-    const float2 q = p[c];
+    const float4 q = p[c];
     x += q.x;
     s += q.y;
+    d += q.z;
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
     x += __shfl_xor(x, o);
     s += __shfl_xor(s, o);
+    d += __shfl_xor(d, o);
   }
   if (lane == 0) {
     const bool fm = a.fast_math;
     const float T = a.temperature;
     const float inv_t = rdiv(1.0f, T, fm);
-    const float gsc = a.kd * T;   // kl.rs:85
-    a.row_kl[r] = (rdiv(x, gsc, fm) * inv_t + a.row_kl[r] * rdiv(s, gsc, fm)) * (T * T);
+    // the offsets the gradient blocks used: p_s^T = 2^(x·log2(e)/T + k.y),
+    // p_t^T = 2^(x·log2(e)/T + k.z), both scaled by kd·T
+    const float4 k = a.row_consts[r];
+    a.row_kl[r] = kl_from_sums(x, s, d, k.z - k.y, inv_t, fm) * (T * T);
   }
 }
 

@@ -61,14 +61,16 @@ class KernelConfig:
     """src/config.rs:45-120. On the GPU path (the reference's CPU path
     ignores the tuning fields):
 
-    * ``fast_math`` (``Profile.Fast``): fp32 inputs run the bf16 pipeline
-      (inputs rounded to bf16 once, bf16 logits storage); approximate
-      per-row logs and divisions;
+    * ``fast_math`` (``Profile.Fast``): the row pass's per-row logs and
+      divisions use the hardware approximations (src/config.rs:37-40,
+      93-103); inputs keep their dtype, so fp32 inputs stay on the fp32
+      GEMMs and match the reference to the fp32 tolerance;
     * ``profile == Profile.Debug`` (the precise preset): bf16 inputs run the
       fp32 pipeline; ``profile`` is set by ``from_profile`` (the reference
       keeps only the fields a preset sets, so this field is added);
-    * ``online_softmax``: one-pass row statistics of logits the GEMM did not
-      produce (Precomputed teacher logits, the chunk-launcher slot);
+    * ``online_softmax``: one-pass row statistics of Precomputed teacher
+      logits (logits the GEMM did not produce; the chunk-launcher slot takes
+      no config and always uses two passes);
     * ``fp32_grad_weight_accumulation``, ``max_fused_size``: accepted and
       validated; grad_W always accumulates in fp32.
     """

@@ -1,8 +1,9 @@
 """Comparison helpers for the GPU parity tests.
 
 Tolerances (stated once, used everywhere):
-* loss, student_ce, teacher_ce, kl: |gpu - ref| <= 1e-4 * max(|ref|, 1e-2)
-  (a 1e-6 absolute floor covers components that are exactly zero);
+* loss, student_ce, teacher_ce, kl: |gpu - ref| <= 1e-4 * |ref| + an
+  absolute floor per component (SCALAR_FLOOR), the fp32 resolution of the
+  terms it is formed from;
 * gradients, fp32 inputs: ||gpu - ref||_F <= 1e-3 * ||ref||_F and every
   element within 1e-3 * max|ref| (+1e-7);
 * gradients, bf16 inputs (the oracle runs on the same bf16-rounded values):
@@ -34,8 +35,20 @@ def to_np(x):
     return np.asarray(x)
 
 
-def check_scalar(name, got, ref, rtol=LOSS_RTOL):
-    tol = rtol * max(abs(ref), 1e-2) + 1e-6
+# Absolute floors of the scalar gate, per component:
+# * the CE terms (and the loss, which sums them): each row's NLL is
+#   lse - x_y with |lse| up to ~20 at these vocabularies, where fp32 values
+#   are spaced 1.9e-6 apart; a mean of such rows keeps that resolution;
+# * kl: the fp32 formation floor of KL·T² per row, at most 0.5·2^-24·T²
+#   (tests/test_gpu_kl_precision.py measures it per path), below 1e-6 for
+#   T <= 4; the small-KL regime is tested there against tighter bounds.
+SCALAR_FLOOR = {"loss": 2e-6, "student_ce": 2e-6, "teacher_ce": 2e-6, "kl": 1e-6}
+
+
+def check_scalar(name, got, ref, rtol=LOSS_RTOL, floor=None):
+    if floor is None:
+        floor = SCALAR_FLOOR.get(name, 2e-6)
+    tol = rtol * abs(ref) + floor
     assert abs(got - ref) <= tol, f"{name}: gpu {got!r} vs ref {ref!r} (tol {tol:.3g})"
 
 

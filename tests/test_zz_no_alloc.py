@@ -4,7 +4,8 @@ identical (the same kernels run; only where their per-row scratch lives
 differs). Two calls in a row, the second with a smaller chunk, so the
 second reads scratch the first left behind. Also: the size limit and the
 device-only rule are rejected with clear errors before any kernel runs, and
-the context's workspace does not grow.
+the context's workspace does not grow. And the call captured into a HIP
+graph, replayed with new inputs, against the allocating slot run eagerly.
 """
 import ctypes as C
 
@@ -87,5 +88,58 @@ def test_noalloc_slot_matches_allocating_slot():
     rc, msg, _ = _call("orda_kl_ce_on_logits_chunk_noalloc", ctx, lc.cpu(), y, 8, False)
     assert rc == L.ORDA_ERR_INVALID
     assert msg == "the no-allocation entry point takes device tensors only"
+    ctx.close()
+    ref_ctx.close()
+
+
+def test_noalloc_slot_under_graph_capture():
+    """The no-allocation slot recorded into a HIP graph (torch.cuda.graph on
+    the context's bound stream): the call returns without waiting, and every
+    replay, with new inputs written in place between replays and eager work
+    and synchronisations around it, gives exactly the outputs of the
+    allocating slot run eagerly on the same inputs."""
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a visible GPU"
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(91)
+    n, v = 256, 3001
+    lc = torch.empty(2 * n, v, device=dev)
+    y = torch.empty(n, dtype=torch.int32, device=dev)
+
+    def refill():
+        lc.copy_(torch.randn(2 * n, v, generator=g, device=dev) * 2)
+        y.copy_(torch.randint(0, v, (n,), generator=g, device=dev, dtype=torch.int32))
+        y[::7] = -100
+
+    refill()
+    outs = [torch.full((n, v), float("nan"), device=dev), torch.full((n,), float("nan"), device=dev),
+            torch.full((2 * n, v), float("nan"), device=dev),
+            torch.full((2 * n,), float("nan"), device=dev)]
+    ctx = H.Context(0)
+    ref_ctx = H.Context(0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    with torch.cuda.graph(graph, stream=side):
+        ctx.bind_stream()   # torch's current stream is now the capturing one
+        rc, msg, _ = _call("orda_kl_ce_on_logits_chunk_noalloc", ctx, lc, y, n, False, outs=outs)
+    assert rc == L.ORDA_OK, msg
+    for replay in range(4):
+        print(f"replay {replay}", flush=True)
+        refill()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ref_ctx.bind_stream()
+        rc_a, msg_a, a = _call("orda_kl_ce_on_logits_chunk", ref_ctx, lc, y, n, False)
+        assert rc_a == L.ORDA_OK, msg_a
+        torch.cuda.synchronize()
+        for name, x, z in zip(("grad_kl_student", "kl_per_row", "grad_ce", "ce_loss"), a, outs):
+            assert torch.equal(x, z), (replay, name)
+        assert bool(torch.isfinite(outs[2]).all())
+        for o in outs:   # the next replay must write every output again
+            o.fill_(float("nan"))
+    del graph
     ctx.close()
     ref_ctx.close()
