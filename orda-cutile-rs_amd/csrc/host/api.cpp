@@ -523,8 +523,9 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   // Statistics and label logits of a whole group: student rows, then teacher
   // rows (the logits GEMM of problem p writes row p*M + r).
   float4* stats = static_cast<float4*>(ws(c, "stats", 2 * cap * nst * 16));
+  // Written for every non-ignored row by the tile or segment holding its
+  // label column (ignored rows are never read).
   float* xy = static_cast<float*>(ws(c, "xy", 2 * cap * 4));
-  hip_check(hipMemsetAsync(xy, 0, 2 * cap * 4, c->stream), "hipMemsetAsync");
   float* rnll_s = row3_out;
   float* rnll_t = row3_out + bt;
   float* rkl = row3_out + 2 * bt;
@@ -619,6 +620,40 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
         return false;
       }
       attach_split_ws(c, sg);
+      const GemmSplit sp = gemm_split_plan(sg);
+      const bool contiguous =
+          g.nprob == 1 || static_cast<float*>(g.prob[1].c) == static_cast<float*>(g.prob[0].c) + g.M * g.ldc;
+      if (sp.splits > 1 && contiguous) {
+        // The whole product splits: its partials only, then one launch over
+        // every problem's rows that sums them in split order, writes the
+        // logits and forms each 8192-column segment's statistics and the
+        // label logit (the reduction and the statistics of the path below
+        // in one pass; timed with the logits GEMM, as the statistics of the
+        // fused epilogue are).
+        sg.partials_only = true;
+        timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_gemm(sg, c->stream); });
+        RowStatsArgs r{};
+        r.src_type = DType::F32;
+        r.src = sg.split_ws;
+        r.lds = sp.ldp;
+        r.src_splits = sp.splits;
+        r.src_split_stride = sp.stride;
+        r.dst_type = DType::F32;
+        r.dst = g.prob[0].c;
+        r.ldd = g.ldc;
+        r.n_rows = g.M * g.nprob;
+        r.v = g.N;
+        r.stats = g.lg.stats;
+        r.stats_ld = g.lg.stats_ld;
+        r.xy = g.lg.xy;
+        r.labels = g.lg.labels;
+        r.label_rows = g.M;
+        r.ignore_index = g.lg.ignore_index;
+        r.inv_t = g.lg.inv_t;
+        r.segmented = true;
+        timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_row_stats(r, c->stream); });
+        return true;
+      }
       timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_gemm(sg, c->stream); });
       for (int p = 0; p < g.nprob; ++p) {
         RowStatsArgs r{};

@@ -1742,6 +1742,14 @@ GemmArgs tail_part(const GemmArgs& g, const TailSplit& ts, bool tail) {
 
 }  // namespace
 
+GemmSplit gemm_split_plan(const GemmArgs& g) {
+  GemmSplit r{0, 0, 0};
+  if (g.split_ws == nullptr || plan_tail(g).at > 0) return r;
+  const SplitPlan sp = plan_split(g);
+  if (sp.splits > 1 && g.split_ws_bytes >= sp.bytes) r = GemmSplit{sp.splits, sp.stride, sp.ldp};
+  return r;
+}
+
 int64_t gemm_split_bytes(const GemmArgs& g) {
   const TailSplit ts = plan_tail(g);
   const SplitPlan sp = plan_split(ts.at > 0 ? tail_part(g, ts, true) : g);
@@ -1762,6 +1770,7 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
   if (g.split_ws != nullptr) {
     const TailSplit ts = plan_tail(g);
+    if (ts.at > 0 && g.partials_only) return hipErrorInvalidValue;
     if (ts.at > 0) {   // whole rounds, then the tail with K split
       const hipError_t e = launch_gemm(tail_part(g, ts, false), stream);
       if (e != hipSuccess) return e;
@@ -1789,6 +1798,7 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
     if (k == nullptr) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(tiles * sp.splits)), dim3(kThreads), 0,
                        stream, s);
+    if (g.partials_only) return hipGetLastError();
     const int64_t total = rows * ((cols + 3) / 4) * g.nprob;
     const unsigned blocks = static_cast<unsigned>((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, g.split_ws,
@@ -1797,6 +1807,7 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
                        g.alpha_ptr, g.epi == GemmEpilogue::AccumF32);
     return hipGetLastError();
   }
+  if (g.partials_only) return hipErrorInvalidValue;   // not split
   GemmArgs one = gr;
   one.split_k = 1;
   const GemmKernel k = select_kernel(one);

@@ -103,9 +103,22 @@ struct GemmArgs {
   // workgroups of split s, partials of split s at split_ws + s*split_stride.
   int split_k;
   int64_t split_len, split_stride;
+  // With split_ws: the split launch writes the partials only and skips the
+  // reduction (the caller reduces them, e.g. launch_row_stats with
+  // src_splits). Only for products gemm_split_plan splits whole.
+  bool partials_only;
 };
 
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);
+// How launch_gemm splits K for g when it splits the whole product (no part
+// in whole rounds) and the workspace suffices: splits > 1, split s's
+// partial of problem p at split_ws + s*stride + p*rows*ldp (rows x ldp, in
+// C's orientation, fp32); otherwise splits = 0.
+struct GemmSplit {
+  int splits;
+  int64_t stride, ldp;
+};
+GemmSplit gemm_split_plan(const GemmArgs& g);
 // Transposed staging of hidden rows for a K-major operand over rows:
 //   dst[c*ldd + r]          = a[r*lda + c]   (r < rows)
 //   dst[c*ldd + rows + r]   = b[r*ldb + c]   (r < rows, when b is set)
@@ -205,6 +218,7 @@ struct RowStatsArgs {
   int64_t stats_ld;
   float* xy;
   const int64_t* labels;   // may be null (then xy is not written)
+  int64_t label_rows;      // > 0: row r's label is labels[r % label_rows]
   int64_t ignore_index;
   float inv_t;
   bool online;             // one online pass; else a max pass, then a sum pass
@@ -212,6 +226,11 @@ struct RowStatsArgs {
   // row, held in registers for both passes (one read), statistics of
   // segment s at stats[r * stats_ld + s]; stats_ld >= row_stats_segments(v).
   bool segmented;
+  // segmented fp32 rows only: src holds src_splits split-K partials, split s
+  // at src + s*src_split_stride; each element is their sum in split order
+  // (the reduction launch_gemm would run), written to dst.
+  int src_splits;
+  int64_t src_split_stride;
 };
 hipError_t launch_row_stats(const RowStatsArgs& a, hipStream_t stream);
 int64_t row_stats_segments(int64_t v);

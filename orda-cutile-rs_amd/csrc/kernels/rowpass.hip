@@ -1095,7 +1095,7 @@ __global__ __launch_bounds__(kThreads) void row_stats_kernel(RowStatsArgs a) {
   if (threadIdx.x == 0) {
     a.stats[r * a.stats_ld] = make_float4(s.m, s.d1, s.dT, s.sx);
     if (a.labels) {
-      const int64_t y = a.labels[r];
+      const int64_t y = a.labels[a.label_rows > 0 ? r % a.label_rows : r];
       if (y != a.ignore_index && y >= 0 && y < a.v) a.xy[r] = static_cast<float>(src[y]);
     }
   }
@@ -1106,7 +1106,7 @@ __global__ __launch_bounds__(kThreads) void row_stats_kernel(RowStatsArgs a) {
 // and the sum pass read HBM once.
 constexpr int kSegCols = 8192;
 constexpr int kSegPer = kSegCols / kThreads;   // 32 columns per thread
-template <typename ST, typename DT>
+template <typename ST, typename DT, bool VEC>
 __global__ __launch_bounds__(kThreads) void row_stats_seg_kernel(RowStatsArgs a, int64_t nseg) {
   __shared__ float sred[kThreads / 64];
   const int64_t r = blockIdx.x / nseg;
@@ -1115,22 +1115,75 @@ __global__ __launch_bounds__(kThreads) void row_stats_seg_kernel(RowStatsArgs a,
   const ST* src = static_cast<const ST*>(a.src) + r * a.lds;
   DT* dst = a.dst ? static_cast<DT*>(a.dst) + r * a.ldd : nullptr;
   const float it2 = a.inv_t * kLog2e;
+  // Element k of this thread is column col(k). VEC (fp32 rows, 16-byte
+  // aligned, pitches a multiple of 4): four consecutive columns per 16-byte
+  // load, so each load instruction of a wave reads one contiguous kilobyte;
+  // a vector that starts below V may end past it inside the row's pitch.
+  // Otherwise one column per load, 64 consecutive elements per wave. Split-K
+  // partials are summed in split order, as splitk_reduce_kernel does.
+  auto col = [&](int k) -> int64_t {
+    return VEC ? c0 + (k >> 2) * (4 * kThreads) + 4 * threadIdx.x + (k & 3)
+               : c0 + k * kThreads + threadIdx.x;
+  };
   float x[kSegPer];
   float m = -INFINITY, sx = 0.f;
-  // Column c0 + k*kThreads + tid for k < kSegPer: each load instruction of a
-  // wave reads 64 consecutive elements.
+  if constexpr (VEC) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-  for (int k = 0; k < kSegPer; ++k) {
-    const int64_t j = c0 + k * kThreads + threadIdx.x;
-    x[k] = j < a.v ? static_cast<float>(src[j]) : -INFINITY;
+    for (int q = 0; q < kSegPer / 4; ++q) {
+      const int64_t j = col(4 * q);
+      f4 v = {0.f, 0.f, 0.f, 0.f};
+      if (j < a.v) {
+        v = *reinterpret_cast<const f4*>(src + j);
+        for (int sp = 1; sp < a.src_splits; ++sp)
+          v += *reinterpret_cast<const f4*>(src + sp * a.src_split_stride + j);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[4 * q + e] = j + e < a.v ? v[e] : -INFINITY;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kSegPer; ++k) {
+      const int64_t j = col(k);
+      x[k] = j < a.v ? static_cast<float>(src[j]) : -INFINITY;
+    }
+  }
+  // the row's label column, when it lies in this segment: its thread writes
+  // the fp32 label logit
+  int64_t yy = -1;
+  if (a.labels) {
+    yy = a.labels[a.label_rows > 0 ? r % a.label_rows : r];
+    if (yy == a.ignore_index || yy < c0 || yy >= c0 + kSegCols || yy >= a.v) yy = -1;
   }
 #pragma unroll
   for (int k = 0; k < kSegPer; ++k) {
-    const int64_t j = c0 + k * kThreads + threadIdx.x;
+    const int64_t j = col(k);
     if (j < a.v) {
       m = fmaxf(m, x[k]);
       sx += x[k];
-      if (dst) dst[j] = static_cast<DT>(x[k]);
+      if (j == yy) a.xy[r] = x[k];
+    }
+  }
+  if (dst) {
+    if constexpr (VEC) {
+      typedef float f4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+      for (int q = 0; q < kSegPer / 4; ++q) {
+        const int64_t j = col(4 * q);
+        if (j + 4 <= a.v) {
+          *reinterpret_cast<f4*>(dst + j) = f4{x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (j + e < a.v) dst[j + e] = static_cast<DT>(x[4 * q + e]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < kSegPer; ++k) {
+        const int64_t j = col(k);
+        if (j < a.v) dst[j] = static_cast<DT>(x[k]);
+      }
     }
   }
   m = block_max(m, sred);
@@ -1147,14 +1200,7 @@ __global__ __launch_bounds__(kThreads) void row_stats_seg_kernel(RowStatsArgs a,
   dT = block_sum(dT, sred);
   if (dst && sg == nseg - 1)
     for (int64_t j = a.v + threadIdx.x; j < a.ldd; j += kThreads) dst[j] = static_cast<DT>(0.f);
-  if (threadIdx.x == 0) {
-    a.stats[r * a.stats_ld + sg] = make_float4(m, d1, dT, sx);
-    if (a.labels) {
-      const int64_t y = a.labels[r];
-      if (y != a.ignore_index && y >= c0 && y < c0 + kSegCols && y < a.v)
-        a.xy[r] = static_cast<float>(src[y]);
-    }
-  }
+  if (threadIdx.x == 0) a.stats[r * a.stats_ld + sg] = make_float4(m, d1, dT, sx);
 }
 
 // ------------------------------------------------------------------ finalize
@@ -1317,6 +1363,8 @@ int64_t row_pass_kl_blocks(int64_t v) { return (v + kF32Chunk - 1) / kF32Chunk; 
 
 hipError_t launch_row_stats(const RowStatsArgs& a, hipStream_t s) {
   if (a.n_rows <= 0) return hipSuccess;
+  if (a.src_splits > 1 && (!a.segmented || a.online || a.src_type != DType::F32 || a.dst == nullptr))
+    return hipErrorInvalidValue;
   dim3 grid(static_cast<unsigned>(a.n_rows));
   const bool sf = a.src_type == DType::F32;
   const bool df = a.dst_type == DType::F32;
@@ -1326,10 +1374,18 @@ hipError_t launch_row_stats(const RowStatsArgs& a, hipStream_t s) {
     const int64_t blocks = a.n_rows * nseg;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     const dim3 g(static_cast<unsigned>(blocks));
-    if (sf && df) hipLaunchKernelGGL((row_stats_seg_kernel<float, float>), g, dim3(kThreads), 0, s, a, nseg);
-    else if (sf) hipLaunchKernelGGL((row_stats_seg_kernel<float, __bf16>), g, dim3(kThreads), 0, s, a, nseg);
-    else if (df) hipLaunchKernelGGL((row_stats_seg_kernel<__bf16, float>), g, dim3(kThreads), 0, s, a, nseg);
-    else hipLaunchKernelGGL((row_stats_seg_kernel<__bf16, __bf16>), g, dim3(kThreads), 0, s, a, nseg);
+    // 16-byte fp32 vectors where the rows allow them (split-K partials
+    // always do; a row of any pitch otherwise goes element by element)
+    const bool vec = sf && a.lds % 4 == 0 && reinterpret_cast<uintptr_t>(a.src) % 16 == 0 &&
+                     a.src_split_stride % 4 == 0 &&
+                     (a.dst == nullptr ||
+                      (df && a.ldd % 4 == 0 && reinterpret_cast<uintptr_t>(a.dst) % 16 == 0));
+    if (a.src_splits > 1 && !vec) return hipErrorInvalidValue;
+    if (vec) hipLaunchKernelGGL((row_stats_seg_kernel<float, float, true>), g, dim3(kThreads), 0, s, a, nseg);
+    else if (sf && df) hipLaunchKernelGGL((row_stats_seg_kernel<float, float, false>), g, dim3(kThreads), 0, s, a, nseg);
+    else if (sf) hipLaunchKernelGGL((row_stats_seg_kernel<float, __bf16, false>), g, dim3(kThreads), 0, s, a, nseg);
+    else if (df) hipLaunchKernelGGL((row_stats_seg_kernel<__bf16, float, false>), g, dim3(kThreads), 0, s, a, nseg);
+    else hipLaunchKernelGGL((row_stats_seg_kernel<__bf16, __bf16, false>), g, dim3(kThreads), 0, s, a, nseg);
     return hipGetLastError();
   }
 #define ORDA_ROWSTATS(ONLINE)                                                                        \
