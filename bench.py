@@ -138,12 +138,12 @@ def work_per_step(wl, plan):
     rowpass = rows_read * v * ls + (bt + t_rows_written) * v * es
     # ... and, to form each row's lse at 1 and at T, the per-row statistics
     # the logits GEMM wrote: one 16-byte entry per 256-column tile (for
-    # Precomputed teacher logits one per 8192-column segment), the teacher's
-    # 4-byte KL cross partial per tile in the paired bf16 layout, the label.
+    # Precomputed teacher logits one per 8192-column segment), the row pair's
+    # two 4-byte KL sums per tile in the paired bf16 layout, the label.
     nst = -(-v // 256)
     t_stats = (-(-v // 8192) if teacher == "precomputed" else nst) if rows_read > bt else 0
     paired = teacher == "tied" and dt == "bf16" and (kd > 0 or wt > 0)
-    rowpass += bt * (nst * 16 + t_stats * 16 + (nst * 4 if paired else 0) + 8)
+    rowpass += bt * (nst * 16 + t_stats * 16 + (nst * 8 if paired else 0) + 8)
     # bf16 logits are stored relative to their 128-column half-tile maxima:
     # 4 bytes per half and row of the logits GEMM (Precomputed teacher rows
     # are stored as they are)
