@@ -441,9 +441,22 @@ bool paired_rows(const LossPlan& P, const Inputs& in) {
          P.dt == orda::DType::BF16;
 }
 
+// Precomputed fp32 teacher logits beside bf16 inputs with a KL term, with a
+// pitch of a multiple of 4 elements and a 16-byte aligned base: the logits
+// GEMM reads each tile's teacher logits in its epilogue and forms the
+// teacher's statistics and the KL sums there (as for paired rows), so that
+// the student logits are stored in bf16 and the row pass reads the teacher
+// rows in place.
+bool teacher_beside_gemm(const LossPlan& P, const Inputs& in) {
+  return P.need_teacher && P.mode == ORDA_TEACHER_PRECOMPUTED && P.kd > 0.f &&
+         P.dt == orda::DType::BF16 && in.tl.t == orda::DType::F32 && in.tl.ld % 4 == 0 &&
+         reinterpret_cast<uintptr_t>(in.tl.p) % 16 == 0;
+}
+
 // Logits storage: bf16 for bf16 inputs wherever only the gradient reads the
-// stored logits (every loss term comes from the GEMM's fp32 statistics);
-// fp32 when the row pass must form the KL cross term from them.
+// stored logits (every loss term comes from the GEMM's fp32 statistics, and
+// the KL sums from the paired GEMM or from Precomputed teacher logits read in
+// its epilogue); fp32 when the row pass must form the KL sums from them.
 orda::DType logits_dtype(const LossPlan& P, bool paired) {
   return P.dt == orda::DType::BF16 && (paired || P.kd <= 0.f) ? orda::DType::BF16
                                                              : orda::DType::F32;
@@ -455,15 +468,16 @@ orda::DType logits_dtype(const LossPlan& P, bool paired) {
 // read past the row, and past the tensor's storage on its last row): the row
 // pass reads them where they are instead of from a copy in the staging buffer.
 bool teacher_logits_direct(const LossPlan& P, const Inputs& in) {
-  return P.need_teacher && P.mode == ORDA_TEACHER_PRECOMPUTED && in.tl.t == logits_dtype(P, false) &&
-         in.tl.ld % 8 == 0 && in.tl.cols % 8 == 0 && reinterpret_cast<uintptr_t>(in.tl.p) % 16 == 0;
+  return teacher_beside_gemm(P, in) ||
+         (P.need_teacher && P.mode == ORDA_TEACHER_PRECOMPUTED && in.tl.t == logits_dtype(P, false) &&
+          in.tl.ld % 8 == 0 && in.tl.cols % 8 == 0 && reinterpret_cast<uintptr_t>(in.tl.p) % 16 == 0);
 }
 
 // Device bytes the loss stages per chunk row: the buffers run_loss sizes by
 // the group's rows. (The split-K partials of small backward GEMMs are sized
 // by the GEMM, at most 256 MB, and come on top.)
 int64_t staged_bytes_per_row(const LossPlan& P, const Inputs& in) {
-  const bool paired = paired_rows(P, in);
+  const bool paired = paired_rows(P, in) || teacher_beside_gemm(P, in);
   const orda::DType lt = logits_dtype(P, paired);
   const int64_t blocks = P.need_teacher && !teacher_logits_direct(P, in) ? 2 : 1;
   const int64_t nst = orda::gemm_stat_tiles(P.v);
@@ -517,7 +531,8 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   // backward GEMMs read are in the input dtype: in place when lt == dt,
   // else a separate bf16 buffer.
   const bool paired = paired_rows(P, in);
-  const DType lt = logits_dtype(P, paired);
+  const bool t_epi = teacher_beside_gemm(P, in);
+  const DType lt = logits_dtype(P, paired || t_epi);
   void* L = ws(c, "logits", blocks * cap * ldl * dtype_size(lt));
   void* Gb = dt == lt ? L : ws(c, "dlogits", blocks * cap * ldl * es);
   // Statistics and label logits of a whole group: student rows, then teacher
@@ -533,7 +548,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   // the K-major A operand of grad_Wᵀ.
   const int64_t ldh_cat = round64(tied_tce ? 2 * cap : cap);   // rows on 128-byte lines
   void* hcat = ws(c, "hcat", std::max(h, P.has_gwt ? P.ht : int64_t{0}) * ldh_cat * es);
-  float2* cross = paired ? static_cast<float2*>(ws(c, "cross", cap * nst * 8)) : nullptr;
+  float2* cross = paired || t_epi ? static_cast<float2*>(ws(c, "cross", cap * nst * 8)) : nullptr;
   // bf16 logits are stored relative to their half-tile maxima: per row
   // pair and 128-column half, the student's and the teacher's maximum side
   // by side (LogitStatsArgs::hmax).
@@ -542,7 +557,8 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   // Row constants of the chunked row passes (paired bf16 logits, or fp32
   // logits), and for fp32 logits with a KL term the per-block KL sums.
   const bool f32_rows = !paired && lt == DType::F32;
-  float4* rconst = paired || f32_rows ? static_cast<float4*>(ws(c, "rconst", cap * 16)) : nullptr;
+  float4* rconst =
+      paired || t_epi || f32_rows ? static_cast<float4*>(ws(c, "rconst", cap * 16)) : nullptr;
   float4* klpart = f32_rows && P.kd > 0.f
                        ? static_cast<float4*>(ws(c, "klpart", cap * row_pass_kl_blocks(v) * 16))
                        : nullptr;
@@ -603,6 +619,12 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
     } else if (fuse_t) {
       f.nprob = 2;
       f.prob[1] = {at(in.th.p, gs * in.th.ld, dt), in.W.p, Lt};
+    } else if (t_epi) {
+      // the group's teacher logits, read in the epilogue beside the student
+      // rows' accumulators: teacher statistics at rows btg + r, KL sums
+      f.lg.teacher_logits = reinterpret_cast<const float*>(at(in.tl.p, gs * in.tl.ld, in.tl.t));
+      f.lg.teacher_ld = in.tl.ld;
+      f.lg.cross = cross;
     }
     f.group_m = 8;
     // fp32 logits of fp32 inputs, for a product with fewer output tiles than
@@ -677,7 +699,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
     };
     const bool seg_s = logits_gemm(f);
     bool seg_t = fuse_t && seg_s;
-    if (P.need_teacher && !fuse_t) {
+    if (P.need_teacher && !fuse_t && !t_epi) {
       if (P.mode == ORDA_TEACHER_PRECOMPUTED) {
         RowStatsArgs r{};
         r.src_type = in.tl.t;
@@ -730,7 +752,9 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       r.stats_ld = nst;
       const int64_t nseg = row_stats_segments(v);
       r.stats_tiles = seg_s ? nseg : nst;
-      r.stats_tiles_t = P.mode == ORDA_TEACHER_PRECOMPUTED ? (P.online ? 1 : nseg) : seg_t ? nseg : nst;
+      r.stats_tiles_t = t_epi ? nst
+                        : P.mode == ORDA_TEACHER_PRECOMPUTED ? (P.online ? 1 : nseg)
+                        : seg_t ? nseg : nst;
       r.xy_s = xy;
       r.xy_t = xy + btg;
       r.cross = cross;
@@ -741,6 +765,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       r.hmax_ld = hld;
       r.row_consts = rconst;
       r.kl_part = klpart;
+      r.teacher_f32 = t_epi;
       r.labels = in.labels + gs;
       r.ignore_index = P.ignore;
       r.w_s = P.w_s;

@@ -579,6 +579,9 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
 
 template <typename T, bool AK, bool BK, GemmEpilogue EPI, typename LT, bool CT>
 __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
+  // The logits epilogues: the product's own rows (Logits), or student rows
+  // beside Precomputed teacher logits read from memory (LogitsTeacher).
+  constexpr bool kLogitsEpi = EPI == GemmEpilogue::Logits || EPI == GemmEpilogue::LogitsTeacher;
   // Ring layout: A tiles of slots 0-3, then B tiles of slots 0-3 (16 KB
   // each), so every slot offset fits a DS instruction's immediate.
   __shared__ __attribute__((aligned(1024))) unsigned char smem[kRing * kStageBytes + kEpiLds];
@@ -628,7 +631,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
   // epilogue's out_row). A global (not flat) load: a flat load would also
   // count in lgkmcnt and turn the main loop's LDS waits into lgkmcnt(0).
   int64_t lab_pre = 0;
-  if constexpr (EPI == GemmEpilogue::Logits) {
+  if constexpr (kLogitsEpi) {
     typedef __attribute__((address_space(1))) const int64_t global_i64;
     const int64_t R = static_cast<int64_t>(tc.m0) + tid;
     const int64_t prs = g.lg.pair_rows;
@@ -647,7 +650,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
   // The logits epilogue takes swapped MFMA operands, so that each lane owns
   // 4 consecutive columns of a row; the store epilogues (grad_hidden, and
   // grad_W computed transposed) take them unswapped.
-  constexpr bool kSwapAB = EPI == GemmEpilogue::Logits;
+  constexpr bool kSwapAB = kLogitsEpi;
 
   const int nkf = static_cast<int>(Kl / SK);   // full stages
   u32x4 ra[2][kFrag], rb[2][kFrag];
@@ -1385,8 +1388,126 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         }
       }
     };
+    // Precomputed teacher logits beside the student rows (LogitsTeacher): per
+    // row block the lane's 32 teacher logits of its row are loaded (16-byte
+    // vectors, one block ahead, so that they are in flight while the previous
+    // block computes) and take the place of the paired GEMM's teacher
+    // accumulators: the teacher's half-tile statistics and label logit and
+    // the two KL sums come out as with paired rows. Only the student rows are
+    // stored. The teacher's half statistics go to partT, in the ring (idle
+    // once the main loop has drained). Non-temporal loads: the logits are read
+    // again only by the row pass, and the L2 holds the operand strips.
+    float4* partT = reinterpret_cast<float4*>(smem);   // [2][256]
+    auto load_t = [&](auto full_c, int i, f32x4 (&tv)[kFrag]) {
+      constexpr bool kFull = decltype(full_c)::value;
+      const int64_t row = static_cast<int64_t>(tc.m0) + wm * 128 + i * 16 + lrow;
+      const float* trow = g.lg.teacher_logits + (row < g.M ? row : g.M - 1) * g.lg.teacher_ld + colw;
+#pragma unroll
+      for (int j = 0; j < kFrag; ++j) {
+        if (kFull || j * 16 + 4 <= ncol) {
+          tv[j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(trow + j * 16));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) tv[j][e] = j * 16 + e < ncol ? trow[j * 16 + e] : 0.f;
+        }
+      }
+    };
+    auto rows_teacher = [&](auto full_c) {
+      constexpr bool kFull = decltype(full_c)::value;
+      f32x4 tbuf[2][kFrag];
+      load_t(full_c, 0, tbuf[0]);
+#pragma unroll
+      for (int i = 0; i < kFrag; ++i) {
+        if (i + 1 < kFrag) load_t(full_c, i + 1, tbuf[(i + 1) & 1]);
+        f32x4 as[kFrag];
+#pragma unroll
+        for (int j = 0; j < kFrag; ++j) as[j] = from_acc(acc[i][j]);
+        const f32x4(&at)[kFrag] = tbuf[i & 1];
+        const int rl = wm * 128 + i * 16 + lrow;            // row within tile
+        const int64_t row = tc.m0 + rl;
+        const int64_t yl64 = lab[rl] - colw;
+        const int yl = (yl64 >= 0 && yl64 < 128) ? static_cast<int>(yl64) : -1;
+        float ms = -INFINITY, mt = -INFINITY;
+        if constexpr (kFull) {
+          ms = row_max32(as);
+          mt = row_max32(at);
+        } else {
+#pragma unroll
+          for (int j = 0; j < kFrag; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (j * 16 + e < ncol) {
+                ms = fmaxf(ms, as[j][e]);
+                mt = fmaxf(mt, at[j][e]);
+              }
+        }
+        ms = quad_max(ms);
+        mt = quad_max(mt);
+        const float o1s = -ms * kLog2e, o1t = -mt * kLog2e;
+        const bool hit = yl >= 0 && (yl & 12) == 0;
+        float xys = 0.f, xyt = 0.f;   // the label's fp32 logits, before as holds t
+        if (hit) {
+          xys = pick(as, yl);
+          xyt = pick(at, yl);
+        }
+        // as in rows_pair: log2 units relative to the half maxima, the KL sums
+        // over (tt - ts) and (aTs - aTt), Σ aTs = dd + Σ aTt
+        float d1s = 0.f, sxs = 0.f, d1t = 0.f, dTt = 0.f, sxt = 0.f, cx = 0.f, dd = 0.f;
+#pragma unroll
+        for (int j = 0; j < kFrag; ++j) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float xs = as[j][e], xt = at[j][e];
+            const float ts = fmaf(xs, kLog2e, o1s), tt = fmaf(xt, kLog2e, o1t);
+            const float a1s = __builtin_amdgcn_exp2f(ts);
+            const float aTs = __builtin_amdgcn_exp2f(ts * inv_t);
+            const float a1t = __builtin_amdgcn_exp2f(tt);
+            const float aTt = __builtin_amdgcn_exp2f(tt * inv_t);
+            if constexpr (kRel) as[j][e] = ts;
+            if (kFull || j * 16 + e < ncol) {
+              d1s += a1s;
+              dd += aTs - aTt;
+              sxs += xs;
+              d1t += a1t;
+              dTt += aTt;
+              sxt += xt;
+              cx = fmaf(aTt, tt - ts, cx);
+            }
+          }
+        }
+        d1s = quad_sum(d1s);
+        dd = quad_sum(dd);
+        sxs = quad_sum(sxs);
+        d1t = quad_sum(d1t);
+        dTt = quad_sum(dTt);
+        sxt = quad_sum(sxt);
+        cx = quad_sum(cx);
+        const float dTs = dd + dTt;
+        if (lgrp == 0) {
+          part[wn * 256 + rl] = make_float4(ms, d1s, dTs, sxs);
+          partT[wn * 256 + rl] = make_float4(mt, d1t, dTt, sxt);
+          xpart[wn * 256 + rl] = make_float2(cx, dd);
+        }
+        u32x4 aw[kFrag / 2];
+        if constexpr (kSwapStore && kFull) swap_rows(as, aw);
+        if (row < g.M) {
+          if (hit) {   // one lane of a row at most, for one column tile
+            g.lg.xy[row] = xys;
+            g.lg.xy[g.M + row] = xyt;
+          }
+          if constexpr (kSwapStore && kFull)
+            store_swapped(C + row * g.ldc + (colw - 4 * lgrp), aw);
+          else
+            store_row(full_c, C + row * g.ldc + colw, as);
+        }
+      }
+    };
     const bool full = tc.n0 + kTile <= g.N;
-    if (prs > 0) {
+    if constexpr (EPI == GemmEpilogue::LogitsTeacher) {
+      static_assert(kRel, "the student rows beside Precomputed teacher logits are bf16");
+      if (full) rows_teacher(SlotC<1>{});
+      else rows_teacher(SlotC<0>{});
+    } else if (prs > 0) {
       if (full) rows_pair(SlotC<1>{});
       else rows_pair(SlotC<0>{});
     } else {
@@ -1433,6 +1554,31 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
           hp[2] = b.x;
         }
         if (teacher) g.lg.cross[(orow - prs) * g.lg.stats_ld + tc.ntile] = cx;
+        if constexpr (EPI == GemmEpilogue::LogitsTeacher) {
+          // the teacher row beside this student row: its tile statistics,
+          // and the two KL sums relative to the two rows' tile maxima
+          const float4 ta = partT[tid], tb = partT[256 + tid];
+          const float mtt = fmaxf(ta.x, tb.x);
+          float4 st;
+          st.x = mtt;
+          st.w = ta.w + tb.w;
+          float2 kx = make_float2(0.f, 0.f);
+          if (mtt == -INFINITY) {
+            st.y = 0.f;
+            st.z = 0.f;
+          } else {
+            st.y = ta.y * __builtin_amdgcn_exp2f((ta.x - mtt) * kLog2e) +
+                   tb.y * __builtin_amdgcn_exp2f((tb.x - mtt) * kLog2e);
+            st.z = ta.z * __builtin_amdgcn_exp2f((ta.x - mtt) * it2) +
+                   tb.z * __builtin_amdgcn_exp2f((tb.x - mtt) * it2);
+            const float2 xa = kl_rebase(xpart[tid], a.x, ta.x, a.z, ta.z, m, mtt, g.lg.inv_t);
+            const float2 xb = kl_rebase(xpart[256 + tid], b.x, tb.x, b.z, tb.z, m, mtt, g.lg.inv_t);
+            kx = make_float2(xa.x + xb.x, xa.y + xb.y);
+          }
+          const int64_t r = orow - static_cast<int64_t>(tc.p) * g.M;
+          g.lg.stats[(g.M + r) * g.lg.stats_ld + tc.ntile] = st;
+          g.lg.cross[r * g.lg.stats_ld + tc.ntile] = kx;
+        }
       }
     }
   }
@@ -1448,6 +1594,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
 #define ORDA_GEMM(NAME, T, AK, BK, EPI, LT, CT) \
   __global__ __launch_bounds__(kThreads, 1) void NAME(GemmArgs g) { gemm_body<T, AK, BK, EPI, LT, CT>(g); }
 ORDA_GEMM(gemm_kk_logits_bf16_bf16, __bf16, true, true, GemmEpilogue::Logits, __bf16, false)
+ORDA_GEMM(gemm_kk_logits_pre_bf16_bf16, __bf16, true, true, GemmEpilogue::LogitsTeacher, __bf16, false)
 ORDA_GEMM(gemm_kk_logits_bf16_f32, __bf16, true, true, GemmEpilogue::Logits, float, false)
 ORDA_GEMM(gemm_km_store_bf16, __bf16, true, false, GemmEpilogue::StoreF32, float, false)
 ORDA_GEMM(gemm_km_accum_bf16, __bf16, true, false, GemmEpilogue::AccumF32, float, false)
@@ -1471,6 +1618,8 @@ GemmKernel select_kernel(const GemmArgs& g) {
   const bool bf = g.in_type == DType::BF16;
   if (g.epi == E::Logits) {
     if (!g.a_kmajor || !g.b_kmajor || g.c_trans) return nullptr;
+    if (g.lg.teacher_logits != nullptr)
+      return bf && g.logits_type == DType::BF16 ? gemm_kk_logits_pre_bf16_bf16 : nullptr;
     if (g.logits_type == DType::BF16) return bf ? gemm_kk_logits_bf16_bf16 : gemm_kk_logits_f32_bf16;
     return bf ? gemm_kk_logits_bf16_f32 : gemm_kk_logits_f32_f32;
   }
@@ -1763,6 +1912,10 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
   if (g.epi == GemmEpilogue::Logits && g.lg.pair_rows > 0 &&
       (g.nprob != 1 || g.lg.cross == nullptr || g.lg.pair_teacher == nullptr ||
        g.in_type != DType::BF16 || g.M != 2 * ((g.lg.pair_rows + 15) / 16 * 16)))
+    return hipErrorInvalidValue;
+  if (g.epi == GemmEpilogue::Logits && g.lg.teacher_logits != nullptr &&
+      (g.nprob != 1 || g.lg.pair_rows > 0 || g.lg.cross == nullptr || g.lg.teacher_ld % 4 ||
+       g.lg.teacher_ld < g.N || reinterpret_cast<uintptr_t>(g.lg.teacher_logits) % 16))
     return hipErrorInvalidValue;
   if (g.epi == GemmEpilogue::Logits && g.logits_type == DType::BF16 &&
       (g.lg.hmax == nullptr || g.lg.hmax_ld % 2 || g.lg.hmax_ld < 4 * ((g.N + kTile - 1) / kTile)))

@@ -759,8 +759,11 @@ __global__ __launch_bounds__(kThreads) void row_consts_kernel(RowPassArgs a) {
 constexpr int kChunkVec = 1;                             // 8-element vectors per thread
 constexpr int kGradThreads = 128;
 constexpr int kChunk = kGradThreads * 8 * kChunkVec;     // columns per workgroup
-template <bool KL, bool TG>
+template <bool KL, bool TG, bool TF32>
 __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, int64_t chunks) {
+  // TF32: the teacher rows are fp32 logits as they are, read in place at
+  // pitch ld_t (Precomputed teacher logits), with no teacher gradient.
+  static_assert(!(TF32 && TG), "Precomputed teacher logits take no gradient");
   constexpr int NV = 8;
   const int64_t r = blockIdx.x / chunks;
   const int64_t c0 = (blockIdx.x - r * chunks) * kChunk;
@@ -768,7 +771,8 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
   const int64_t y = a.labels[r];
   const int64_t v = a.v;
   __bf16* srow = static_cast<__bf16*>(a.student) + r * a.ld;
-  __bf16* trow = (KL || TG) ? static_cast<__bf16*>(a.teacher) + r * a.ld : nullptr;
+  __bf16* trow = (KL || TG) && !TF32 ? static_cast<__bf16*>(a.teacher) + r * a.ld : nullptr;
+  const float* trowf = TF32 ? static_cast<const float*>(a.teacher) + r * a.ld_t : nullptr;
   if (y == a.ignore_index || y < 0 || y >= v) {   // zero gradient rows
     const float z[NV] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -790,13 +794,16 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
   const float k0 = -a.w_s * eps, kt0 = -a.w_t * eps;
   // Both rows are stored relative to their half-tile maxima, in log2 units
   // (LogitStatsArgs::hmax): each 128-column half's maximum is folded into
-  // the exponent offsets, and the T terms scale by 1/T.
+  // the exponent offsets, and the T terms scale by 1/T. fp32 teacher rows
+  // (TF32) are logits as they are: scale log2(e)/T, no maximum.
   auto offs = [&](float hs, float ht) {
-    return float4{fmaf(hs, kLog2e, k.x), fmaf(hs, it2, k.y), fmaf(ht, it2, k.z), fmaf(ht, kLog2e, k.w)};
+    return float4{fmaf(hs, kLog2e, k.x), fmaf(hs, it2, k.y), TF32 ? k.z : fmaf(ht, it2, k.z),
+                  fmaf(ht, kLog2e, k.w)};
   };
+  const float eTt = TF32 ? it2 : inv_t;
   auto elem = [&](float xs, float xt, const float4& o, float& g, float& gt) {
     g = fmaf(sgn, __builtin_amdgcn_exp2f(xs + o.x), k0);
-    if (KL) g += __builtin_amdgcn_exp2f(fmaf(xs, inv_t, o.y)) - __builtin_amdgcn_exp2f(fmaf(xt, inv_t, o.z));
+    if (KL) g += __builtin_amdgcn_exp2f(fmaf(xs, inv_t, o.y)) - __builtin_amdgcn_exp2f(fmaf(xt, eTt, o.z));
     if (TG) gt = __builtin_amdgcn_exp2f(xt + o.w) + kt0;
   };
   // The label column's logits, read by the thread that writes that column.
@@ -805,7 +812,8 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
   float xs_y = 0.f, xt_y = 0.f;
   if (owner) {
     xs_y = static_cast<float>(srow[y]);
-    if (KL || TG) xt_y = static_cast<float>(trow[y]);
+    if (TF32) xt_y = trowf[y];
+    else if (KL || TG) xt_y = static_cast<float>(trow[y]);
   }
   // Half-tile maxima, loaded first (ahead of the logits, so that no wait
   // comes between): the student's and the teacher's maxima of a half are
@@ -820,14 +828,29 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
     hs[q] = m.x;
     ht[q] = m.y;
   }
-  // The loads stay packed (bf16 pairs) until their group is computed.
-  u32x4 rs[kChunkVec], rt[kChunkVec];
+  // The loads stay packed (bf16 pairs) until their group is computed. An
+  // fp32 teacher vector is two 16-byte loads, or single elements where it
+  // would pass the row's end (its pitch is only a multiple of 4).
+  u32x4 rs[kChunkVec], rt[kChunkVec], rt2[kChunkVec];
 #pragma unroll
   for (int q = 0; q < kChunkVec; ++q) {
     const int64_t j = c0 + (static_cast<int64_t>(q) * kGradThreads + tid) * NV;
     if (j < v) {
       rs[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(srow + j));
-      if (KL || TG) rt[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(trow + j));
+      if (TF32) {
+        if (j + NV <= v) {
+          rt[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(trowf + j));
+          rt2[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(trowf + j) + 1);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            rt[q][i] = j + i < v ? __float_as_uint(trowf[j + i]) : 0u;
+            rt2[q][i] = j + 4 + i < v ? __float_as_uint(trowf[j + 4 + i]) : 0u;
+          }
+        }
+      } else if (KL || TG) {
+        rt[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(trow + j));
+      }
     }
   }
 #pragma unroll
@@ -836,7 +859,15 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
     if (j >= v) continue;
     float xs[NV], xt[NV] = {};
     Vec<__bf16>::unpack(rs[q], xs);
-    if (KL || TG) Vec<__bf16>::unpack(rt[q], xt);
+    if (TF32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xt[i] = __uint_as_float(rt[q][i]);
+        xt[4 + i] = __uint_as_float(rt2[q][i]);
+      }
+    } else if (KL || TG) {
+      Vec<__bf16>::unpack(rt[q], xt);
+    }
     float g[NV], gt[NV];
     const float4 o = offs(hs[q], ht[q]);
 #pragma unroll
@@ -1271,6 +1302,30 @@ hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
   const bool kl = a.kl && has_t;
   const bool tg = a.teacher_grad && has_t;
   if ((a.teacher_ce || kl || tg) && a.stats_t == nullptr) return hipErrorInvalidValue;
+  if (a.teacher_f32) {
+    // bf16 student rows (relative to their half-tile maxima) beside fp32
+    // Precomputed teacher logits read in place at pitch ld_t; the statistics
+    // and KL sums of both come from the logits GEMM's epilogue.
+    if (!has_t || tg || a.grad_s != nullptr || a.cross == nullptr || a.row_consts == nullptr ||
+        a.ltype != DType::BF16 || a.hmax_s == nullptr || a.hmax_t != nullptr || a.hmax_ld % 2 ||
+        reinterpret_cast<uintptr_t>(a.hmax_s) % 8 || a.ld_t % 4 || a.ld_t < a.v ||
+        reinterpret_cast<uintptr_t>(a.teacher) % 16)
+      return hipErrorInvalidValue;
+    const int64_t chunks = (a.v + kChunk - 1) / kChunk;
+    const int64_t blocks = a.n_rows * chunks;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 cgrid(static_cast<unsigned>((a.n_rows + kThreads / 64 - 1) / (kThreads / 64)));
+    if (kl) {
+      hipLaunchKernelGGL((row_consts_kernel<true, false>), cgrid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((row_grad_kernel<true, false, true>), dim3(static_cast<unsigned>(blocks)),
+                         dim3(kGradThreads), 0, s, a, chunks);
+    } else {
+      hipLaunchKernelGGL((row_consts_kernel<false, false>), cgrid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((row_grad_kernel<false, false, true>), dim3(static_cast<unsigned>(blocks)),
+                         dim3(kGradThreads), 0, s, a, chunks);
+    }
+    return hipGetLastError();
+  }
   const DType gt = a.grad_s ? a.gtype : a.ltype;
   if (a.grad_s && (tg && a.grad_t == nullptr)) return hipErrorInvalidValue;
   if (a.ld_t && ((a.ld_t % 8) || (tg && a.grad_s == nullptr))) return hipErrorInvalidValue;
@@ -1286,19 +1341,19 @@ hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     if (kl && tg) {
       hipLaunchKernelGGL((row_consts_kernel<true, true>), cgrid, dim3(kThreads), 0, s, a);
-      hipLaunchKernelGGL((row_grad_kernel<true, true>), dim3(static_cast<unsigned>(blocks)),
+      hipLaunchKernelGGL((row_grad_kernel<true, true, false>), dim3(static_cast<unsigned>(blocks)),
                          dim3(kGradThreads), 0, s, a, chunks);
     } else if (kl) {
       hipLaunchKernelGGL((row_consts_kernel<true, false>), cgrid, dim3(kThreads), 0, s, a);
-      hipLaunchKernelGGL((row_grad_kernel<true, false>), dim3(static_cast<unsigned>(blocks)),
+      hipLaunchKernelGGL((row_grad_kernel<true, false, false>), dim3(static_cast<unsigned>(blocks)),
                          dim3(kGradThreads), 0, s, a, chunks);
     } else if (tg) {
       hipLaunchKernelGGL((row_consts_kernel<false, true>), cgrid, dim3(kThreads), 0, s, a);
-      hipLaunchKernelGGL((row_grad_kernel<false, true>), dim3(static_cast<unsigned>(blocks)),
+      hipLaunchKernelGGL((row_grad_kernel<false, true, false>), dim3(static_cast<unsigned>(blocks)),
                          dim3(kGradThreads), 0, s, a, chunks);
     } else {
       hipLaunchKernelGGL((row_consts_kernel<false, false>), cgrid, dim3(kThreads), 0, s, a);
-      hipLaunchKernelGGL((row_grad_kernel<false, false>), dim3(static_cast<unsigned>(blocks)),
+      hipLaunchKernelGGL((row_grad_kernel<false, false, false>), dim3(static_cast<unsigned>(blocks)),
                          dim3(kGradThreads), 0, s, a, chunks);
     }
     return hipGetLastError();

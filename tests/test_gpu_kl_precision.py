@@ -9,6 +9,9 @@ from a nearly equal teacher, on every path that forms the KL term:
   with bf16 inputs), small and large chunks (the row-per-workgroup kernel and
   the (row, column-block) kernels). These form the difference sum
   Σ (p_s^T - p_t^T) per element from the probabilities they compute.
+* precomputed-bf16: fp32 Precomputed teacher logits (the student's logits
+  plus noise) beside bf16 hidden states; the logits GEMM reads the teacher
+  logits in its epilogue and forms the same sums as on the paired path.
 * the chunk-launcher slot (kl_ce_on_logits_chunk) on near-equal rows.
 
 Each compares the per-row KL·T² and the mean KL with the oracle (f64 over the
@@ -44,6 +47,7 @@ T = 1.5
 # so the KL, the same at every shape.
 PATHS = {
     "paired-bf16": ("tied", "bf16", 256, 128, 5000, 128, 0.05, 0.1),
+    "precomputed-bf16": ("precomputed", "bf16", 256, 128, 5000, 128, 0.05, 0.1),
     "f32-fused-tied": ("tied", None, 256, 128, 5000, 128, 0.05, 0.5),
     "f32-fused-separate": ("separate", None, 256, 128, 5000, 128, 0.05, 0.5),
     "f32-fused-separate-bf16": ("separate", "bf16", 256, 128, 5000, 128, 0.05, 0.5),
@@ -93,10 +97,17 @@ def test_small_kl(torch_dev, path, eps):
     if dtype == "bf16":
         s, th, w = bf16_round(s), bf16_round(th), bf16_round(w)
         tw = None if tw is None else bf16_round(tw)
+    if mode == "precomputed":
+        # the student's logits (f64 over the bf16 values) plus noise of the
+        # size a teacher eps away in the hidden states gives
+        tl = (s.astype(np.float64) @ w.astype(np.float64).T +
+              normal((bt, v), 46, eps * wsd * np.sqrt(h))).astype(np.float32)
     opts = LossOptions(kd_weight=0.4, temperature=T, label_smoothing=0.1,
                        chunk_size=ChunkSize.Fixed(cs))
     if mode == "tied":
         tg, to = Teacher.Tied(gpu(torch_dev, th, dtype)), Teacher.Tied(th)
+    elif mode == "precomputed":
+        tg, to = Teacher.Precomputed(gpu(torch_dev, tl)), Teacher.Precomputed(tl)
     else:
         tg = Teacher.Separate(gpu(torch_dev, th, dtype), gpu(torch_dev, tw, dtype))
         to = Teacher.Separate(th, tw)
