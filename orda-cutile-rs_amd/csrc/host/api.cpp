@@ -453,6 +453,17 @@ bool teacher_beside_gemm(const LossPlan& P, const Inputs& in) {
          reinterpret_cast<uintptr_t>(in.tl.p) % 16 == 0;
 }
 
+// A Separate teacher beside bf16 inputs with a KL term and no teacher CE
+// (no teacher gradient): the teacher's logits GEMM runs first and stores its
+// logits in fp32, and the student's logits GEMM reads them in its epilogue as
+// it reads Precomputed logits. Half the staging bytes of fp32 logits for both
+// rows (6 instead of 12 per column with the bf16 gradient buffer) and the
+// same HBM traffic.
+bool separate_beside_gemm(const LossPlan& P) {
+  return P.need_teacher && P.mode == ORDA_TEACHER_SEPARATE && P.kd > 0.f && P.w_t <= 0.f &&
+         P.dt == orda::DType::BF16;
+}
+
 // Logits storage: bf16 for bf16 inputs wherever only the gradient reads the
 // stored logits (every loss term comes from the GEMM's fp32 statistics, and
 // the KL sums from the paired GEMM or from Precomputed teacher logits read in
@@ -477,12 +488,14 @@ bool teacher_logits_direct(const LossPlan& P, const Inputs& in) {
 // the group's rows. (The split-K partials of small backward GEMMs are sized
 // by the GEMM, at most 256 MB, and come on top.)
 int64_t staged_bytes_per_row(const LossPlan& P, const Inputs& in) {
-  const bool paired = paired_rows(P, in) || teacher_beside_gemm(P, in);
+  const bool sep_epi = separate_beside_gemm(P);
+  const bool paired = paired_rows(P, in) || teacher_beside_gemm(P, in) || sep_epi;
   const orda::DType lt = logits_dtype(P, paired);
-  const int64_t blocks = P.need_teacher && !teacher_logits_direct(P, in) ? 2 : 1;
+  const int64_t blocks = P.need_teacher && !teacher_logits_direct(P, in) && !sep_epi ? 2 : 1;
   const int64_t nst = orda::gemm_stat_tiles(P.v);
   int64_t b = blocks * logits_pitch(P.v) *
               (orda::dtype_size(lt) + (lt == P.dt ? 0 : orda::dtype_size(P.dt)));
+  if (sep_epi) b += logits_pitch(P.v) * 4;   // the teacher's fp32 logits
   b += 2 * nst * 16 + 2 * 4;   // statistics, label logits
   if (paired) b += nst * 8 + 16;   // KL partials, row constants
   if (lt == orda::DType::BF16) b += 4 * nst * 4;   // half-tile maxima of both rows
@@ -522,7 +535,8 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   const int64_t nst = gemm_stat_tiles(v);
   const int64_t cap = std::min(bt, G * cs);
   const bool tl_direct = teacher_logits_direct(P, in);
-  const int blocks = P.need_teacher && !tl_direct ? 2 : 1;
+  const bool sep_epi = separate_beside_gemm(P);
+  const int blocks = P.need_teacher && !tl_direct && !sep_epi ? 2 : 1;
   const bool tied_tce = P.mode == ORDA_TEACHER_TIED && P.w_t > 0.f;
 
   // Every loss term comes from fp32 values: the GEMM's tile statistics and
@@ -531,9 +545,12 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   // backward GEMMs read are in the input dtype: in place when lt == dt,
   // else a separate bf16 buffer.
   const bool paired = paired_rows(P, in);
-  const bool t_epi = teacher_beside_gemm(P, in);
+  // fp32 teacher logits read in the student's logits-GEMM epilogue:
+  // Precomputed ones in place, or a Separate teacher's from its own GEMM
+  const bool t_epi = teacher_beside_gemm(P, in) || sep_epi;
   const DType lt = logits_dtype(P, paired || t_epi);
   void* L = ws(c, "logits", blocks * cap * ldl * dtype_size(lt));
+  void* TL = sep_epi ? ws(c, "tlogits", cap * ldl * 4) : nullptr;
   void* Gb = dt == lt ? L : ws(c, "dlogits", blocks * cap * ldl * es);
   // Statistics and label logits of a whole group: student rows, then teacher
   // rows (the logits GEMM of problem p writes row p*M + r).
@@ -571,7 +588,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
     const int64_t ge = std::min(bt, g1 * cs);
     const int64_t btg = ge - gs;
     void* Ls = L;
-    void* Lt = at(L, btg * ldl, lt);
+    void* Lt = sep_epi ? TL : at(L, btg * ldl, lt);
     void* Gs = Gb;
     void* Gt = at(Gb, btg * ldl, dt);
     const bool first = g0 == 0;
@@ -622,8 +639,9 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
     } else if (t_epi) {
       // the group's teacher logits, read in the epilogue beside the student
       // rows' accumulators: teacher statistics at rows btg + r, KL sums
-      f.lg.teacher_logits = reinterpret_cast<const float*>(at(in.tl.p, gs * in.tl.ld, in.tl.t));
-      f.lg.teacher_ld = in.tl.ld;
+      f.lg.teacher_logits = sep_epi ? static_cast<const float*>(Lt)
+                                    : reinterpret_cast<const float*>(at(in.tl.p, gs * in.tl.ld, in.tl.t));
+      f.lg.teacher_ld = sep_epi ? ldl : in.tl.ld;
       f.lg.cross = cross;
     }
     f.group_m = 8;
@@ -697,6 +715,31 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       }
       return true;
     };
+    // A Separate (or Tied at another pitch) teacher's own logits GEMM. With
+    // sep_epi it runs first and stores fp32 logits, which the student's
+    // epilogue then reads (it writes the teacher statistics again, from the
+    // same fp32 values).
+    auto teacher_gemm = [&] {
+      GemmArgs t = f;
+      t.nprob = 1;
+      const bool sep = P.mode == ORDA_TEACHER_SEPARATE;
+      t.K = sep ? P.ht : h;
+      t.lda = in.th.ld;
+      t.ldb = sep ? in.tw.ld : in.W.ld;
+      t.prob[0] = {at(in.th.p, gs * in.th.ld, dt), sep ? in.tw.p : in.W.p, Lt};
+      t.lg.stats = stats + btg * nst;
+      t.lg.xy = xy + btg;
+      t.lg.hmax = hmax ? hmax + 1 : nullptr;   // the teacher side
+      if (sep_epi) {
+        t.logits_type = DType::F32;
+        t.lg.hmax = nullptr;
+        t.lg.teacher_logits = nullptr;
+        t.lg.teacher_ld = 0;
+        t.lg.cross = nullptr;
+      }
+      return logits_gemm(t);
+    };
+    if (sep_epi) teacher_gemm();
     const bool seg_s = logits_gemm(f);
     bool seg_t = fuse_t && seg_s;
     if (P.need_teacher && !fuse_t && !t_epi) {
@@ -720,17 +763,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
         r.segmented = true;
         timed(c, ORDA_KERNEL_OTHER, [&] { return launch_row_stats(r, c->stream); });
       } else {
-        GemmArgs t = f;
-        t.nprob = 1;
-        const bool sep = P.mode == ORDA_TEACHER_SEPARATE;
-        t.K = sep ? P.ht : h;
-        t.lda = in.th.ld;
-        t.ldb = sep ? in.tw.ld : in.W.ld;
-        t.prob[0] = {at(in.th.p, gs * in.th.ld, dt), sep ? in.tw.p : in.W.p, Lt};
-        t.lg.stats = stats + btg * nst;
-        t.lg.xy = xy + btg;
-        t.lg.hmax = hmax ? hmax + 1 : nullptr;   // the teacher side
-        seg_t = logits_gemm(t);
+        seg_t = teacher_gemm();
       }
     }
 
@@ -740,7 +773,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       r.ltype = lt;
       r.student = Ls;
       r.teacher = !P.need_teacher ? nullptr : tl_direct ? at(in.tl.p, gs * in.tl.ld, in.tl.t) : Lt;
-      r.ld_t = tl_direct ? in.tl.ld : 0;
+      r.ld_t = tl_direct ? in.tl.ld : sep_epi ? ldl : 0;
       r.grad_s = dt == lt ? nullptr : Gs;
       r.grad_t = dt == lt ? nullptr : Gt;
       r.gtype = dt;
@@ -759,9 +792,11 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       r.xy_t = xy + btg;
       r.cross = cross;
       // Rows of the logits GEMM in bf16 are relative to their half-tile
-      // maxima; Precomputed teacher rows (converted or in place) are not.
+      // maxima; Precomputed teacher rows (converted or in place) and fp32
+      // teacher rows read beside the student GEMM are not.
       r.hmax_s = hmax;
-      r.hmax_t = hmax && P.need_teacher && P.mode != ORDA_TEACHER_PRECOMPUTED ? hmax + 1 : nullptr;
+      r.hmax_t = hmax && P.need_teacher && P.mode != ORDA_TEACHER_PRECOMPUTED && !t_epi ? hmax + 1
+                                                                                      : nullptr;
       r.hmax_ld = hld;
       r.row_consts = rconst;
       r.kl_part = klpart;

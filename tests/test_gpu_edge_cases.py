@@ -6,7 +6,11 @@ bf16-rounded values; tolerances as in tests/parity.py):
   (staged into a padded copy) and Hs != Ht;
 * Precomputed teacher logits next to bf16 hidden states: fp32 logits used in
   place, fp32 logits with an odd vocabulary (converted), bf16 logits
-  (converted), and a strided device view;
+  (converted), and a strided device view; fp32 logits read in the logits
+  GEMM's epilogue (ragged vocabularies, their own pitch, teacher CE);
+* a Separate teacher's fp32 logits read in the student logits GEMM's
+  epilogue (bf16 inputs, KL, no teacher CE), and with teacher CE (fp32 logits
+  for both rows);
 * hidden widths that are not a multiple of 8 (padded staging of bf16);
 * strided device views of the inputs, 16-byte aligned (used in place) and
   not (staged);
@@ -78,6 +82,37 @@ def test_separate_bf16_unaligned_teacher_width(torch_dev):
                                                dev(torch_dev, wt, "bf16")), opts)
     ref = O.distillation_loss(s, ws, y, Teacher.Separate(th, wt), opts)
     check_output(got, ref, kind="bf16")
+
+
+@pytest.mark.parametrize("bt,hs,ht,v,chunk,w_t", [
+    (192, 96, 100, 1500, 64, None),    # Ht != Hs, ragged V, two staging groups
+    (257, 64, 64, 4096, None, 0.0),    # full tiles, M not a multiple of 256
+    (70, 40, 24, 1003, 16, None),      # V odd: a partial last vector of 8
+    (96, 64, 64, 1000, 32, 0.5),       # teacher CE on: fp32 logits for both rows instead
+])
+def test_separate_bf16_teacher_logits_in_the_gemm_epilogue(torch_dev, bt, hs, ht, v, chunk, w_t):
+    """A Separate teacher with bf16 inputs and a KL term but no teacher CE:
+    the teacher's logits GEMM stores fp32 logits first, and the student's
+    logits GEMM reads them in its epilogue (teacher statistics, label logit
+    and KL sums) and stores the student logits in bf16; the row pass reads
+    the fp32 teacher rows. The last case has teacher CE (a teacher gradient),
+    which keeps fp32 logits for both rows."""
+    s, ws = bf16_round(normal((bt, hs), 141)), bf16_round(normal((v, hs), 142, 0.05))
+    th, wt = bf16_round(normal((bt, ht), 143)), bf16_round(normal((v, ht), 144, 0.05))
+    y = uniform_labels(bt, v, 145)
+    y[::7] = -100
+    opts = LossOptions(kd_weight=0.6, temperature=2.5, label_smoothing=0.05, teacher_ce_weight=w_t,
+                       chunk_size=ChunkSize.Auto if chunk is None else ChunkSize.Fixed(chunk))
+    got = H.distillation_loss(dev(torch_dev, s, "bf16"), dev(torch_dev, ws, "bf16"),
+                              dev(torch_dev, y),
+                              Teacher.Separate(dev(torch_dev, th, "bf16"),
+                                               dev(torch_dev, wt, "bf16")), opts, rows=True)
+    ref = O.distillation_loss(s, ws, y, Teacher.Separate(th, wt), opts)
+    check_output(got, ref, kind="bf16")
+    keep = y != -100
+    rk = got.row_kl.cpu().numpy()
+    assert np.all(rk[~keep] == 0.0)
+    np.testing.assert_allclose(rk[keep], ref.row_kl[keep], rtol=1e-4, atol=1e-6)
 
 
 @pytest.mark.parametrize("tl_dtype,v,view", [(None, 1024, False), (None, 1001, False),

@@ -6,12 +6,15 @@ from a nearly equal teacher, on every path that forms the KL term:
   fp32 accumulators, each element's terms relative to its own row's half-tile
   maximum and each difference rounded before it is summed.
 * f32 fused / f32 chunked: fp32 logits (fp32 inputs; or a Separate teacher
-  with bf16 inputs), small and large chunks (the row-per-workgroup kernel and
-  the (row, column-block) kernels). These form the difference sum
-  Σ (p_s^T - p_t^T) per element from the probabilities they compute.
-* precomputed-bf16: fp32 Precomputed teacher logits (the student's logits
-  plus noise) beside bf16 hidden states; the logits GEMM reads the teacher
-  logits in its epilogue and forms the same sums as on the paired path.
+  with bf16 inputs and teacher CE), small and large chunks (the
+  row-per-workgroup kernel and the (row, column-block) kernels). These form
+  the difference sum Σ (p_s^T - p_t^T) per element from the probabilities they
+  compute.
+* precomputed-bf16 / separate-bf16: fp32 Precomputed teacher logits (the
+  student's logits plus noise), or a Separate teacher's fp32 logits from its
+  own GEMM (no teacher CE), beside bf16 hidden states; the student's logits
+  GEMM reads the teacher logits in its epilogue and forms the same sums as on
+  the paired path.
 * the chunk-launcher slot (kl_ce_on_logits_chunk) on near-equal rows.
 
 Each compares the per-row KL·T² and the mean KL with the oracle (f64 over the
@@ -43,16 +46,18 @@ pytestmark = pytest.mark.gpu
 U = 2.0 ** -24
 T = 1.5
 # path: (teacher, input dtype, BT, H, V, chunk rows, weight std, per-row floor
-# in U·T²). The weight std keeps the logit difference eps·sqrt(H)·std, and
-# so the KL, the same at every shape.
+# in U·T², teacher CE weight). The weight std keeps the logit difference
+# eps·sqrt(H)·std, and so the KL, the same at every shape.
 PATHS = {
-    "paired-bf16": ("tied", "bf16", 256, 128, 5000, 128, 0.05, 0.1),
-    "precomputed-bf16": ("precomputed", "bf16", 256, 128, 5000, 128, 0.05, 0.1),
-    "f32-fused-tied": ("tied", None, 256, 128, 5000, 128, 0.05, 0.5),
-    "f32-fused-separate": ("separate", None, 256, 128, 5000, 128, 0.05, 0.5),
-    "f32-fused-separate-bf16": ("separate", "bf16", 256, 128, 5000, 128, 0.05, 0.5),
+    "paired-bf16": ("tied", "bf16", 256, 128, 5000, 128, 0.05, 0.1, None),
+    "precomputed-bf16": ("precomputed", "bf16", 256, 128, 5000, 128, 0.05, 0.1, None),
+    "separate-bf16": ("separate", "bf16", 256, 128, 5000, 128, 0.05, 0.1, None),
+    "f32-fused-tied": ("tied", None, 256, 128, 5000, 128, 0.05, 0.5, None),
+    "f32-fused-separate": ("separate", None, 256, 128, 5000, 128, 0.05, 0.5, None),
+    # teacher CE on: the teacher gradient, so fp32 logits for both rows
+    "f32-fused-separate-bf16": ("separate", "bf16", 256, 128, 5000, 128, 0.05, 0.5, 0.3),
     # 512 x 65600 >= 2^25 logits per group: the chunked fp32 kernels
-    "f32-chunked-tied": ("tied", None, 512, 32, 65600, 512, 0.1, 0.5),
+    "f32-chunked-tied": ("tied", None, 512, 32, 65600, 512, 0.1, 0.5, None),
 }
 
 
@@ -87,7 +92,7 @@ def check_rows(name, eps, got_rows, ref_rows, got_kl, ref_kl, floor):
 @pytest.mark.parametrize("eps", [1e-1, 1e-2, 1e-3])
 @pytest.mark.parametrize("path", list(PATHS))
 def test_small_kl(torch_dev, path, eps):
-    mode, dtype, bt, h, v, cs, wsd, floor_u = PATHS[path]
+    mode, dtype, bt, h, v, cs, wsd, floor_u, w_t = PATHS[path]
     s = normal((bt, h), 41)
     th = s + normal((bt, h), 42, eps)
     w = normal((v, h), 43, wsd)
@@ -102,7 +107,7 @@ def test_small_kl(torch_dev, path, eps):
         # size a teacher eps away in the hidden states gives
         tl = (s.astype(np.float64) @ w.astype(np.float64).T +
               normal((bt, v), 46, eps * wsd * np.sqrt(h))).astype(np.float32)
-    opts = LossOptions(kd_weight=0.4, temperature=T, label_smoothing=0.1,
+    opts = LossOptions(kd_weight=0.4, temperature=T, label_smoothing=0.1, teacher_ce_weight=w_t,
                        chunk_size=ChunkSize.Fixed(cs))
     if mode == "tied":
         tg, to = Teacher.Tied(gpu(torch_dev, th, dtype)), Teacher.Tied(th)
