@@ -453,14 +453,14 @@ bool teacher_beside_gemm(const LossPlan& P, const Inputs& in) {
          reinterpret_cast<uintptr_t>(in.tl.p) % 16 == 0;
 }
 
-// A Separate teacher beside bf16 inputs with a KL term and no teacher CE
-// (no teacher gradient): the teacher's logits GEMM runs first and stores its
-// logits in fp32, and the student's logits GEMM reads them in its epilogue as
-// it reads Precomputed logits. Half the staging bytes of fp32 logits for both
-// rows (6 instead of 12 per column with the bf16 gradient buffer) and the
-// same HBM traffic.
+// A Separate teacher beside bf16 inputs with a KL term: the teacher's logits
+// GEMM runs first and stores its logits in fp32, and the student's logits
+// GEMM reads them in its epilogue as it reads Precomputed logits; with
+// teacher CE the row pass writes the teacher's gradient rows to a bf16
+// buffer. Staging bytes per column 6 (8 with teacher CE) instead of 12 for
+// fp32 logits of both rows and their bf16 gradients; the same HBM traffic.
 bool separate_beside_gemm(const LossPlan& P) {
-  return P.need_teacher && P.mode == ORDA_TEACHER_SEPARATE && P.kd > 0.f && P.w_t <= 0.f &&
+  return P.need_teacher && P.mode == ORDA_TEACHER_SEPARATE && P.kd > 0.f &&
          P.dt == orda::DType::BF16;
 }
 
@@ -495,7 +495,8 @@ int64_t staged_bytes_per_row(const LossPlan& P, const Inputs& in) {
   const int64_t nst = orda::gemm_stat_tiles(P.v);
   int64_t b = blocks * logits_pitch(P.v) *
               (orda::dtype_size(lt) + (lt == P.dt ? 0 : orda::dtype_size(P.dt)));
-  if (sep_epi) b += logits_pitch(P.v) * 4;   // the teacher's fp32 logits
+  // the teacher's fp32 logits, and its bf16 gradient rows with teacher CE
+  if (sep_epi) b += logits_pitch(P.v) * (P.w_t > 0.f ? 6 : 4);
   b += 2 * nst * 16 + 2 * 4;   // statistics, label logits
   if (paired) b += nst * 8 + 16;   // KL partials, row constants
   if (lt == orda::DType::BF16) b += 4 * nst * 4;   // half-tile maxima of both rows
@@ -551,6 +552,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   const DType lt = logits_dtype(P, paired || t_epi);
   void* L = ws(c, "logits", blocks * cap * ldl * dtype_size(lt));
   void* TL = sep_epi ? ws(c, "tlogits", cap * ldl * 4) : nullptr;
+  void* TG = sep_epi && P.w_t > 0.f ? ws(c, "tgrad", cap * ldl * es) : nullptr;
   void* Gb = dt == lt ? L : ws(c, "dlogits", blocks * cap * ldl * es);
   // Statistics and label logits of a whole group: student rows, then teacher
   // rows (the logits GEMM of problem p writes row p*M + r).
@@ -590,7 +592,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
     void* Ls = L;
     void* Lt = sep_epi ? TL : at(L, btg * ldl, lt);
     void* Gs = Gb;
-    void* Gt = at(Gb, btg * ldl, dt);
+    void* Gt = sep_epi ? TG : at(Gb, btg * ldl, dt);
     const bool first = g0 == 0;
     const bool last = ge >= bt;
 
@@ -775,7 +777,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       r.teacher = !P.need_teacher ? nullptr : tl_direct ? at(in.tl.p, gs * in.tl.ld, in.tl.t) : Lt;
       r.ld_t = tl_direct ? in.tl.ld : sep_epi ? ldl : 0;
       r.grad_s = dt == lt ? nullptr : Gs;
-      r.grad_t = dt == lt ? nullptr : Gt;
+      r.grad_t = sep_epi || dt != lt ? Gt : nullptr;
       r.gtype = dt;
       r.ld = ldl;
       r.n_rows = btg;
@@ -1101,6 +1103,8 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
       ws_release(c, "cross");
       ws_release(c, "rconst");
       ws_release(c, "klpart");
+      ws_release(c, "tlogits");
+      ws_release(c, "tgrad");
       ws_release(c, "splitk");
       if (G > 1) {
         G /= 2;

@@ -206,9 +206,10 @@ struct RowPassArgs {
   float inv_t;             // split mode: 1/T as given
   bool student_only;       // split mode: CE over student rows only
   bool fast_math;          // per-row logs and divisions by the hardware approximations
-  // The teacher rows are fp32 logits as they are (Precomputed teacher logits
-  // read in place at pitch ld_t, no teacher gradient) beside bf16 student
-  // rows relative to their half-tile maxima, with the paired KL sums in cross
+  // The teacher rows are fp32 logits as they are (Precomputed teacher logits,
+  // or a Separate teacher's, read in place at pitch ld_t; a teacher gradient
+  // goes to the bf16 rows grad_t at pitch ld) beside bf16 student rows
+  // relative to their half-tile maxima, with the paired KL sums in cross
   // (LogitStatsArgs::teacher_logits).
   bool teacher_f32;
 };

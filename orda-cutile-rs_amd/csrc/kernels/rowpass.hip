@@ -762,8 +762,8 @@ constexpr int kChunk = kGradThreads * 8 * kChunkVec;     // columns per workgrou
 template <bool KL, bool TG, bool TF32>
 __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, int64_t chunks) {
   // TF32: the teacher rows are fp32 logits as they are, read in place at
-  // pitch ld_t (Precomputed teacher logits), with no teacher gradient.
-  static_assert(!(TF32 && TG), "Precomputed teacher logits take no gradient");
+  // pitch ld_t (Precomputed teacher logits, or a Separate teacher's); its
+  // gradient (TG) then goes to the bf16 rows grad_t at pitch ld.
   constexpr int NV = 8;
   const int64_t r = blockIdx.x / chunks;
   const int64_t c0 = (blockIdx.x - r * chunks) * kChunk;
@@ -773,6 +773,7 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
   __bf16* srow = static_cast<__bf16*>(a.student) + r * a.ld;
   __bf16* trow = (KL || TG) && !TF32 ? static_cast<__bf16*>(a.teacher) + r * a.ld : nullptr;
   const float* trowf = TF32 ? static_cast<const float*>(a.teacher) + r * a.ld_t : nullptr;
+  __bf16* gtrow = TF32 ? (TG ? static_cast<__bf16*>(a.grad_t) + r * a.ld : nullptr) : trow;
   if (y == a.ignore_index || y < 0 || y >= v) {   // zero gradient rows
     const float z[NV] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -780,7 +781,7 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
       const int64_t j = c0 + (static_cast<int64_t>(q) * kGradThreads + tid) * NV;
       if (j < v) {
         store8_nt(srow + j, z);
-        if (TG) store8_nt(trow + j, z);
+        if (TG) store8_nt(gtrow + j, z);
       }
     }
     return;
@@ -798,13 +799,14 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
   // (TF32) are logits as they are: scale log2(e)/T, no maximum.
   auto offs = [&](float hs, float ht) {
     return float4{fmaf(hs, kLog2e, k.x), fmaf(hs, it2, k.y), TF32 ? k.z : fmaf(ht, it2, k.z),
-                  fmaf(ht, kLog2e, k.w)};
+                  TF32 ? k.w : fmaf(ht, kLog2e, k.w)};
   };
   const float eTt = TF32 ? it2 : inv_t;
+  const float e1t = TF32 ? kLog2e : 1.f;
   auto elem = [&](float xs, float xt, const float4& o, float& g, float& gt) {
     g = fmaf(sgn, __builtin_amdgcn_exp2f(xs + o.x), k0);
     if (KL) g += __builtin_amdgcn_exp2f(fmaf(xs, inv_t, o.y)) - __builtin_amdgcn_exp2f(fmaf(xt, eTt, o.z));
-    if (TG) gt = __builtin_amdgcn_exp2f(xt + o.w) + kt0;
+    if (TG) gt = __builtin_amdgcn_exp2f(fmaf(xt, e1t, o.w)) + kt0;
   };
   // The label column's logits, read by the thread that writes that column.
   const int64_t yl = y - c0;
@@ -879,13 +881,13 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
       gt[i] = valid ? ti : 0.f;
     }
     store8_nt(srow + j, g);
-    if (TG) store8_nt(trow + j, gt);
+    if (TG) store8_nt(gtrow + j, gt);
   }
   if (owner) {   // the label term, after this thread's own store of that column
     float gy = 0.f, ty = 0.f;
     elem(xs_y, xt_y, offs(hs[0], ht[0]), gy, ty);   // column y is in this thread's vector
     srow[y] = static_cast<__bf16>(gy - a.w_s * one_m_a);
-    if (TG) trow[y] = static_cast<__bf16>(ty - a.w_t * one_m_a);
+    if (TG) gtrow[y] = static_cast<__bf16>(ty - a.w_t * one_m_a);
   }
 }
 
@@ -1304,25 +1306,31 @@ hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
   if ((a.teacher_ce || kl || tg) && a.stats_t == nullptr) return hipErrorInvalidValue;
   if (a.teacher_f32) {
     // bf16 student rows (relative to their half-tile maxima) beside fp32
-    // Precomputed teacher logits read in place at pitch ld_t; the statistics
-    // and KL sums of both come from the logits GEMM's epilogue.
-    if (!has_t || tg || a.grad_s != nullptr || a.cross == nullptr || a.row_consts == nullptr ||
-        a.ltype != DType::BF16 || a.hmax_s == nullptr || a.hmax_t != nullptr || a.hmax_ld % 2 ||
-        reinterpret_cast<uintptr_t>(a.hmax_s) % 8 || a.ld_t % 4 || a.ld_t < a.v ||
-        reinterpret_cast<uintptr_t>(a.teacher) % 16)
+    // teacher logits read in place at pitch ld_t; the statistics and KL sums
+    // of both come from the logits GEMM's epilogue. The teacher gradient, if
+    // any, goes to the bf16 rows grad_t (pitch ld).
+    if (!has_t || a.grad_s != nullptr || (tg && a.grad_t == nullptr) || a.cross == nullptr ||
+        a.row_consts == nullptr || a.ltype != DType::BF16 || a.hmax_s == nullptr ||
+        a.hmax_t != nullptr || a.hmax_ld % 2 || reinterpret_cast<uintptr_t>(a.hmax_s) % 8 ||
+        a.ld_t % 4 || a.ld_t < a.v || reinterpret_cast<uintptr_t>(a.teacher) % 16)
       return hipErrorInvalidValue;
     const int64_t chunks = (a.v + kChunk - 1) / kChunk;
     const int64_t blocks = a.n_rows * chunks;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     const dim3 cgrid(static_cast<unsigned>((a.n_rows + kThreads / 64 - 1) / (kThreads / 64)));
-    if (kl) {
+    const dim3 ggrid(static_cast<unsigned>(blocks));
+    if (kl && tg) {
+      hipLaunchKernelGGL((row_consts_kernel<true, true>), cgrid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((row_grad_kernel<true, true, true>), ggrid, dim3(kGradThreads), 0, s, a, chunks);
+    } else if (kl) {
       hipLaunchKernelGGL((row_consts_kernel<true, false>), cgrid, dim3(kThreads), 0, s, a);
-      hipLaunchKernelGGL((row_grad_kernel<true, false, true>), dim3(static_cast<unsigned>(blocks)),
-                         dim3(kGradThreads), 0, s, a, chunks);
+      hipLaunchKernelGGL((row_grad_kernel<true, false, true>), ggrid, dim3(kGradThreads), 0, s, a, chunks);
+    } else if (tg) {
+      hipLaunchKernelGGL((row_consts_kernel<false, true>), cgrid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((row_grad_kernel<false, true, true>), ggrid, dim3(kGradThreads), 0, s, a, chunks);
     } else {
       hipLaunchKernelGGL((row_consts_kernel<false, false>), cgrid, dim3(kThreads), 0, s, a);
-      hipLaunchKernelGGL((row_grad_kernel<false, false, true>), dim3(static_cast<unsigned>(blocks)),
-                         dim3(kGradThreads), 0, s, a, chunks);
+      hipLaunchKernelGGL((row_grad_kernel<false, false, true>), ggrid, dim3(kGradThreads), 0, s, a, chunks);
     }
     return hipGetLastError();
   }

@@ -9,8 +9,7 @@ bf16-rounded values; tolerances as in tests/parity.py):
   (converted), and a strided device view; fp32 logits read in the logits
   GEMM's epilogue (ragged vocabularies, their own pitch, teacher CE);
 * a Separate teacher's fp32 logits read in the student logits GEMM's
-  epilogue (bf16 inputs, KL, no teacher CE), and with teacher CE (fp32 logits
-  for both rows);
+  epilogue (bf16 inputs, KL, with and without teacher CE);
 * hidden widths that are not a multiple of 8 (padded staging of bf16);
 * strided device views of the inputs, 16-byte aligned (used in place) and
   not (staged);
@@ -88,15 +87,16 @@ def test_separate_bf16_unaligned_teacher_width(torch_dev):
     (192, 96, 100, 1500, 64, None),    # Ht != Hs, ragged V, two staging groups
     (257, 64, 64, 4096, None, 0.0),    # full tiles, M not a multiple of 256
     (70, 40, 24, 1003, 16, None),      # V odd: a partial last vector of 8
-    (96, 64, 64, 1000, 32, 0.5),       # teacher CE on: fp32 logits for both rows instead
+    (96, 64, 64, 1000, 32, 0.5),       # teacher CE: the teacher's bf16 gradient rows
+    (130, 48, 72, 2050, 40, 1.0),      # teacher CE, Ht != Hs, V % 8 = 2
 ])
 def test_separate_bf16_teacher_logits_in_the_gemm_epilogue(torch_dev, bt, hs, ht, v, chunk, w_t):
-    """A Separate teacher with bf16 inputs and a KL term but no teacher CE:
-    the teacher's logits GEMM stores fp32 logits first, and the student's
-    logits GEMM reads them in its epilogue (teacher statistics, label logit
-    and KL sums) and stores the student logits in bf16; the row pass reads
-    the fp32 teacher rows. The last case has teacher CE (a teacher gradient),
-    which keeps fp32 logits for both rows."""
+    """A Separate teacher with bf16 inputs and a KL term: the teacher's
+    logits GEMM stores fp32 logits first, and the student's logits GEMM reads
+    them in its epilogue (teacher statistics, label logit and KL sums) and
+    stores the student logits in bf16; the row pass reads the fp32 teacher
+    rows, and with teacher CE writes the teacher's gradient rows in bf16 to
+    their own buffer (grad_teacher_hidden and grad_teacher_weight read them)."""
     s, ws = bf16_round(normal((bt, hs), 141)), bf16_round(normal((v, hs), 142, 0.05))
     th, wt = bf16_round(normal((bt, ht), 143)), bf16_round(normal((v, ht), 144, 0.05))
     y = uniform_labels(bt, v, 145)

@@ -5,16 +5,15 @@ from a nearly equal teacher, on every path that forms the KL term:
 * paired: Tied teacher, bf16 inputs. The logits GEMM forms the KL sums from
   fp32 accumulators, each element's terms relative to its own row's half-tile
   maximum and each difference rounded before it is summed.
-* f32 fused / f32 chunked: fp32 logits (fp32 inputs; or a Separate teacher
-  with bf16 inputs and teacher CE), small and large chunks (the
-  row-per-workgroup kernel and the (row, column-block) kernels). These form
-  the difference sum Σ (p_s^T - p_t^T) per element from the probabilities they
-  compute.
+* f32 fused / f32 chunked: fp32 logits of fp32 inputs, small and large
+  chunks (the row-per-workgroup kernel and the (row, column-block) kernels).
+  These form the difference sum Σ (p_s^T - p_t^T) per element from the
+  probabilities they compute.
 * precomputed-bf16 / separate-bf16: fp32 Precomputed teacher logits (the
   student's logits plus noise), or a Separate teacher's fp32 logits from its
-  own GEMM (no teacher CE), beside bf16 hidden states; the student's logits
-  GEMM reads the teacher logits in its epilogue and forms the same sums as on
-  the paired path.
+  own GEMM (with and without teacher CE), beside bf16 hidden states; the
+  student's logits GEMM reads the teacher logits in its epilogue and forms the
+  same sums as on the paired path.
 * the chunk-launcher slot (kl_ce_on_logits_chunk) on near-equal rows.
 
 Each compares the per-row KL·T² and the mean KL with the oracle (f64 over the
@@ -52,10 +51,9 @@ PATHS = {
     "paired-bf16": ("tied", "bf16", 256, 128, 5000, 128, 0.05, 0.1, None),
     "precomputed-bf16": ("precomputed", "bf16", 256, 128, 5000, 128, 0.05, 0.1, None),
     "separate-bf16": ("separate", "bf16", 256, 128, 5000, 128, 0.05, 0.1, None),
+    "separate-bf16-teacher-ce": ("separate", "bf16", 256, 128, 5000, 128, 0.05, 0.1, 0.3),
     "f32-fused-tied": ("tied", None, 256, 128, 5000, 128, 0.05, 0.5, None),
     "f32-fused-separate": ("separate", None, 256, 128, 5000, 128, 0.05, 0.5, None),
-    # teacher CE on: the teacher gradient, so fp32 logits for both rows
-    "f32-fused-separate-bf16": ("separate", "bf16", 256, 128, 5000, 128, 0.05, 0.5, 0.3),
     # 512 x 65600 >= 2^25 logits per group: the chunked fp32 kernels
     "f32-chunked-tied": ("tied", None, 512, 32, 65600, 512, 0.1, 0.5, None),
 }
