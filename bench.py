@@ -132,23 +132,32 @@ def work_per_step(wl, plan):
     # row pass: read the student and teacher logits once, write the gradient
     # rows in the input dtype. Logits are stored in bf16 for bf16 inputs when
     # every loss term comes from the GEMM's fp32 accumulators (tied teacher,
-    # or no KL term), else in fp32.
+    # or no KL term), else in fp32; with bf16 inputs, a KL term and a Separate
+    # or Precomputed teacher, the student's in bf16 beside fp32 teacher
+    # logits (read in the student logits GEMM's epilogue).
     rows_read = 2 * bt if (kd > 0 or wt > 0) else bt
+    beside = dt == "bf16" and kd > 0 and teacher != "tied"
     ls = 2 if dt == "bf16" and (teacher == "tied" or kd == 0) else 4
-    rowpass = rows_read * v * ls + (bt + t_rows_written) * v * es
+    if beside:
+        rowpass = bt * v * (2 + 4) + (bt + t_rows_written) * v * es
+    else:
+        rowpass = rows_read * v * ls + (bt + t_rows_written) * v * es
     # ... and, to form each row's lse at 1 and at T, the per-row statistics
     # the logits GEMM wrote: one 16-byte entry per 256-column tile (for
-    # Precomputed teacher logits one per 8192-column segment), the row pair's
-    # two 4-byte KL sums per tile in the paired bf16 layout, the label.
+    # Precomputed teacher logits that the GEMM did not read, one per
+    # 8192-column segment), the row pair's two 4-byte KL sums per tile where
+    # the GEMM forms them, the label.
     nst = -(-v // 256)
-    t_stats = (-(-v // 8192) if teacher == "precomputed" else nst) if rows_read > bt else 0
-    paired = teacher == "tied" and dt == "bf16" and (kd > 0 or wt > 0)
+    t_stats = (-(-v // 8192) if teacher == "precomputed" and not beside else nst) \
+        if rows_read > bt else 0
+    paired = dt == "bf16" and ((teacher == "tied" and (kd > 0 or wt > 0)) or beside)
     rowpass += bt * (nst * 16 + t_stats * 16 + (nst * 8 if paired else 0) + 8)
     # bf16 logits are stored relative to their 128-column half-tile maxima:
     # 4 bytes per half and row of the logits GEMM (Precomputed teacher rows
-    # are stored as they are)
-    if ls == 2:
-        rowpass += bt * nst * 8 * (2 if rows_read > bt and teacher != "precomputed" else 1)
+    # and fp32 teacher rows are stored as they are)
+    if ls == 2 or beside:
+        rowpass += bt * nst * 8 * (2 if rows_read > bt and teacher != "precomputed" and not beside
+                                   else 1)
     quant_b = v * h * 8 if quant else 0
     return {"gemm_logits": ("mfma", fwd), "gemm_grad_hidden": ("mfma", dgrad),
             "gemm_grad_weight": ("mfma", wgrad), "row_pass": ("hbm", rowpass),
