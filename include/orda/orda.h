@@ -80,10 +80,14 @@ typedef struct {
  *                   tolerance. Set by orda_kernel_config_from_profile; the
  *                   reference records the preset only through the fields
  *                   it sets, so this one field is new.
- *   online_softmax  row statistics of Precomputed teacher logits (logits
- *                   the GEMM did not produce) in one online pass instead of
- *                   a max pass and a sum pass. (The chunk-launcher slot takes
- *                   no KernelConfig; it always uses the two passes.)
+ *   online_softmax  row statistics of Precomputed teacher logits that the
+ *                   logits GEMM does not read (fp32 inputs, or logits that
+ *                   are bf16, unaligned or at a pitch that is not a multiple
+ *                   of 4; with bf16 inputs and a KL term, aligned fp32
+ *                   logits are read in the GEMM's epilogue) in one online
+ *                   pass instead of a max pass and a sum pass. (The
+ *                   chunk-launcher slot takes no KernelConfig; it always
+ *                   uses the two passes.)
  *   fp32_grad_weight_accumulation, max_fused_size: accepted and validated;
  *                   grad_W always accumulates in fp32 (the reference's
  *                   output is f32) and the tile widths are fixed. */

@@ -69,8 +69,10 @@ class KernelConfig:
       fp32 pipeline; ``profile`` is set by ``from_profile`` (the reference
       keeps only the fields a preset sets, so this field is added);
     * ``online_softmax``: one-pass row statistics of Precomputed teacher
-      logits (logits the GEMM did not produce; the chunk-launcher slot takes
-      no config and always uses two passes);
+      logits that the logits GEMM does not read in its epilogue (fp32
+      inputs, or logits that are bf16, unaligned or at a pitch that is not a
+      multiple of 4; the chunk-launcher slot takes no config and always uses
+      two passes);
     * ``fp32_grad_weight_accumulation``, ``max_fused_size``: accepted and
       validated; grad_W always accumulates in fp32.
     """
