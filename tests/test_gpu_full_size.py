@@ -13,6 +13,10 @@ INT8 step itself is pinned end to end: the same call with quantization off
 gives the fp32 grad_W that the quantized call quantized, and quantizing it
 with orda_quant_rows_int8 (bit-exact against the oracle's quantizer) must
 give identical codes, scales and dequantized rows (src/api.rs:380-399).
+
+Also at full shape against the same restatement: the three fp32 workloads
+(Tied 2048x4096x32000, Separate 4096x(2048, 4096)x32000, Precomputed
+4096x4096x65536), and the Separate and Precomputed shapes with bf16 inputs.
 """
 import pytest
 
@@ -130,3 +134,46 @@ def test_fp32_workloads_full_shape(name):
         _, rq, rs = quant(ref["grad_weight"], y)
         flips = check_quantized_vs_reference_device(q, got.grad_weight, ref["grad_weight"], rq, rs)
         print(f"INT8 codes differing at rounding boundaries: {flips} of {v * h}")
+
+
+@pytest.mark.parametrize("name", ["separate-4096x2048x4096x32000-f32",
+                                  "precomputed-4096x4096x65536-f32"])
+def test_bf16_inputs_beside_fp32_teacher_logits_full_shape(name):
+    """The Separate and Precomputed workloads' full shapes with bf16 hidden
+    rows and weights (Precomputed logits stay fp32): the student's logits
+    GEMM reads the teacher's fp32 logits in its epilogue (a Separate
+    teacher's from its own GEMM, with teacher CE and its gradient), the
+    student logits are stored in bf16. Against loss_chunked on the same
+    bf16-rounded values on the same GPU: loss terms to 1e-4, bf16 gradients
+    to 2e-2."""
+    import torch
+    import bench
+    from torch_reference import loss_chunked
+    assert torch.cuda.is_available(), "GPU tests need a visible GPU"
+    assert H.is_available(), "liborda_hip.so does not see a gfx950 device"
+    torch.backends.cuda.matmul.allow_tf32 = False
+    wl = list(bench.WORKLOADS[name])
+    wl[5] = "bf16"
+    wl = tuple(wl)
+    mode, bt, h, ht, v, dt, kd, T, alpha, w_t, _ = wl
+    dev = torch.device("cuda:0")
+    s, w, y, t = bench.make_inputs(torch, wl, dev, seed=11)
+    y[::17] = -100
+    opts = bench.options(H, wl)
+    print(f"case {name} with bf16 inputs", flush=True)
+    got = H.distillation_loss(s, w, y, bench.teacher_obj(H, t), opts)
+    th = t[1] if mode == "separate" else None
+    tw = t[2] if mode == "separate" else None
+    tl = t[1] if mode == "precomputed" else None
+    ref = loss_chunked(s, w, y, mode, th, tw, tl, kd=kd, T=T, alpha=alpha,
+                       w_t=opts.teacher_ce_weight)
+    rel = {}
+    for k in ("loss", "student_ce", "teacher_ce", "kl"):
+        check_scalar(k, getattr(got, k), ref[k])
+        rel[k] = abs(getattr(got, k) - ref[k]) / max(abs(ref[k]), 1e-2)
+    for k in ("grad_student_hidden", "grad_weight", "grad_teacher_hidden", "grad_teacher_weight"):
+        g, r = getattr(got, k), ref[k]
+        assert (g is None) == (r is None), f"{k}: presence differs"
+        if r is not None:
+            rel[k] = check_grad_device(k, g, r, "bf16")
+    print("relative errors:", {k: f"{e:.2e}" for k, e in rel.items()})
