@@ -10,8 +10,9 @@ backward GEMMs (small shapes), grad_hidden in shared raster rounds with a
 grouped tail, grad_hidden as one whole round plus a tail of rows with K
 split, the paired bf16 row pass with INT8 grad_W (deterministic and
 stochastic rounding), several staging groups accumulating into grad_W, a
-Separate teacher, Precomputed logits through the chunked fp32 row pass, and
-the fp32 inputs under Profile.Fast.
+Separate teacher (bf16: its fp32 logits read in the student logits GEMM's
+epilogue), Precomputed logits through the chunked fp32 row pass and beside
+bf16 inputs (read in the epilogue), and the fp32 inputs under Profile.Fast.
 """
 import numpy as np
 import pytest
@@ -54,6 +55,9 @@ CASES = {
                       dict(kd_weight=0.5, temperature=2.0, teacher_ce_weight=0.3)),
     "precomputed-f32-chunked": ("precomputed", "f32", 300, 64, 0, 120000, 0.1,
                                 dict(kd_weight=0.7, temperature=1.5)),
+    "precomputed-bf16-epilogue": ("precomputed", "bf16", 700, 256, 0, 30000, 0.05,
+                                  dict(kd_weight=0.7, temperature=1.5, label_smoothing=0.1,
+                                       chunk_size=ChunkSize.Fixed(256))),
     "tied-f32-fast": ("tied", "f32", 512, 384, 384, 16000, 0.05,
                       dict(kd_weight=0.4, temperature=1.5,
                            config=KernelConfig.from_profile(Profile.Fast))),
@@ -72,8 +76,8 @@ def _inputs(torch, dev, mode, dtype, bt, h, ht, v, wscale):
         teacher = Teacher.Tied(t(normal((bt, h), 64)))
     elif mode == "separate":
         teacher = Teacher.Separate(t(normal((bt, ht), 64)), t(normal((v, ht), 65, wscale)))
-    else:
-        teacher = Teacher.Precomputed(t(normal((bt, v), 64, 2.0)))
+    else:   # fp32 logits beside either input dtype
+        teacher = Teacher.Precomputed(torch.from_numpy(normal((bt, v), 64, 2.0)).to(dev))
     return s, w, y, teacher
 
 
