@@ -296,6 +296,42 @@ def test_multi_group_split_k(torch_dev, dtype):
     ctx.close()
 
 
+@pytest.mark.parametrize("mode", ["separate", "precomputed"])
+def test_multi_group_bf16_teacher_logits_beside_gemm(torch_dev, mode):
+    """bf16 inputs with a Separate teacher (teacher CE on) or fp32
+    Precomputed logits, whose fp32 logits the student's logits GEMM reads in
+    its epilogue, over four staging groups of one chunk: the teacher logits
+    buffer (Separate) or the caller's logits (Precomputed, at each group's
+    row offset) and the teacher gradient rows are reused or offset per
+    group, and grad_W and grad_teacher_weight accumulate across groups."""
+    bt, h, ht, v = 1024, 64, 96, 2000
+    s = bf16_round(normal((bt, h), 75))
+    w = bf16_round(normal((v, h), 76, 0.05))
+    y = uniform_labels(bt, v, 77)
+    y[::9] = -100
+    if mode == "separate":
+        th, tw = bf16_round(normal((bt, ht), 78)), bf16_round(normal((v, ht), 79, 0.05))
+        tg = Teacher.Separate(gpu(torch_dev, th, "bf16"), gpu(torch_dev, tw, "bf16"))
+        to = Teacher.Separate(th, tw)
+        w_t = 0.6
+    else:
+        tl = normal((bt, v), 78, 2.0)
+        tg, to = Teacher.Precomputed(gpu(torch_dev, tl)), Teacher.Precomputed(tl)
+        w_t = None
+    opts = LossOptions(kd_weight=0.5, temperature=1.3, label_smoothing=0.1, teacher_ce_weight=w_t,
+                       chunk_size=ChunkSize.Fixed(256))
+    ctx = H.Context(0)
+    ctx.set_staging_budget(1)   # one chunk per group
+    ctx.set_timing(True)
+    got = H.distillation_loss(gpu(torch_dev, s, "bf16"), gpu(torch_dev, w, "bf16"),
+                              gpu(torch_dev, y), tg, opts, ctx=ctx)
+    _, groups = ctx.kernel_time("row_pass")
+    ref = O.distillation_loss(s, w, y, to, opts)
+    check_output(got, ref, kind="bf16")
+    assert groups == 4, groups
+    ctx.close()
+
+
 def test_ignored_labels_and_reductions(torch_dev):
     bt, h, v = 200, 64, 777
     s, th = normal((bt, h), 51), normal((bt, h), 52)
