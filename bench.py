@@ -350,6 +350,9 @@ KERNEL_CLASSES = (
     # (substring of the kernel name, kernel kind)
     ("gemm_kk_logits_", "gemm_logits"),
     ("gemm_kk_store_", "gemm_logits"),      # small fp32 problems: logits split over K
+    ("gemm_kk_small_", "gemm_logits"),      # ... or on 128 x 128 tiles
+    ("gemm_km_small_", "gemm_grad_hidden"),
+    ("gemm_kmt_small_", "gemm_grad_weight"),
     ("gemm_km_", "gemm_grad_hidden"),
     ("gemm_kmt_", "gemm_grad_weight"),
     ("splitk_reduce", "splitk_reduce"),   # split-K: ordered sum of the partials

@@ -648,16 +648,18 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
     }
     f.group_m = 8;
     // fp32 logits of fp32 inputs, for a product with fewer output tiles than
-    // CUs (small BT·V):
-    // stored plainly with K split over the CUs (launch_gemm's ordered split
-    // K), then each row's statistics and label logit from the stored rows,
-    // per 8192-column segment. The statistics epilogue needs all of K in one
-    // workgroup, so it cannot split. Returns whether that path ran.
+    // CUs (small BT·V): stored plainly, on 128 x 128 tiles where the product
+    // has at most 64 of 256 x 256 and/or with K split over the CUs
+    // (launch_gemm's ordered split K), then each row's statistics and label
+    // logit from the stored rows, per 8192-column segment. The statistics
+    // epilogue needs all of K and 256-wide tiles in one workgroup, so it can
+    // neither split nor take the small tiles. Returns whether that path ran.
     auto logits_gemm = [&](const GemmArgs& g) {
       GemmArgs sg = g;
       sg.epi = GemmEpilogue::StoreF32;
       sg.lg = LogitStatsArgs{};
-      if (lt != DType::F32 || g.in_type != DType::F32 || paired || gemm_split_bytes(sg) <= 0) {
+      if (lt != DType::F32 || g.in_type != DType::F32 || paired ||
+          (gemm_split_bytes(sg) <= 0 && !gemm_small_tiles(sg))) {
         timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_gemm(g, c->stream); });
         return false;
       }
@@ -697,23 +699,28 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
         return true;
       }
       timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_gemm(sg, c->stream); });
-      for (int p = 0; p < g.nprob; ++p) {
+      // the statistics of every problem's rows in one launch where the
+      // problems' rows follow each other
+      const int groups = contiguous ? 1 : g.nprob;
+      for (int p = 0; p < groups; ++p) {
         RowStatsArgs r{};
         r.src_type = DType::F32;
         r.src = g.prob[p].c;
         r.lds = g.ldc;
         r.dst_type = DType::F32;
         r.ldd = g.ldc;
-        r.n_rows = g.M;
+        r.n_rows = contiguous ? g.M * g.nprob : g.M;
         r.v = g.N;
         r.stats = g.lg.stats + p * g.M * g.lg.stats_ld;
         r.stats_ld = g.lg.stats_ld;
         r.xy = g.lg.xy + p * g.M;
         r.labels = g.lg.labels;
+        r.label_rows = g.M;
         r.ignore_index = g.lg.ignore_index;
         r.inv_t = g.lg.inv_t;
         r.segmented = true;
-        timed(c, ORDA_KERNEL_OTHER, [&] { return launch_row_stats(r, c->stream); });
+        // timed with the logits GEMM, as the fused epilogue's statistics are
+        timed(c, ORDA_KERNEL_GEMM_LOGITS, [&] { return launch_row_stats(r, c->stream); });
       }
       return true;
     };

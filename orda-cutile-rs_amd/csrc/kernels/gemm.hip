@@ -1795,6 +1795,305 @@ SplitPlan plan_split(const GemmArgs& g) {
   return sp;
 }
 
+// ------------------------------------------------------- small fp32 products
+// fp32 Store/Accum products with at most 64 tiles of 256 x 256 (a quarter of
+// the CUs) run on 128 x 128 workgroup tiles instead: four times the
+// workgroups, so that K is split less finely or not at all. With 256-wide
+// tiles such a product splits K into slices of 128 (at BT=256, H=512,
+// V=8192: the logits into 4, grad_hidden into 64, grad_W into 4), and each
+// workgroup then spends about as long on its 256 KB of partials and on
+// filling its operand ring as on its 16.8 MFLOP. A kernel of its own: 4
+// waves of 64 x 64 (4 x 4 fragments of v_mfma_f32_16x16x4_f32), operands
+// read from global memory into registers one K stage (32) ahead and stored
+// to LDS transposed ([k][row], so that the 16 lanes of a fragment read 16
+// consecutive floats), two LDS stages (72 KB). A stage's fragments are all
+// read from LDS before its MFMAs (64 registers), so that only the first read
+// of a stage waits; left to the scheduler, every 4 K rows waited for their
+// reads between MFMAs.
+constexpr int kSmTile = 128;
+constexpr int kSmK = 32;
+constexpr int kSmPer = kSmTile * kSmK / 256;   // floats of each operand per thread and stage
+constexpr int kSmPitch = kSmTile + 16;   // floats per LDS K row: the 4 K rows of a read in 4 bank groups
+
+int64_t small_tiles(const GemmArgs& g) {
+  return ((g.M + kSmTile - 1) / kSmTile) * ((g.N + kSmTile - 1) / kSmTile) * g.nprob;
+}
+
+// Whether launch_gemm runs g (a whole product, not a part of a tail split)
+// on the small kernel.
+bool small_f32(const GemmArgs& g) {
+  if (g.in_type != DType::F32 || !g.a_kmajor || g.split_k > 1 || g.M <= 0 || g.N <= 0) return false;
+  if (g.epi != GemmEpilogue::StoreF32 && g.epi != GemmEpilogue::AccumF32) return false;
+  if (g.b_kmajor && (g.c_trans || g.epi == GemmEpilogue::AccumF32)) return false;
+  const int64_t tiles = ((g.M + kTile - 1) / kTile) * ((g.N + kTile - 1) / kTile) * g.nprob;
+  return tiles <= 64;
+}
+
+// The small kernel's split of K: as plan_split, over its 128 x 128 tiles,
+// each split at least 256 elements of K.
+SplitPlan plan_split_small(const GemmArgs& g) {
+  SplitPlan sp{1, g.K, 0, 0, 0};
+  if (g.K <= 0) return sp;
+  const int64_t tiles = small_tiles(g);
+  if (tiles >= 192) return sp;
+  int64_t s = (256 + tiles - 1) / tiles;
+  const int64_t by_k = g.K / 256;
+  if (s > by_k) s = by_k;
+  if (s > 64) s = 64;
+  const int64_t per_split = g.nprob * (g.c_trans ? g.N * ((g.M + 3) / 4 * 4) : g.M * ((g.N + 3) / 4 * 4)) * 4;
+  if (s > (int64_t{256} << 20) / per_split) s = (int64_t{256} << 20) / per_split;
+  if (s <= 1) return sp;
+  const int64_t len = ((g.K + s - 1) / s + 63) / 64 * 64;
+  s = (g.K + len - 1) / len;
+  if (s <= 1) return sp;
+  sp.splits = static_cast<int>(s);
+  sp.len = len;
+  sp.ldp = ((g.c_trans ? g.M : g.N) + 3) / 4 * 4;
+  sp.stride = g.nprob * (g.c_trans ? g.N : g.M) * sp.ldp;
+  sp.bytes = s * sp.stride * 4;
+  return sp;
+}
+
+// A is K-major ([M][K], lda); B is K-major ([N][K], BK) or N-major ([K][N]);
+// C is [M][ldc], or stored transposed ([N][ldc], CT); ACC adds C's old value
+// before the scale, as the big kernel's AccumF32 does. Workgroup w < tiles
+// * split_k: split w / tiles over K range [s * split_len, +split_len),
+// partials at C + s * split_stride.
+template <bool BK, bool CT, bool ACC>
+__device__ __forceinline__ void small_body(const GemmArgs& g) {
+  __shared__ __attribute__((aligned(16))) float sA[2][kSmK][kSmPitch];
+  __shared__ __attribute__((aligned(16))) float sB[2][kSmK][kSmPitch];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t mt = (g.M + kSmTile - 1) / kSmTile, nt = (g.N + kSmTile - 1) / kSmTile;
+  const int64_t per = mt * nt;
+  int64_t lin = blockIdx.x;
+  int64_t kbeg = 0, kend = g.K;
+  int split = 0;
+  if (g.split_k > 1) {
+    split = static_cast<int>(lin / (per * g.nprob));
+    lin -= static_cast<int64_t>(split) * per * g.nprob;
+    kbeg = static_cast<int64_t>(split) * g.split_len;
+    kend = g.K - kbeg < g.split_len ? g.K : kbeg + g.split_len;
+  }
+  const int p = static_cast<int>(lin / per);
+  lin -= static_cast<int64_t>(p) * per;
+  const int64_t m0 = (lin % mt) * kSmTile, n0 = (lin / mt) * kSmTile;
+  const float* A = static_cast<const float*>(g.prob[p].a);
+  const float* B = static_cast<const float*>(g.prob[p].b);
+  float* C = static_cast<float*>(g.prob[p].c) + static_cast<int64_t>(split) * g.split_stride;
+  const bool avec = (reinterpret_cast<uintptr_t>(A) % 16) == 0 && (g.lda % 4) == 0;
+  const bool bvec = (reinterpret_cast<uintptr_t>(B) % 16) == 0 && (g.ldb % 4) == 0;
+
+  // Global loads of one stage: kSmPer consecutive floats of each operand
+  // per thread.
+  //   K-major operand: tile row tid % 128, K columns kSmPer * (tid / 128) + i;
+  //   N-major B: K row tid / kBRow, columns kSmPer * (tid % kBRow) + i, with
+  //   kBRow = 128 / kSmPer threads per K row.
+  constexpr int kBRow = kSmTile / kSmPer;
+  static_assert(2 * kSmPer == kSmK && 256 / kBRow == kSmK, "a stage is 256 threads x kSmPer floats");
+  const int kr = tid & 127, kq = (tid >> 7) * kSmPer;
+  const int br = tid / kBRow, bq = (tid % kBRow) * kSmPer;
+  float ra[kSmPer], rb[kSmPer];
+  auto load_run = [&](const float* src, bool whole, int64_t avail, float (&r)[kSmPer]) {
+    if (whole) {
+#pragma unroll
+      for (int v = 0; v < kSmPer / 4; ++v) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(src + 4 * v);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[4 * v + i] = x[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kSmPer; ++i) r[i] = i < avail ? src[i] : 0.f;
+    }
+  };
+  auto load_kmajor = [&](const float* X, int64_t ld, int64_t rows, int64_t r0, bool vec, int64_t k0,
+                         float (&r)[kSmPer]) {
+    const int64_t row = r0 + kr, k = k0 + kq;
+    const int64_t avail = row < rows ? kend - k : 0;   // elements of the run inside K
+    load_run(X + row * ld + k, vec && avail >= kSmPer, avail, r);
+  };
+  auto load_nmajor = [&](int64_t k0, float (&r)[kSmPer]) {
+    const int64_t k = k0 + br, n = n0 + bq;
+    const int64_t avail = k < kend ? g.N - n : 0;
+    load_run(B + k * g.ldb + n, bvec && avail >= kSmPer, avail, r);
+  };
+  auto load = [&](int64_t k0) {
+    load_kmajor(A, g.lda, g.M, m0, avec, k0, ra);
+    if constexpr (BK) load_kmajor(B, g.ldb, g.N, n0, bvec, k0, rb);
+    else load_nmajor(k0, rb);
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < kSmPer; ++i) sA[buf][kq + i][kr] = ra[i];
+    if constexpr (BK) {
+#pragma unroll
+      for (int i = 0; i < kSmPer; ++i) sB[buf][kq + i][kr] = rb[i];
+    } else {
+#pragma unroll
+      for (int v = 0; v < kSmPer / 4; ++v) {
+        f32x4 x;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = rb[4 * v + i];
+        *reinterpret_cast<f32x4*>(&sB[buf][br][bq + 4 * v]) = x;
+      }
+    }
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // MFMA ks of a stage takes K row 4 * ks + lane / 16 of the stage: lane
+  // (m, q) = (lane % 16, lane / 16) gives A[row m][k] and B[k][column m].
+  const int lm = lane & 15, lq = lane >> 4;
+  const int64_t nst = kend > kbeg ? (kend - kbeg + kSmK - 1) / kSmK : 0;
+  auto compute = [&](int buf) {
+    float fa[kSmK / 4][4], fb[kSmK / 4][4];
+#pragma unroll
+    for (int ks = 0; ks < kSmK / 4; ++ks) {
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        fa[ks][f] = sA[buf][4 * ks + lq][wm * 64 + f * 16 + lm];
+        fb[ks][f] = sB[buf][4 * ks + lq][wn * 64 + f * 16 + lm];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks < kSmK / 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  if (nst > 0) {
+    load(kbeg);
+    store(0);
+  }
+  __syncthreads();
+  for (int64_t st = 0; st < nst; ++st) {
+    const int buf = static_cast<int>(st & 1);
+    if (st + 1 < nst) load(kbeg + (st + 1) * kSmK);
+    compute(buf);
+    if (st + 1 < nst) store(buf ^ 1);
+    __syncthreads();
+  }
+
+  // acc[i][j][e] is row wm*64 + 16i + 4*lq + e, column wn*64 + 16j + lm.
+  const float alpha = g.alpha_ptr != nullptr ? g.alpha * *g.alpha_ptr : g.alpha;
+  const int64_t row_w = m0 + wm * 64 + 4 * lq;
+  const int64_t col_l = n0 + wn * 64 + lm;
+  if constexpr (CT) {
+    const bool vec = (g.ldc % 4) == 0 && (reinterpret_cast<uintptr_t>(C) % 16) == 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t n = col_l + j * 16;
+      if (n >= g.N) continue;
+      float* cn = C + n * g.ldc;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t m = row_w + i * 16;
+        f32x4 v = acc[i][j];
+        if (vec && m + 4 <= g.M) {
+          f32x4* dst = reinterpret_cast<f32x4*>(cn + m);
+          if constexpr (ACC) v = alpha * (*dst + v);
+          else v = alpha * v;
+          *dst = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (m + e < g.M) {
+              float x = v[e];
+              if constexpr (ACC) x = alpha * (cn[m + e] + x);
+              else x = alpha * x;
+              cn[m + e] = x;
+            }
+          }
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t row = row_w + i * 16 + e;
+        if (row >= g.M) continue;
+        float* crow = C + row * g.ldc;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t col = col_l + j * 16;
+          if (col < g.N) {
+            float v = acc[i][j][e];
+            if constexpr (ACC) v = alpha * (crow[col] + v);
+            else v = alpha * v;
+            crow[col] = v;
+          }
+        }
+      }
+    }
+  }
+}
+
+// One named entry point per variant, as for the 256-wide kernels:
+// gemm_<A layout><B layout>[t]_small[_accum]_f32.
+#define ORDA_SMALL(NAME, BK, CT, ACC) \
+  __global__ __launch_bounds__(256) void NAME(GemmArgs g) { small_body<BK, CT, ACC>(g); }
+ORDA_SMALL(gemm_kk_small_f32, true, false, false)
+ORDA_SMALL(gemm_km_small_f32, false, false, false)
+ORDA_SMALL(gemm_km_small_accum_f32, false, false, true)
+ORDA_SMALL(gemm_kmt_small_f32, false, true, false)
+ORDA_SMALL(gemm_kmt_small_accum_f32, false, true, true)
+#undef ORDA_SMALL
+
+// g with small_f32(g): split K over the small tiles where plan_split_small
+// splits and the workspace suffices (partials with alpha 1, then the ordered
+// reduction applying g's epilogue), else one launch.
+hipError_t launch_small(const GemmArgs& g, hipStream_t stream) {
+  using K = void (*)(GemmArgs);
+  auto pick = [](bool bk, bool ct, bool acc) -> K {
+    if (bk) return acc ? nullptr : gemm_kk_small_f32;
+    if (ct) return acc ? gemm_kmt_small_accum_f32 : gemm_kmt_small_f32;
+    return acc ? gemm_km_small_accum_f32 : gemm_km_small_f32;
+  };
+  const int64_t tiles = small_tiles(g);
+  const SplitPlan sp = plan_split_small(g);
+  if (sp.splits > 1 && g.split_ws != nullptr && g.split_ws_bytes >= sp.bytes) {
+    GemmArgs s = g;
+    s.epi = GemmEpilogue::StoreF32;
+    s.alpha = 1.f;
+    s.alpha_ptr = nullptr;
+    s.ldc = sp.ldp;
+    s.split_k = sp.splits;
+    s.split_len = sp.len;
+    s.split_stride = sp.stride;
+    const int64_t rows = g.c_trans ? g.N : g.M, cols = g.c_trans ? g.M : g.N;
+    for (int p = 0; p < g.nprob; ++p) s.prob[p].c = g.split_ws + p * rows * sp.ldp;
+    const K k = pick(g.b_kmajor, g.c_trans, false);
+    if (k == nullptr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(tiles * sp.splits)), dim3(256), 0, stream, s);
+    if (g.partials_only) return hipGetLastError();
+    const int64_t total = rows * ((cols + 3) / 4) * g.nprob;
+    const unsigned blocks = static_cast<unsigned>((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, g.split_ws,
+                       sp.stride, sp.splits, rows, cols, sp.ldp, static_cast<float*>(g.prob[0].c),
+                       g.nprob > 1 ? static_cast<float*>(g.prob[1].c) : nullptr, g.ldc, g.alpha,
+                       g.alpha_ptr, g.epi == GemmEpilogue::AccumF32);
+    return hipGetLastError();
+  }
+  if (g.partials_only) return hipErrorInvalidValue;   // not split
+  GemmArgs one = g;
+  one.split_k = 1;
+  const K k = pick(g.b_kmajor, g.c_trans, g.epi == GemmEpilogue::AccumF32);
+  if (k == nullptr) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(tiles)), dim3(256), 0, stream, one);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 int64_t gemm_stat_tiles(int64_t n) { return (n + kTile - 1) / kTile; }
@@ -1893,19 +2192,38 @@ GemmArgs tail_part(const GemmArgs& g, const TailSplit& ts, bool tail) {
 
 GemmSplit gemm_split_plan(const GemmArgs& g) {
   GemmSplit r{0, 0, 0};
-  if (g.split_ws == nullptr || plan_tail(g).at > 0) return r;
-  const SplitPlan sp = plan_split(g);
+  if (g.split_ws == nullptr) return r;
+  const bool small = small_f32(g);
+  if (!small && plan_tail(g).at > 0) return r;
+  const SplitPlan sp = small ? plan_split_small(g) : plan_split(g);
   if (sp.splits > 1 && g.split_ws_bytes >= sp.bytes) r = GemmSplit{sp.splits, sp.stride, sp.ldp};
   return r;
 }
 
 int64_t gemm_split_bytes(const GemmArgs& g) {
+  if (small_f32(g)) {
+    const SplitPlan sp = plan_split_small(g);
+    return sp.splits > 1 ? sp.bytes : 0;
+  }
   const TailSplit ts = plan_tail(g);
   const SplitPlan sp = plan_split(ts.at > 0 ? tail_part(g, ts, true) : g);
   return sp.splits > 1 ? sp.bytes : 0;
 }
 
+bool gemm_small_tiles(const GemmArgs& g) { return small_f32(g); }
+
+namespace {
+hipError_t launch_gemm_impl(const GemmArgs& g, hipStream_t stream, bool whole);
+}  // namespace
+
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
+  return launch_gemm_impl(g, stream, true);
+}
+
+namespace {
+// whole: g is the caller's whole product (not a part of a tail split), which
+// may run on the small kernel.
+hipError_t launch_gemm_impl(const GemmArgs& g, hipStream_t stream, bool whole) {
   if (g.nprob < 1 || g.nprob > 2) return hipErrorInvalidValue;
   if ((g.lda % 8) || (g.ldb % 8) || (g.ldc % 8 && g.epi == GemmEpilogue::Logits))
     return hipErrorInvalidValue;
@@ -1921,13 +2239,14 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
       (g.lg.hmax == nullptr || g.lg.hmax_ld % 2 || g.lg.hmax_ld < 4 * ((g.N + kTile - 1) / kTile)))
     return hipErrorInvalidValue;
   if (g.M <= 0 || g.N <= 0) return hipSuccess;
+  if (whole && small_f32(g)) return launch_small(g, stream);
   if (g.split_ws != nullptr) {
     const TailSplit ts = plan_tail(g);
     if (ts.at > 0 && g.partials_only) return hipErrorInvalidValue;
     if (ts.at > 0) {   // whole rounds, then the tail with K split
-      const hipError_t e = launch_gemm(tail_part(g, ts, false), stream);
+      const hipError_t e = launch_gemm_impl(tail_part(g, ts, false), stream, false);
       if (e != hipSuccess) return e;
-      return launch_gemm(tail_part(g, ts, true), stream);
+      return launch_gemm_impl(tail_part(g, ts, true), stream, false);
     }
   }
   const int64_t tiles = ((g.M + kTile - 1) / kTile) * ((g.N + kTile - 1) / kTile) * g.nprob;
@@ -1968,5 +2287,6 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
   hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, stream, one);
   return hipGetLastError();
 }
+}  // namespace
 
 }  // namespace orda

@@ -139,6 +139,10 @@ hipError_t launch_transpose_rows(const void* a, int64_t lda, const void* b, int6
                                  hipStream_t stream);
 // Workspace bytes launch_gemm uses to split K for this GEMM (0: no split).
 int64_t gemm_split_bytes(const GemmArgs& g);
+// Whether launch_gemm runs this Store/Accum GEMM on 128 x 128 tiles (fp32
+// inputs, at most 64 tiles of 256 x 256): splits and partials as given by
+// gemm_split_plan / gemm_split_bytes.
+bool gemm_small_tiles(const GemmArgs& g);
 int64_t gemm_stat_tiles(int64_t n);   // ceil(n/256)
 
 // ---------------------------------------------------------------- row pass
