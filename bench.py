@@ -45,6 +45,13 @@ WORKLOADS = {
                                                2.0, 0.1, 1.0, False, "fast"),
     "precomputed-4096x4096x65536-f32-fast": ("precomputed", 4096, 4096, 4096, 65536, "f32", 0.7,
                                              1.0, 0.0, None, False, "fast"),
+    # the same Separate and Precomputed shapes with bf16 hidden rows and
+    # weights (Precomputed logits stay fp32): the student's logits in bf16,
+    # the teacher's fp32 logits read in the student logits GEMM's epilogue
+    "separate-4096x2048x4096x32000-bf16": ("separate", 4096, 2048, 4096, 32000, "bf16", 0.5, 2.0,
+                                           0.1, 1.0, False),
+    "precomputed-4096x4096x65536-bf16": ("precomputed", 4096, 4096, 4096, 65536, "bf16", 0.7,
+                                         1.0, 0.0, None, False),
 }
 DEFAULT = "tied-8192x4096x131072-bf16-int8"
 

@@ -136,8 +136,8 @@ def test_fp32_workloads_full_shape(name):
         print(f"INT8 codes differing at rounding boundaries: {flips} of {v * h}")
 
 
-@pytest.mark.parametrize("name", ["separate-4096x2048x4096x32000-f32",
-                                  "precomputed-4096x4096x65536-f32"])
+@pytest.mark.parametrize("name", ["separate-4096x2048x4096x32000-bf16",
+                                  "precomputed-4096x4096x65536-bf16"])
 def test_bf16_inputs_beside_fp32_teacher_logits_full_shape(name):
     """The Separate and Precomputed workloads' full shapes with bf16 hidden
     rows and weights (Precomputed logits stay fp32): the student's logits
@@ -152,15 +152,14 @@ def test_bf16_inputs_beside_fp32_teacher_logits_full_shape(name):
     assert torch.cuda.is_available(), "GPU tests need a visible GPU"
     assert H.is_available(), "liborda_hip.so does not see a gfx950 device"
     torch.backends.cuda.matmul.allow_tf32 = False
-    wl = list(bench.WORKLOADS[name])
-    wl[5] = "bf16"
-    wl = tuple(wl)
+    wl = bench.WORKLOADS[name]
     mode, bt, h, ht, v, dt, kd, T, alpha, w_t, _ = wl
+    assert dt == "bf16"
     dev = torch.device("cuda:0")
     s, w, y, t = bench.make_inputs(torch, wl, dev, seed=11)
     y[::17] = -100
     opts = bench.options(H, wl)
-    print(f"case {name} with bf16 inputs", flush=True)
+    print(f"case {name}", flush=True)
     got = H.distillation_loss(s, w, y, bench.teacher_obj(H, t), opts)
     th = t[1] if mode == "separate" else None
     tw = t[2] if mode == "separate" else None
