@@ -131,7 +131,7 @@ def check(path):
     checked = 0
     for fn in re.split(r"\n(?=_Z\w+:)", text):
         name = fn.split(":")[0]
-        if not re.search(r"gemm_(kk|km|kmt)_(logits|logits_pre|store|accum)_bf16", name):
+        if not re.search(r"gemm_(kk|km|kmt)_(logits|logits_pre|logits_pre16|store|accum)_bf16", name):
             continue
         checked += 1
         end = fn.find("s_endpgm")
@@ -158,8 +158,8 @@ def check(path):
                     entry[j] = merged
                     if j not in work:
                         work.append(j)
-    if checked < 7:
-        errors.add(f"expected the 7 bf16 GEMM variants, found {checked}")
+    if checked < 8:
+        errors.add(f"expected the 8 bf16 GEMM variants, found {checked}")
     return sorted(errors)
 
 

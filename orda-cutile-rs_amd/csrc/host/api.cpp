@@ -441,16 +441,18 @@ bool paired_rows(const LossPlan& P, const Inputs& in) {
          P.dt == orda::DType::BF16;
 }
 
-// Precomputed fp32 teacher logits beside bf16 inputs with a KL term, with a
-// pitch of a multiple of 4 elements and a 16-byte aligned base: the logits
-// GEMM reads each tile's teacher logits in its epilogue and forms the
-// teacher's statistics and the KL sums there (as for paired rows), so that
-// the student logits are stored in bf16 and the row pass reads the teacher
-// rows in place.
+// Precomputed teacher logits beside bf16 inputs with a KL term, fp32 with a
+// pitch of a multiple of 4 elements or bf16 with a pitch of a multiple of 8,
+// on a 16-byte aligned base: the logits GEMM reads each tile's teacher logits
+// in its epilogue and forms the teacher's statistics and the KL sums there
+// (as for paired rows), so that the student logits are stored in bf16 and the
+// row pass reads the teacher rows in place.
 bool teacher_beside_gemm(const LossPlan& P, const Inputs& in) {
-  return P.need_teacher && P.mode == ORDA_TEACHER_PRECOMPUTED && P.kd > 0.f &&
-         P.dt == orda::DType::BF16 && in.tl.t == orda::DType::F32 && in.tl.ld % 4 == 0 &&
-         reinterpret_cast<uintptr_t>(in.tl.p) % 16 == 0;
+  if (!P.need_teacher || P.mode != ORDA_TEACHER_PRECOMPUTED || P.kd <= 0.f ||
+      P.dt != orda::DType::BF16 || reinterpret_cast<uintptr_t>(in.tl.p) % 16)
+    return false;
+  return (in.tl.t == orda::DType::F32 && in.tl.ld % 4 == 0) ||
+         (in.tl.t == orda::DType::BF16 && in.tl.ld % 8 == 0);
 }
 
 // A Separate teacher beside bf16 inputs with a KL term: the teacher's logits
@@ -641,9 +643,9 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
     } else if (t_epi) {
       // the group's teacher logits, read in the epilogue beside the student
       // rows' accumulators: teacher statistics at rows btg + r, KL sums
-      f.lg.teacher_logits = sep_epi ? static_cast<const float*>(Lt)
-                                    : reinterpret_cast<const float*>(at(in.tl.p, gs * in.tl.ld, in.tl.t));
+      f.lg.teacher_logits = sep_epi ? Lt : at(in.tl.p, gs * in.tl.ld, in.tl.t);
       f.lg.teacher_ld = sep_epi ? ldl : in.tl.ld;
+      f.lg.teacher_type = sep_epi ? DType::F32 : in.tl.t;
       f.lg.cross = cross;
     }
     f.group_m = 8;
@@ -809,7 +811,10 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       r.hmax_ld = hld;
       r.row_consts = rconst;
       r.kl_part = klpart;
-      r.teacher_f32 = t_epi;
+      // the teacher rows as they are: a Separate teacher's fp32 logits, or the
+      // caller's Precomputed logits in their own dtype
+      r.teacher_f32 = t_epi && (sep_epi || in.tl.t == DType::F32);
+      r.teacher_bf16 = t_epi && !sep_epi && in.tl.t == DType::BF16;
       r.labels = in.labels + gs;
       r.ignore_index = P.ignore;
       r.w_s = P.w_s;

@@ -580,8 +580,10 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
 template <typename T, bool AK, bool BK, GemmEpilogue EPI, typename LT, bool CT>
 __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
   // The logits epilogues: the product's own rows (Logits), or student rows
-  // beside Precomputed teacher logits read from memory (LogitsTeacher).
-  constexpr bool kLogitsEpi = EPI == GemmEpilogue::Logits || EPI == GemmEpilogue::LogitsTeacher;
+  // beside teacher logits read from memory (LogitsTeacher: fp32,
+  // LogitsTeacher16: bf16).
+  constexpr bool kTeacherEpi = EPI == GemmEpilogue::LogitsTeacher || EPI == GemmEpilogue::LogitsTeacher16;
+  constexpr bool kLogitsEpi = EPI == GemmEpilogue::Logits || kTeacherEpi;
   // Ring layout: A tiles of slots 0-3, then B tiles of slots 0-3 (16 KB
   // each), so every slot offset fits a DS instruction's immediate.
   __shared__ __attribute__((aligned(1024))) unsigned char smem[kRing * kStageBytes + kEpiLds];
@@ -1388,27 +1390,47 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
         }
       }
     };
-    // Precomputed teacher logits beside the student rows (LogitsTeacher): per
-    // row block the lane's 32 teacher logits of its row are loaded (16-byte
-    // vectors, one block ahead, so that they are in flight while the previous
-    // block computes) and take the place of the paired GEMM's teacher
-    // accumulators: the teacher's half-tile statistics and label logit and
-    // the two KL sums come out as with paired rows. Only the student rows are
-    // stored. The teacher's half statistics go to partT, in the ring (idle
-    // once the main loop has drained). Non-temporal loads: the logits are read
-    // again only by the row pass, and the L2 holds the operand strips.
+    // Teacher logits beside the student rows (LogitsTeacher, LogitsTeacher16):
+    // per row block the lane's 32 teacher logits of its row are loaded
+    // (16-byte vectors of fp32 or 8-byte vectors of bf16, one block ahead,
+    // so that they are in flight while the previous block computes) and take
+    // the place of the paired GEMM's teacher accumulators: the teacher's
+    // half-tile statistics and label logit and the two KL sums come out as
+    // with paired rows. Only the student rows are stored. The teacher's half
+    // statistics go to partT, in the ring (idle once the main loop has
+    // drained). Non-temporal loads: the logits are read again only by the row
+    // pass, and the L2 holds the operand strips.
     float4* partT = reinterpret_cast<float4*>(smem);   // [2][256]
     auto load_t = [&](auto full_c, int i, f32x4 (&tv)[kFrag]) {
       constexpr bool kFull = decltype(full_c)::value;
       const int64_t row = static_cast<int64_t>(tc.m0) + wm * 128 + i * 16 + lrow;
-      const float* trow = g.lg.teacher_logits + (row < g.M ? row : g.M - 1) * g.lg.teacher_ld + colw;
+      const int64_t off = (row < g.M ? row : g.M - 1) * g.lg.teacher_ld + colw;
+      if constexpr (EPI == GemmEpilogue::LogitsTeacher16) {
+        const __bf16* trow = static_cast<const __bf16*>(g.lg.teacher_logits) + off;
 #pragma unroll
-      for (int j = 0; j < kFrag; ++j) {
-        if (kFull || j * 16 + 4 <= ncol) {
-          tv[j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(trow + j * 16));
-        } else {
+        for (int j = 0; j < kFrag; ++j) {
+          if (kFull || j * 16 + 4 <= ncol) {
+            const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(trow + j * 16));
+            tv[j][0] = __uint_as_float(w[0] << 16);
+            tv[j][1] = __uint_as_float(w[0] & 0xffff0000u);
+            tv[j][2] = __uint_as_float(w[1] << 16);
+            tv[j][3] = __uint_as_float(w[1] & 0xffff0000u);
+          } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) tv[j][e] = j * 16 + e < ncol ? trow[j * 16 + e] : 0.f;
+            for (int e = 0; e < 4; ++e)
+              tv[j][e] = j * 16 + e < ncol ? static_cast<float>(trow[j * 16 + e]) : 0.f;
+          }
+        }
+      } else {
+        const float* trow = static_cast<const float*>(g.lg.teacher_logits) + off;
+#pragma unroll
+        for (int j = 0; j < kFrag; ++j) {
+          if (kFull || j * 16 + 4 <= ncol) {
+            tv[j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(trow + j * 16));
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) tv[j][e] = j * 16 + e < ncol ? trow[j * 16 + e] : 0.f;
+          }
         }
       }
     };
@@ -1503,7 +1525,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
       }
     };
     const bool full = tc.n0 + kTile <= g.N;
-    if constexpr (EPI == GemmEpilogue::LogitsTeacher) {
+    if constexpr (kTeacherEpi) {
       static_assert(kRel, "the student rows beside Precomputed teacher logits are bf16");
       if (full) rows_teacher(SlotC<1>{});
       else rows_teacher(SlotC<0>{});
@@ -1554,7 +1576,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
           hp[2] = b.x;
         }
         if (teacher) g.lg.cross[(orow - prs) * g.lg.stats_ld + tc.ntile] = cx;
-        if constexpr (EPI == GemmEpilogue::LogitsTeacher) {
+        if constexpr (kTeacherEpi) {
           // the teacher row beside this student row: its tile statistics,
           // and the two KL sums relative to the two rows' tile maxima
           const float4 ta = partT[tid], tb = partT[256 + tid];
@@ -1595,6 +1617,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& g) {
   __global__ __launch_bounds__(kThreads, 1) void NAME(GemmArgs g) { gemm_body<T, AK, BK, EPI, LT, CT>(g); }
 ORDA_GEMM(gemm_kk_logits_bf16_bf16, __bf16, true, true, GemmEpilogue::Logits, __bf16, false)
 ORDA_GEMM(gemm_kk_logits_pre_bf16_bf16, __bf16, true, true, GemmEpilogue::LogitsTeacher, __bf16, false)
+ORDA_GEMM(gemm_kk_logits_pre16_bf16_bf16, __bf16, true, true, GemmEpilogue::LogitsTeacher16, __bf16, false)
 ORDA_GEMM(gemm_kk_logits_bf16_f32, __bf16, true, true, GemmEpilogue::Logits, float, false)
 ORDA_GEMM(gemm_km_store_bf16, __bf16, true, false, GemmEpilogue::StoreF32, float, false)
 ORDA_GEMM(gemm_km_accum_bf16, __bf16, true, false, GemmEpilogue::AccumF32, float, false)
@@ -1618,8 +1641,10 @@ GemmKernel select_kernel(const GemmArgs& g) {
   const bool bf = g.in_type == DType::BF16;
   if (g.epi == E::Logits) {
     if (!g.a_kmajor || !g.b_kmajor || g.c_trans) return nullptr;
-    if (g.lg.teacher_logits != nullptr)
-      return bf && g.logits_type == DType::BF16 ? gemm_kk_logits_pre_bf16_bf16 : nullptr;
+    if (g.lg.teacher_logits != nullptr) {
+      if (!bf || g.logits_type != DType::BF16) return nullptr;
+      return g.lg.teacher_type == DType::BF16 ? gemm_kk_logits_pre16_bf16_bf16 : gemm_kk_logits_pre_bf16_bf16;
+    }
     if (g.logits_type == DType::BF16) return bf ? gemm_kk_logits_bf16_bf16 : gemm_kk_logits_f32_bf16;
     return bf ? gemm_kk_logits_bf16_f32 : gemm_kk_logits_f32_f32;
   }
@@ -2233,7 +2258,8 @@ hipError_t launch_gemm_impl(const GemmArgs& g, hipStream_t stream, bool whole) {
     return hipErrorInvalidValue;
   if (g.epi == GemmEpilogue::Logits && g.lg.teacher_logits != nullptr &&
       (g.nprob != 1 || g.lg.pair_rows > 0 || g.lg.cross == nullptr || g.lg.teacher_ld % 4 ||
-       g.lg.teacher_ld < g.N || reinterpret_cast<uintptr_t>(g.lg.teacher_logits) % 16))
+       g.lg.teacher_ld < g.N ||
+       reinterpret_cast<uintptr_t>(g.lg.teacher_logits) % (g.lg.teacher_type == DType::BF16 ? 8 : 16)))
     return hipErrorInvalidValue;
   if (g.epi == GemmEpilogue::Logits && g.logits_type == DType::BF16 &&
       (g.lg.hmax == nullptr || g.lg.hmax_ld % 2 || g.lg.hmax_ld < 4 * ((g.N + kTile - 1) / kTile)))

@@ -26,7 +26,8 @@ enum class GemmEpilogue : int {
   AccumF32 = 1,    // C = alpha*(C + acc)                 (C is float)
   Logits = 2,      // C = acc stored in the logits dtype, plus per-row
                    // partial softmax statistics for every 256-column tile
-  LogitsTeacher = 3,   // internal: a Logits product with lg.teacher_logits
+  LogitsTeacher = 3,   // internal: a Logits product with fp32 lg.teacher_logits
+  LogitsTeacher16 = 4, // internal: a Logits product with bf16 lg.teacher_logits
                        // (launch_gemm selects it; callers pass Logits)
 };
 
@@ -70,15 +71,17 @@ struct LogitStatsArgs {
   // even. fp32 logits are stored as they are.
   float* hmax;
   int64_t hmax_ld;
-  // Precomputed teacher logits (one problem, bf16 inputs and bf16 logits,
-  // no paired rows): teacher_logits[r * teacher_ld + n] (fp32, 16-byte
-  // aligned, teacher_ld a multiple of 4) is the teacher logit of the
+  // Teacher logits beside the product (one problem, bf16 inputs and bf16
+  // logits, no paired rows): teacher_logits[r * teacher_ld + n], of type
+  // teacher_type (fp32: 16-byte aligned, teacher_ld a multiple of 4; bf16:
+  // 8-byte aligned, teacher_ld a multiple of 4), is the teacher logit of the
   // product's row r. The epilogue reads the tile's teacher logits and writes,
   // as for paired rows, the teacher rows' statistics (stats row M + r), label
   // logits (xy[M + r]) and the two KL sums (cross[r]); the teacher logits are
   // not stored, and hmax holds the student rows' maxima (side 0) only.
-  const float* teacher_logits;
+  const void* teacher_logits;
   int64_t teacher_ld;
+  DType teacher_type;
 };
 
 struct GemmArgs {
@@ -210,12 +213,14 @@ struct RowPassArgs {
   float inv_t;             // split mode: 1/T as given
   bool student_only;       // split mode: CE over student rows only
   bool fast_math;          // per-row logs and divisions by the hardware approximations
-  // The teacher rows are fp32 logits as they are (Precomputed teacher logits,
-  // or a Separate teacher's, read in place at pitch ld_t; a teacher gradient
-  // goes to the bf16 rows grad_t at pitch ld) beside bf16 student rows
-  // relative to their half-tile maxima, with the paired KL sums in cross
+  // The teacher rows are logits as they are, fp32 (Precomputed teacher
+  // logits, or a Separate teacher's) or bf16 (teacher_bf16: Precomputed
+  // teacher logits), read in place at pitch ld_t (a teacher gradient goes to
+  // the bf16 rows grad_t at pitch ld), beside bf16 student rows relative to
+  // their half-tile maxima, with the paired KL sums in cross
   // (LogitStatsArgs::teacher_logits).
   bool teacher_f32;
+  bool teacher_bf16;
 };
 
 hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t stream);

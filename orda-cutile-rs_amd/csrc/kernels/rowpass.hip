@@ -759,11 +759,14 @@ __global__ __launch_bounds__(kThreads) void row_consts_kernel(RowPassArgs a) {
 constexpr int kChunkVec = 1;                             // 8-element vectors per thread
 constexpr int kGradThreads = 128;
 constexpr int kChunk = kGradThreads * 8 * kChunkVec;     // columns per workgroup
-template <bool KL, bool TG, bool TF32>
+template <bool KL, bool TG, int TT>
 __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, int64_t chunks) {
-  // TF32: the teacher rows are fp32 logits as they are, read in place at
-  // pitch ld_t (Precomputed teacher logits, or a Separate teacher's); its
-  // gradient (TG) then goes to the bf16 rows grad_t at pitch ld.
+  // TT: the teacher rows' form. 0: bf16 relative to their half-tile maxima
+  // (the paired GEMM's rows, pitch ld, gradient in place); 1 (fp32) or 2
+  // (bf16): logits as they are, read in place at pitch ld_t (Precomputed
+  // teacher logits, or a Separate teacher's), the gradient (TG) to the bf16
+  // rows grad_t at pitch ld.
+  constexpr bool kRaw = TT != 0;
   constexpr int NV = 8;
   const int64_t r = blockIdx.x / chunks;
   const int64_t c0 = (blockIdx.x - r * chunks) * kChunk;
@@ -771,9 +774,10 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
   const int64_t y = a.labels[r];
   const int64_t v = a.v;
   __bf16* srow = static_cast<__bf16*>(a.student) + r * a.ld;
-  __bf16* trow = (KL || TG) && !TF32 ? static_cast<__bf16*>(a.teacher) + r * a.ld : nullptr;
-  const float* trowf = TF32 ? static_cast<const float*>(a.teacher) + r * a.ld_t : nullptr;
-  __bf16* gtrow = TF32 ? (TG ? static_cast<__bf16*>(a.grad_t) + r * a.ld : nullptr) : trow;
+  __bf16* trow = (KL || TG) && TT == 0 ? static_cast<__bf16*>(a.teacher) + r * a.ld : nullptr;
+  const float* trowf = TT == 1 ? static_cast<const float*>(a.teacher) + r * a.ld_t : nullptr;
+  const __bf16* trowh = TT == 2 ? static_cast<const __bf16*>(a.teacher) + r * a.ld_t : nullptr;
+  __bf16* gtrow = kRaw ? (TG ? static_cast<__bf16*>(a.grad_t) + r * a.ld : nullptr) : trow;
   if (y == a.ignore_index || y < 0 || y >= v) {   // zero gradient rows
     const float z[NV] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -796,13 +800,13 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
   // Both rows are stored relative to their half-tile maxima, in log2 units
   // (LogitStatsArgs::hmax): each 128-column half's maximum is folded into
   // the exponent offsets, and the T terms scale by 1/T. fp32 teacher rows
-  // (TF32) are logits as they are: scale log2(e)/T, no maximum.
+  // (kRaw) are logits as they are: scale log2(e)/T, no maximum.
   auto offs = [&](float hs, float ht) {
-    return float4{fmaf(hs, kLog2e, k.x), fmaf(hs, it2, k.y), TF32 ? k.z : fmaf(ht, it2, k.z),
-                  TF32 ? k.w : fmaf(ht, kLog2e, k.w)};
+    return float4{fmaf(hs, kLog2e, k.x), fmaf(hs, it2, k.y), kRaw ? k.z : fmaf(ht, it2, k.z),
+                  kRaw ? k.w : fmaf(ht, kLog2e, k.w)};
   };
-  const float eTt = TF32 ? it2 : inv_t;
-  const float e1t = TF32 ? kLog2e : 1.f;
+  const float eTt = kRaw ? it2 : inv_t;
+  const float e1t = kRaw ? kLog2e : 1.f;
   auto elem = [&](float xs, float xt, const float4& o, float& g, float& gt) {
     g = fmaf(sgn, __builtin_amdgcn_exp2f(xs + o.x), k0);
     if (KL) g += __builtin_amdgcn_exp2f(fmaf(xs, inv_t, o.y)) - __builtin_amdgcn_exp2f(fmaf(xt, eTt, o.z));
@@ -814,7 +818,8 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
   float xs_y = 0.f, xt_y = 0.f;
   if (owner) {
     xs_y = static_cast<float>(srow[y]);
-    if (TF32) xt_y = trowf[y];
+    if (TT == 1) xt_y = trowf[y];
+    else if (TT == 2) xt_y = static_cast<float>(trowh[y]);
     else if (KL || TG) xt_y = static_cast<float>(trow[y]);
   }
   // Half-tile maxima, loaded first (ahead of the logits, so that no wait
@@ -839,7 +844,7 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
     const int64_t j = c0 + (static_cast<int64_t>(q) * kGradThreads + tid) * NV;
     if (j < v) {
       rs[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(srow + j));
-      if (TF32) {
+      if (TT == 1) {
         if (j + NV <= v) {
           rt[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(trowf + j));
           rt2[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(trowf + j) + 1);
@@ -848,6 +853,20 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
           for (int i = 0; i < 4; ++i) {
             rt[q][i] = j + i < v ? __float_as_uint(trowf[j + i]) : 0u;
             rt2[q][i] = j + 4 + i < v ? __float_as_uint(trowf[j + 4 + i]) : 0u;
+          }
+        }
+      } else if (TT == 2) {
+        // 8 bf16 logits a 16-byte vector; single elements where it would
+        // pass the row's end (the pitch is only a multiple of 8 elements)
+        if (j + NV <= v) {
+          rt[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(trowh + j));
+        } else {
+          const uint16_t* h16 = reinterpret_cast<const uint16_t*>(trowh + j);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = j + 2 * i < v ? h16[2 * i] : 0u;
+            const uint32_t hi = j + 2 * i + 1 < v ? h16[2 * i + 1] : 0u;
+            rt[q][i] = lo | (hi << 16);
           }
         }
       } else if (KL || TG) {
@@ -861,7 +880,7 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
     if (j >= v) continue;
     float xs[NV], xt[NV] = {};
     Vec<__bf16>::unpack(rs[q], xs);
-    if (TF32) {
+    if (TT == 1) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         xt[i] = __uint_as_float(rt[q][i]);
@@ -1304,15 +1323,16 @@ hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
   const bool kl = a.kl && has_t;
   const bool tg = a.teacher_grad && has_t;
   if ((a.teacher_ce || kl || tg) && a.stats_t == nullptr) return hipErrorInvalidValue;
-  if (a.teacher_f32) {
-    // bf16 student rows (relative to their half-tile maxima) beside fp32
-    // teacher logits read in place at pitch ld_t; the statistics and KL sums
+  if (a.teacher_f32 || a.teacher_bf16) {
+    // bf16 student rows (relative to their half-tile maxima) beside fp32 or
+    // bf16 teacher logits read in place at pitch ld_t; the statistics and KL sums
     // of both come from the logits GEMM's epilogue. The teacher gradient, if
     // any, goes to the bf16 rows grad_t (pitch ld).
     if (!has_t || a.grad_s != nullptr || (tg && a.grad_t == nullptr) || a.cross == nullptr ||
         a.row_consts == nullptr || a.ltype != DType::BF16 || a.hmax_s == nullptr ||
         a.hmax_t != nullptr || a.hmax_ld % 2 || reinterpret_cast<uintptr_t>(a.hmax_s) % 8 ||
-        a.ld_t % 4 || a.ld_t < a.v || reinterpret_cast<uintptr_t>(a.teacher) % 16)
+        a.ld_t % (a.teacher_bf16 ? 8 : 4) || a.ld_t < a.v ||
+        reinterpret_cast<uintptr_t>(a.teacher) % 16 || (a.teacher_f32 && a.teacher_bf16))
       return hipErrorInvalidValue;
     const int64_t chunks = (a.v + kChunk - 1) / kChunk;
     const int64_t blocks = a.n_rows * chunks;
@@ -1321,16 +1341,20 @@ hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
     const dim3 ggrid(static_cast<unsigned>(blocks));
     if (kl && tg) {
       hipLaunchKernelGGL((row_consts_kernel<true, true>), cgrid, dim3(kThreads), 0, s, a);
-      hipLaunchKernelGGL((row_grad_kernel<true, true, true>), ggrid, dim3(kGradThreads), 0, s, a, chunks);
+      hipLaunchKernelGGL((a.teacher_bf16 ? row_grad_kernel<true, true, 2> : row_grad_kernel<true, true, 1>), ggrid,
+                         dim3(kGradThreads), 0, s, a, chunks);
     } else if (kl) {
       hipLaunchKernelGGL((row_consts_kernel<true, false>), cgrid, dim3(kThreads), 0, s, a);
-      hipLaunchKernelGGL((row_grad_kernel<true, false, true>), ggrid, dim3(kGradThreads), 0, s, a, chunks);
+      hipLaunchKernelGGL((a.teacher_bf16 ? row_grad_kernel<true, false, 2> : row_grad_kernel<true, false, 1>), ggrid,
+                         dim3(kGradThreads), 0, s, a, chunks);
     } else if (tg) {
       hipLaunchKernelGGL((row_consts_kernel<false, true>), cgrid, dim3(kThreads), 0, s, a);
-      hipLaunchKernelGGL((row_grad_kernel<false, true, true>), ggrid, dim3(kGradThreads), 0, s, a, chunks);
+      hipLaunchKernelGGL((a.teacher_bf16 ? row_grad_kernel<false, true, 2> : row_grad_kernel<false, true, 1>), ggrid,
+                         dim3(kGradThreads), 0, s, a, chunks);
     } else {
       hipLaunchKernelGGL((row_consts_kernel<false, false>), cgrid, dim3(kThreads), 0, s, a);
-      hipLaunchKernelGGL((row_grad_kernel<false, false, true>), ggrid, dim3(kGradThreads), 0, s, a, chunks);
+      hipLaunchKernelGGL((a.teacher_bf16 ? row_grad_kernel<false, false, 2> : row_grad_kernel<false, false, 1>), ggrid,
+                         dim3(kGradThreads), 0, s, a, chunks);
     }
     return hipGetLastError();
   }
@@ -1349,19 +1373,19 @@ hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     if (kl && tg) {
       hipLaunchKernelGGL((row_consts_kernel<true, true>), cgrid, dim3(kThreads), 0, s, a);
-      hipLaunchKernelGGL((row_grad_kernel<true, true, false>), dim3(static_cast<unsigned>(blocks)),
+      hipLaunchKernelGGL((row_grad_kernel<true, true, 0>), dim3(static_cast<unsigned>(blocks)),
                          dim3(kGradThreads), 0, s, a, chunks);
     } else if (kl) {
       hipLaunchKernelGGL((row_consts_kernel<true, false>), cgrid, dim3(kThreads), 0, s, a);
-      hipLaunchKernelGGL((row_grad_kernel<true, false, false>), dim3(static_cast<unsigned>(blocks)),
+      hipLaunchKernelGGL((row_grad_kernel<true, false, 0>), dim3(static_cast<unsigned>(blocks)),
                          dim3(kGradThreads), 0, s, a, chunks);
     } else if (tg) {
       hipLaunchKernelGGL((row_consts_kernel<false, true>), cgrid, dim3(kThreads), 0, s, a);
-      hipLaunchKernelGGL((row_grad_kernel<false, true, false>), dim3(static_cast<unsigned>(blocks)),
+      hipLaunchKernelGGL((row_grad_kernel<false, true, 0>), dim3(static_cast<unsigned>(blocks)),
                          dim3(kGradThreads), 0, s, a, chunks);
     } else {
       hipLaunchKernelGGL((row_consts_kernel<false, false>), cgrid, dim3(kThreads), 0, s, a);
-      hipLaunchKernelGGL((row_grad_kernel<false, false, false>), dim3(static_cast<unsigned>(blocks)),
+      hipLaunchKernelGGL((row_grad_kernel<false, false, 0>), dim3(static_cast<unsigned>(blocks)),
                          dim3(kGradThreads), 0, s, a, chunks);
     }
     return hipGetLastError();

@@ -134,28 +134,36 @@ def test_precomputed_logits_with_bf16_hidden(torch_dev, tl_dtype, v, view):
     check_output(got, ref, kind="bf16")
 
 
-@pytest.mark.parametrize("bt,v,offset,pad,chunk,w_t", [
-    (160, 1004, 0, 0, 48, None),      # V % 8 = 4: a ragged last tile, a partial last vector
-    (300, 2052, 4, 8, 128, 0.6),      # pitch V + 8 (a multiple of 4, not 8), base 16 bytes in
-    (257, 4096, 8, 8, None, 0.6),     # full tiles, M not a multiple of 256
-    (96, 1000, 3, 5, 32, None),       # misaligned view: converted instead
+@pytest.mark.parametrize("tl_dtype,bt,v,offset,pad,chunk,w_t", [
+    (None, 160, 1004, 0, 0, 48, None),    # V % 8 = 4: a ragged last tile, a partial last vector
+    (None, 300, 2052, 4, 8, 128, 0.6),    # pitch V + 8 (a multiple of 4, not 8), base 16 bytes in
+    (None, 257, 4096, 8, 8, None, 0.6),   # full tiles, M not a multiple of 256
+    (None, 96, 1000, 3, 5, 32, None),     # misaligned view: converted instead
+    ("bf16", 160, 1000, 0, 0, 48, None),  # bf16 logits: a ragged last tile
+    ("bf16", 300, 2056, 8, 8, 128, 0.6),  # bf16, pitch V + 8, base 16 bytes in
+    ("bf16", 257, 4096, 0, 0, None, 0.6), # bf16, full tiles
+    ("bf16", 96, 1004, 0, 0, 32, None),   # bf16 at a pitch of 4 mod 8: converted instead
 ])
-def test_precomputed_fp32_logits_in_the_bf16_gemm_epilogue(torch_dev, bt, v, offset, pad, chunk,
-                                                           w_t):
-    """fp32 Precomputed logits beside bf16 hidden states with a KL term,
-    16-byte aligned with a pitch of a multiple of 4: the logits GEMM reads
-    each tile's teacher logits in its epilogue (teacher statistics, label
-    logit and KL sums there), the student logits are stored in bf16 and the
-    row pass reads the teacher rows in place. Ignored rows, label smoothing,
-    T != 1, the teacher CE term and views with their own pitch; the last case
-    is a view that is not 16-byte aligned (converted into staging instead)."""
+def test_precomputed_logits_in_the_bf16_gemm_epilogue(torch_dev, tl_dtype, bt, v, offset, pad,
+                                                      chunk, w_t):
+    """Precomputed logits beside bf16 hidden states with a KL term, fp32 at a
+    pitch of a multiple of 4 or bf16 at a multiple of 8, 16-byte aligned: the
+    logits GEMM reads each tile's teacher logits in its epilogue (teacher
+    statistics, label logit and KL sums there), the student logits are
+    stored in bf16 and the row pass reads the teacher rows in place. Ignored
+    rows, label smoothing, T != 1, the teacher CE term and views with their
+    own pitch; a view that is not 16-byte aligned and bf16 logits at a pitch
+    of 4 mod 8 are converted into staging instead (the oracle is fed the same
+    bf16-rounded logits)."""
     h = 96
     s, w = bf16_round(normal((bt, h), 131)), bf16_round(normal((v, h), 132, 0.03))
     y = uniform_labels(bt, v, 133)
     y[::11] = -100
     tl = normal((bt, v), 134, 2.0)
     tl[np.arange(bt), np.maximum(y, 0)] += 4.0
-    tl_dev = strided(torch_dev, tl, offset, pad) if pad else dev(torch_dev, tl)
+    if tl_dtype == "bf16":
+        tl = bf16_round(tl)
+    tl_dev = strided(torch_dev, tl, offset, pad, tl_dtype) if pad else dev(torch_dev, tl, tl_dtype)
     opts = LossOptions(kd_weight=0.7, temperature=1.7, label_smoothing=0.1, teacher_ce_weight=w_t,
                        chunk_size=ChunkSize.Auto if chunk is None else ChunkSize.Fixed(chunk))
     got = H.distillation_loss(dev(torch_dev, s, "bf16"), dev(torch_dev, w, "bf16"),

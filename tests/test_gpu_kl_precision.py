@@ -50,6 +50,9 @@ T = 1.5
 PATHS = {
     "paired-bf16": ("tied", "bf16", 256, 128, 5000, 128, 0.05, 0.1, None),
     "precomputed-bf16": ("precomputed", "bf16", 256, 128, 5000, 128, 0.05, 0.1, None),
+    # the same with the teacher logits themselves in bf16 (the oracle gets them
+    # rounded the same way)
+    "precomputed-bf16-bf16-logits": ("precomputed16", "bf16", 256, 128, 5000, 128, 0.05, 0.1, None),
     "separate-bf16": ("separate", "bf16", 256, 128, 5000, 128, 0.05, 0.1, None),
     "separate-bf16-teacher-ce": ("separate", "bf16", 256, 128, 5000, 128, 0.05, 0.1, 0.3),
     "f32-fused-tied": ("tied", None, 256, 128, 5000, 128, 0.05, 0.5, None),
@@ -100,17 +103,21 @@ def test_small_kl(torch_dev, path, eps):
     if dtype == "bf16":
         s, th, w = bf16_round(s), bf16_round(th), bf16_round(w)
         tw = None if tw is None else bf16_round(tw)
-    if mode == "precomputed":
+    if mode in ("precomputed", "precomputed16"):
         # the student's logits (f64 over the bf16 values) plus noise of the
         # size a teacher eps away in the hidden states gives
         tl = (s.astype(np.float64) @ w.astype(np.float64).T +
               normal((bt, v), 46, eps * wsd * np.sqrt(h))).astype(np.float32)
+        if mode == "precomputed16":
+            tl = bf16_round(tl)
     opts = LossOptions(kd_weight=0.4, temperature=T, label_smoothing=0.1, teacher_ce_weight=w_t,
                        chunk_size=ChunkSize.Fixed(cs))
     if mode == "tied":
         tg, to = Teacher.Tied(gpu(torch_dev, th, dtype)), Teacher.Tied(th)
     elif mode == "precomputed":
         tg, to = Teacher.Precomputed(gpu(torch_dev, tl)), Teacher.Precomputed(tl)
+    elif mode == "precomputed16":
+        tg, to = Teacher.Precomputed(gpu(torch_dev, tl, "bf16")), Teacher.Precomputed(tl)
     else:
         tg = Teacher.Separate(gpu(torch_dev, th, dtype), gpu(torch_dev, tw, dtype))
         to = Teacher.Separate(th, tw)
