@@ -82,9 +82,9 @@ typedef struct {
  *                   it sets, so this one field is new.
  *   online_softmax  row statistics of Precomputed teacher logits that the
  *                   logits GEMM does not read (fp32 inputs, or logits that
- *                   are bf16, unaligned or at a pitch that is not a multiple
- *                   of 4; with bf16 inputs and a KL term, aligned fp32
- *                   logits are read in the GEMM's epilogue) in one online
+ *                   are unaligned or at a pitch that is not a multiple of 4
+ *                   (fp32) or 8 (bf16); with bf16 inputs and a KL term,
+ *                   aligned logits are read in the GEMM's epilogue) in one online
  *                   pass instead of a max pass and a sum pass. (The
  *                   chunk-launcher slot takes no KernelConfig; it always
  *                   uses the two passes.)

@@ -70,9 +70,9 @@ class KernelConfig:
       keeps only the fields a preset sets, so this field is added);
     * ``online_softmax``: one-pass row statistics of Precomputed teacher
       logits that the logits GEMM does not read in its epilogue (fp32
-      inputs, or logits that are bf16, unaligned or at a pitch that is not a
-      multiple of 4; the chunk-launcher slot takes no config and always uses
-      two passes);
+      inputs, or logits that are unaligned or at a pitch that is not a
+      multiple of 4 (fp32) or 8 (bf16); the chunk-launcher slot takes no
+      config and always uses two passes);
     * ``fp32_grad_weight_accumulation``, ``max_fused_size``: accepted and
       validated; grad_W always accumulates in fp32.
     """
