@@ -6,8 +6,10 @@ bf16-rounded values; tolerances as in tests/parity.py):
   (staged into a padded copy) and Hs != Ht;
 * Precomputed teacher logits next to bf16 hidden states: fp32 logits used in
   place, fp32 logits with an odd vocabulary (converted), bf16 logits
-  (converted), and a strided device view; fp32 logits read in the logits
-  GEMM's epilogue (ragged vocabularies, their own pitch, teacher CE);
+  (read in the logits GEMM's epilogue where aligned), and a strided device
+  view; fp32 and bf16 logits read in the logits GEMM's epilogue (ragged
+  vocabularies, their own pitch, teacher CE) or converted where they cannot
+  be;
 * a Separate teacher's fp32 logits read in the student logits GEMM's
   epilogue (bf16 inputs, KL, with and without teacher CE);
 * hidden widths that are not a multiple of 8 (padded staging of bf16);
