@@ -475,11 +475,13 @@ orda::DType logits_dtype(const LossPlan& P, bool paired) {
                                                              : orda::DType::F32;
 }
 
-// Precomputed teacher logits already in the logits dtype, with a pitch and a
-// width of a multiple of 8 elements and a 16-byte aligned base (the row pass
-// reads whole 16-byte vectors of 8 logits, so a narrower last vector would
-// read past the row, and past the tensor's storage on its last row): the row
-// pass reads them where they are instead of from a copy in the staging buffer.
+// Precomputed teacher logits that the row pass reads where they are instead
+// of from a copy in the staging buffer: those read beside the logits GEMM
+// (teacher_beside_gemm; the row pass takes single elements past a row's
+// end), or logits already in the logits dtype with a pitch and a width of a
+// multiple of 8 elements and a 16-byte aligned base (that row pass reads
+// whole 16-byte vectors of 8 logits, so a narrower last vector would read
+// past the row, and past the tensor's storage on its last row).
 bool teacher_logits_direct(const LossPlan& P, const Inputs& in) {
   return teacher_beside_gemm(P, in) ||
          (P.need_teacher && P.mode == ORDA_TEACHER_PRECOMPUTED && in.tl.t == logits_dtype(P, false) &&
