@@ -9,10 +9,11 @@ several 256-wide GEMM tiles in every dimension and take about a second. The
 point is the combinations: ragged K, M and N tails of every GEMM
 (grad_W computed transposed over the hidden rows included), chunk plans
 whose last chunk is short, staging groups of one chunk or many, odd hidden
-widths that are staged with padding, and the paired and unpaired row
-passes. Tolerances as in tests/parity.py: loss terms 1e-4 relative,
-gradients 1e-3 (fp32) or 2e-2 (bf16, the oracle fed the same bf16-rounded
-values), chunk plans bit-exact.
+widths that are staged with padding, the paired and unpaired row passes,
+and Precomputed logits in fp32 or (every other bf16 case) bf16, read in the
+logits GEMM's epilogue or converted. Tolerances as in tests/parity.py: loss
+terms 1e-4 relative, gradients 1e-3 (fp32) or 2e-2 (bf16, the oracle fed
+the same bf16-rounded values), chunk plans bit-exact.
 """
 import os
 
@@ -97,6 +98,11 @@ def test_shape_sweep(torch_dev, case):
     else:
         tl = normal((bt, v), seed + 3, 2.0)
         tl[np.arange(bt), np.maximum(y, 0)] += 4.0
+        # every other case with bf16 inputs passes bf16 teacher logits (the
+        # oracle gets them rounded the same way)
+        tl16 = dtype == "bf16" and seed % 2 == 1
+        if tl16:
+            tl = bf16_round(tl)
         t = Teacher.Precomputed(tl)
     opts = LossOptions(**kw)
 
@@ -109,7 +115,8 @@ def test_shape_sweep(torch_dev, case):
     elif mode == "separate":
         tg = Teacher.Separate(dev_t(t.hidden), dev_t(t.weight))
     else:
-        tg = Teacher.Precomputed(torch.from_numpy(np.ascontiguousarray(t.logits)).to(dev))
+        tl_dev = torch.from_numpy(np.ascontiguousarray(t.logits)).to(dev)
+        tg = Teacher.Precomputed(tl_dev.to(torch.bfloat16) if tl16 else tl_dev)
     print(f"case {case_id(case)}", flush=True)
     got = H.distillation_loss(dev_t(s), dev_t(w), torch.from_numpy(y).to(dev), tg, opts)
     ref = O.distillation_loss(s, w, y, t, opts)
