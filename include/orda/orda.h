@@ -61,7 +61,10 @@ typedef struct {
     int32_t mode;           /* orda_teacher_mode */
     orda_tensor hidden;     /* Tied [BT,H]; Separate [BT,Ht] */
     orda_tensor weight;     /* Separate [V,Ht] */
-    orda_tensor logits;     /* Precomputed [BT,V] */
+    orda_tensor logits;     /* Precomputed [BT,V], fp32 or bf16; beside bf16
+                               inputs read in place when 16-byte aligned
+                               with ld a multiple of 4 (fp32) or 8 (bf16),
+                               else copied into the staging buffer */
 } orda_teacher;
 
 /* KernelConfig (src/config.rs:45-63). Option<T> fields carry has_* flags.
