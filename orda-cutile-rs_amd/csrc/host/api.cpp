@@ -229,7 +229,9 @@ void check_view(const orda_tensor& t, const char* what) {
 }
 
 // Device-resident view of an input matrix with a pitch that is a multiple of
-// 8 elements and a 16-byte aligned base; copies only when needed.
+// 8 elements and a 16-byte aligned base; copies only when needed. A matrix
+// of no columns is staged as one column of zeros (pitch 8), so that a
+// product over an empty hidden width reads zeros (exactly 0 logits).
 DMat stage(orda_ctx* c, const orda_tensor& t, const std::string& name, const char* what) {
   DMat d;
   d.t = to_dtype(t.dtype, what);
@@ -240,7 +242,7 @@ DMat stage(orda_ctx* c, const orda_tensor& t, const std::string& name, const cha
   check_view(t, what);
   // Pass-through needs whole 16-byte chunks inside every row, including the
   // last one: pitch and width both multiples of 8 elements.
-  if (t.location == ORDA_DEVICE && ld % 8 == 0 && t.cols % 8 == 0 &&
+  if (t.location == ORDA_DEVICE && t.cols > 0 && ld % 8 == 0 && t.cols % 8 == 0 &&
       (reinterpret_cast<uintptr_t>(t.data) % 16) == 0) {
     d.p = t.data;
     d.ld = ld;
@@ -256,9 +258,10 @@ DMat stage(orda_ctx* c, const orda_tensor& t, const std::string& name, const cha
   } else {
     if (d.ld != t.cols)
       hip_check(hipMemsetAsync(buf, 0, t.rows * d.ld * es, c->stream), "hipMemsetAsync");
-    hip_check(hipMemcpy2DAsync(buf, d.ld * es, t.data, ld * es, t.cols * es, t.rows,
-                               hipMemcpyHostToDevice, c->stream),
-              "upload input");
+    if (t.cols > 0)
+      hip_check(hipMemcpy2DAsync(buf, d.ld * es, t.data, ld * es, t.cols * es, t.rows,
+                                 hipMemcpyHostToDevice, c->stream),
+                "upload input");
   }
   return d;
 }
@@ -586,8 +589,24 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
                        ? static_cast<float4*>(ws(c, "klpart", cap * row_pass_kl_blocks(v) * 16))
                        : nullptr;
   const float inv_t = 1.0f / P.T;
+  // The logits products' K: an empty hidden width (H = 0, or a Separate
+  // teacher's Ht = 0) runs over the single zero column its operands are
+  // staged with, so the logits are exactly 0; the backward products keep the
+  // true width (no output columns, nothing launched).
+  const int64_t kh = std::max<int64_t>(h, 1);
 
-  for (int64_t g0 = 0; g0 < nc; g0 += G) {
+  if (v == 0) {
+    // An empty vocabulary: every label is ignore_index (validated), so every
+    // loss term and every gradient is 0, and grad_W has no rows.
+    auto zero_out = [&](const OutMat& o, int64_t cols) {
+      if (cols > 0)
+        hip_check(hipMemset2DAsync(o.p, o.ld * 4, 0, cols * 4, bt, c->stream), "hipMemset2DAsync");
+    };
+    zero_out(in.gh, h);
+    if (P.has_ght) zero_out(in.ght, P.ht);
+    hip_check(hipMemsetAsync(row3_out, 0, 3 * bt * 4, c->stream), "hipMemsetAsync");
+  }
+  for (int64_t g0 = 0; v > 0 && g0 < nc; g0 += G) {
     const int64_t g1 = std::min(nc, g0 + G);
     const int64_t gs = g0 * cs;
     if (gs >= bt) break;
@@ -610,7 +629,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
     GemmArgs f{};
     f.M = btg;
     f.N = v;
-    f.K = h;
+    f.K = kh;
     f.lda = in.hs.ld;
     f.ldb = in.W.ld;
     f.ldc = ldl;
@@ -736,7 +755,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       GemmArgs t = f;
       t.nprob = 1;
       const bool sep = P.mode == ORDA_TEACHER_SEPARATE;
-      t.K = sep ? P.ht : h;
+      t.K = sep ? std::max<int64_t>(P.ht, 1) : kh;
       t.lda = in.th.ld;
       t.ldb = sep ? in.tw.ld : in.W.ld;
       t.prob[0] = {at(in.th.p, gs * in.th.ld, dt), sep ? in.tw.p : in.W.p, Lt};
@@ -1140,10 +1159,15 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
   }
 
   // ---- optional INT8 round trip of grad_W (api.rs:390-399)
+  // (V = 0: no rows to quantize; H = 0: rows of no codes, each with the
+  // scale of an all-zero row.)
   if (P.quant) {
-    uint8_t* keep = static_cast<uint8_t*>(ws(c, "keep", v));
-    hip_check(hipMemsetAsync(keep, 0, v, c->stream), "hipMemsetAsync");
-    hip_check(launch_mark_targets(in.labels, bt, P.ignore, keep, v, c->stream), "mark targets");
+    uint8_t* keep = nullptr;
+    if (v > 0) {
+      keep = static_cast<uint8_t*>(ws(c, "keep", v));
+      hip_check(hipMemsetAsync(keep, 0, v, c->stream), "hipMemsetAsync");
+      hip_check(launch_mark_targets(in.labels, bt, P.ignore, keep, v, c->stream), "mark targets");
+    }
     const bool want_codes = out->quant_codes.data != nullptr;
     const bool want_scales = out->quant_scales.data != nullptr;
     int8_t* codes = nullptr;
@@ -1153,7 +1177,9 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
       if (out->quant_codes.dtype != ORDA_I8 || out->quant_codes.rows != v || out->quant_codes.cols != h)
         fail(ORDA_ERR_INVALID, "quant_codes must be int8 (%lld, %lld)", static_cast<long long>(v),
              static_cast<long long>(h));
-      if (out->quant_codes.location == ORDA_DEVICE) {
+      if (v * h == 0) {
+        // no codes to write
+      } else if (out->quant_codes.location == ORDA_DEVICE) {
         codes = static_cast<int8_t*>(out->quant_codes.data);
         ldq = tensor_ld(out->quant_codes);
       } else {
@@ -1182,11 +1208,11 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
     q.seed = P.seed;
     q.grad_output = 1.0f;
     timed(c, ORDA_KERNEL_QUANT, [&] { return launch_quant(q, c->stream); });
-    if (want_codes && out->quant_codes.location != ORDA_DEVICE)
+    if (codes && out->quant_codes.location != ORDA_DEVICE)
       hip_check(hipMemcpy2DAsync(out->quant_codes.data, tensor_ld(out->quant_codes), codes, h, h, v,
                                  hipMemcpyDeviceToHost, c->stream),
                 "download codes");
-    if (want_scales && out->quant_scales.location != ORDA_DEVICE)
+    if (want_scales && v > 0 && out->quant_scales.location != ORDA_DEVICE)
       hip_check(hipMemcpyAsync(out->quant_scales.data, scales, v * 4, hipMemcpyDeviceToHost,
                                c->stream),
                 "download scales");

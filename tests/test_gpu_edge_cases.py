@@ -17,7 +17,10 @@ bf16-rounded values; tolerances as in tests/parity.py):
   not (staged);
 * paired student/teacher rows at a row count that is not a multiple of 16;
 * temperatures far from 1 and full label smoothing (alpha = 1);
-* stochastic INT8 rounding of grad_W through the whole path.
+* stochastic INT8 rounding of grad_W through the whole path;
+* an empty hidden width (H = 0, or a Separate teacher's Ht = 0) and an
+  empty vocabulary (V = 0, every label ignored), which the reference
+  accepts (src/api.rs:104-181).
 """
 import numpy as np
 import pytest
@@ -265,3 +268,71 @@ def test_stochastic_int8_through_the_path(torch_dev, dtype):
     else:
         check_output(got, ref, kind="bf16", skip_grad_weight=True)
         check_grad("grad_weight (dequantized)", to_np(got.grad_weight), ref.grad_weight, "bf16")
+
+
+EMPTY_CASES = [
+    # mode, dtype, H, Ht (Separate), V, inputs on the host, INT8 grad_W
+    ("tied", None, 0, None, 9, False, False),
+    ("tied", "bf16", 0, None, 9, False, True),
+    ("tied", None, 6, None, 0, False, True),
+    ("tied", None, 0, None, 0, True, False),
+    ("tied", None, 0, None, 9, True, True),
+    ("separate", None, 0, 5, 9, False, False),
+    ("separate", "bf16", 6, 0, 9, False, False),
+    ("separate", None, 6, 0, 9, True, False),
+    ("separate", None, 6, 5, 0, False, False),
+    ("precomputed", None, 0, None, 9, False, False),
+    ("precomputed", "bf16", 0, None, 9, False, True),
+    ("precomputed", None, 6, None, 0, False, False),
+]
+
+
+@pytest.mark.parametrize("mode,dtype,h,ht,v,host,quant", EMPTY_CASES,
+                         ids=[f"{c[0]}-{c[1] or 'f32'}-h{c[2]}" + (f"-ht{c[3]}" if c[3] is not None else "")
+                              + f"-v{c[4]}" + ("-host" if c[5] else "") + ("-int8" if c[6] else "")
+                              for c in EMPTY_CASES])
+def test_empty_hidden_width_or_vocabulary(torch_dev, mode, dtype, h, ht, v, host, quant):
+    """H = 0 gives logits of exactly 0 (every CE term log V, the Tied KL 0)
+    and gradients with no columns; V = 0 leaves only ignored rows (every
+    term 0, grad_hidden 0, grad_W with no rows); with INT8, rows of no
+    columns keep the scale of an all-zero row (src/quant.rs:52-57). All
+    against the oracle, including the per-row losses."""
+    bt = 5
+    rnd = bf16_round if dtype == "bf16" else (lambda a: a)
+    s = rnd(normal((bt, h), 311))
+    w = rnd(normal((v, h), 312, 0.1))
+    y = uniform_labels(bt, v, 313) if v > 0 else np.full(bt, -100, np.int64)
+    if mode == "tied":
+        t = Teacher.Tied(rnd(normal((bt, h), 314)))
+    elif mode == "separate":
+        t = Teacher.Separate(rnd(normal((bt, ht), 315)), rnd(normal((v, ht), 316, 0.1)))
+    else:
+        t = Teacher.Precomputed(normal((bt, v), 317, 2.0))
+    cfg = KernelConfig(quantize_grad_weight=quant)
+    opts = LossOptions(kd_weight=0.5, temperature=1.5, label_smoothing=0.1,
+                       teacher_ce_weight=None if mode == "precomputed" else 0.7, config=cfg)
+    print(f"case {mode} {dtype} h={h} ht={ht} v={v} host={host} quant={quant}", flush=True)
+    if host:
+        args = (s, w, y, t)
+    else:
+        if mode == "tied":
+            tg = Teacher.Tied(dev(torch_dev, t.hidden, dtype))
+        elif mode == "separate":
+            tg = Teacher.Separate(dev(torch_dev, t.hidden, dtype), dev(torch_dev, t.weight, dtype))
+        else:
+            tg = Teacher.Precomputed(dev(torch_dev, t.logits))
+        args = (dev(torch_dev, s, dtype), dev(torch_dev, w, dtype), dev(torch_dev, y), tg)
+    got = H.distillation_loss(*args, opts, rows=True, quant_codes=quant)
+    ref = O.distillation_loss(s, w, y, t, opts)
+    check_output(got, ref, kind="bf16" if dtype else "f32")
+    for k in ("row_nll_student", "row_nll_teacher", "row_kl"):
+        np.testing.assert_allclose(to_np(getattr(got, k)).reshape(-1), getattr(ref, k),
+                                   rtol=1e-4, atol=2e-6, err_msg=k)
+    if h == 0 and v > 0:
+        assert abs(got.student_ce - np.log(v)) <= 1e-5 * np.log(v)
+    if v == 0:
+        assert got.loss == 0.0 and np.all(to_np(got.grad_student_hidden) == 0.0)
+    if quant:
+        assert to_np(got.quant_codes).shape == (v, h)
+        np.testing.assert_array_equal(to_np(got.quant_scales).reshape(-1), ref.quant_scales)
+        np.testing.assert_array_equal(to_np(got.quant_codes), ref.quant_codes)
