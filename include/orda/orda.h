@@ -226,7 +226,9 @@ int32_t orda_ctx_reset_kernel_time(orda_ctx *ctx);
  * back with the loss at the call's one synchronisation, so an out-of-range
  * label is reported (with the reference's message, and ahead of any later
  * validation error, as in src/api.rs:104-181) after the kernels have run:
- * the output buffers then hold unspecified values. */
+ * the output buffers then hold unspecified values. As in the reference, BT
+ * must be > 0 while H, a Separate teacher's width and V may be 0 (V = 0
+ * leaves only ignored labels: every term and gradient is 0). */
 int32_t orda_distillation_loss(orda_ctx *ctx, const orda_tensor *student_hidden,
                                const orda_tensor *weight, const int64_t *labels,
                                int64_t n_labels, int32_t labels_location,
