@@ -117,3 +117,75 @@ def test_no_gpu_fails_loudly_not_silently():
     w = np.zeros((16, 8), np.float32)
     with pytest.raises(H.OrdaError):
         H.distillation_loss(s, w, np.zeros(4, np.int64), H.Teacher.Tied(s), H.LossOptions())
+
+
+STRUCTS = {
+    "orda_tensor": L.Tensor,
+    "orda_teacher": L.TeacherC,
+    "orda_kernel_config": L.KernelConfigC,
+    "orda_loss_options": L.LossOptionsC,
+    "orda_loss_output": L.LossOutputC,
+}
+
+
+def test_header_is_c_and_matches_the_python_layouts(tmp_path):
+    """include/orda/orda.h compiles as strict C11, a C caller links against
+    liborda_hip.so and gets the reference's defaults and chunk plan
+    (src/api.rs:49-64, src/resolver.rs:173-181), and every struct's size
+    and field offsets, as the C compiler lays them out, are those of the
+    ctypes mirror the Python binding passes."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    if os.environ.get("ORDA_HIP_LIB"):
+        pytest.skip("another build of the library (the sanitizer build links its runtimes)")
+    lines = []
+    for name, py in STRUCTS.items():
+        lines.append(f'  printf("{name} size %zu\\n", sizeof({name}));')
+        for field, _ in py._fields_:
+            lines.append(f'  printf("{name} {field} %zu\\n", offsetof({name}, {field}));')
+    src = "\n".join([
+        "#include <stddef.h>",
+        "#include <stdio.h>",
+        '#include "orda/orda.h"',
+        "int main(void) {",
+        *lines,
+        "  orda_loss_options o;",
+        "  orda_loss_options_default(&o);",
+        '  printf("defaults %g %g %g %lld %d %lld\\n", (double)o.student_ce_weight,',
+        "         (double)o.kd_weight, (double)o.temperature, (long long)o.ignore_index,",
+        "         o.reduction, (long long)o.config.max_fused_size);",
+        "  int64_t cs = 0, nc = 0;",
+        "  int32_t rc = orda_resolve_chunk_size(8192, 0, 0, 1, 131072, 0, 0, &cs, &nc);",
+        '  printf("plan %d %lld %lld\\n", rc, (long long)cs, (long long)nc);',
+        '  printf("abi %d\\n", orda_abi_version());',
+        "  return 0;",
+        "}",
+    ])
+    prog = tmp_path / "abi.c"
+    prog.write_text(src + "\n")
+    exe = tmp_path / "abi"
+    libdir = os.path.dirname(L.LIB_PATH)
+    subprocess.run([cc, "-std=c11", "-Wall", "-Wextra", "-Werror", "-pedantic",
+                    "-I", os.path.join(ROOT, "include"), str(prog), "-o", str(exe),
+                    "-L", libdir, "-l:" + os.path.basename(L.LIB_PATH),
+                    "-Wl,-rpath," + libdir], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    got = {}
+    for line in out.splitlines():
+        parts = line.split()
+        got[tuple(parts[:-1])] = parts[-1]
+    for name, py in STRUCTS.items():
+        assert int(got[(name, "size")]) == C.sizeof(py), name
+        for field, _ in py._fields_:
+            assert int(got[(name, field)]) == getattr(py, field).offset, f"{name}.{field}"
+    d = next(l.split()[1:] for l in out.splitlines() if l.startswith("defaults"))
+    ref = H.LossOptions()
+    assert (float(d[0]), float(d[1]), float(d[2]), int(d[3])) == \
+        (ref.student_ce_weight, ref.kd_weight, ref.temperature, ref.ignore_index)
+    assert d[4] == "0"   # ORDA_REDUCTION_MEAN
+    assert int(d[5]) == 65536 // 2
+    assert got[("plan", "0", "512")] == "16"
+    assert got[("abi",)] == str(L.load().orda_abi_version())
