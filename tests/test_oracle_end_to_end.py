@@ -36,6 +36,13 @@ def check_grad(param, analytic, eps, atol, rtol, loss_at):
     assert max_rel < 0.05, f"max relative grad error too high: {max_rel}"
 
 
+@pytest.fixture
+def dl():
+    """The distillation_loss under test: the oracle here (the same tests run
+    against the HIP library in tests/test_gpu_end_to_end.py)."""
+    return O.distillation_loss
+
+
 def base_opts(**kw):
     """tests/end_to_end.rs:80-87"""
     d = dict(student_ce_weight=1.0, kd_weight=0.5, temperature=1.5)
@@ -43,7 +50,7 @@ def base_opts(**kw):
     return LossOptions(**d)
 
 
-def test_tied_teacher_gradients_match_finite_difference():
+def test_tied_teacher_gradients_match_finite_difference(dl):
     # tests/end_to_end.rs:89-128
     bt, h, v = 6, 5, 7
     student = mat(bt, h, 1, 0.3)
@@ -52,7 +59,7 @@ def test_tied_teacher_gradients_match_finite_difference():
     labs = labels(bt, v, 4)
     teacher = Teacher.Tied(t_hidden)
     opts = base_opts(teacher_ce_weight=1.0, label_smoothing=0.1)
-    out = O.distillation_loss(student, weight, labs, teacher, opts)
+    out = dl(student, weight, labs, teacher, opts)
     kt = O.teacher_logits(teacher, weight)
     check_grad(student, out.grad_student_hidden, 1e-3, 1e-3, 1e-2,
                lambda s: O.forward_loss_f64(s, weight, labs, teacher, opts, kt))
@@ -63,7 +70,7 @@ def test_tied_teacher_gradients_match_finite_difference():
                lambda th: O.forward_loss_f64(student, weight, labs, Teacher.Tied(th), opts, kt))
 
 
-def test_separate_teacher_gradients_match_finite_difference():
+def test_separate_teacher_gradients_match_finite_difference(dl):
     # tests/end_to_end.rs:130-178
     bt, h, ht, v = 6, 5, 4, 7
     student = mat(bt, h, 11, 0.3)
@@ -73,7 +80,7 @@ def test_separate_teacher_gradients_match_finite_difference():
     labs = labels(bt, v, None)
     opts = base_opts(teacher_ce_weight=0.7)
     teacher = Teacher.Separate(t_hidden, t_weight)
-    out = O.distillation_loss(student, weight, labs, teacher, opts)
+    out = dl(student, weight, labs, teacher, opts)
     kt = O.teacher_logits(teacher, weight)
     check_grad(student, out.grad_student_hidden, 1e-3, 1e-3, 1e-2,
                lambda s: O.forward_loss_f64(s, weight, labs, teacher, opts, kt))
@@ -87,7 +94,7 @@ def test_separate_teacher_gradients_match_finite_difference():
                                              Teacher.Separate(t_hidden, tw), opts, kt))
 
 
-def test_precomputed_teacher_gradients_match_finite_difference():
+def test_precomputed_teacher_gradients_match_finite_difference(dl):
     # tests/end_to_end.rs:180-204
     bt, h, v = 6, 5, 7
     student = mat(bt, h, 21, 0.3)
@@ -96,7 +103,7 @@ def test_precomputed_teacher_gradients_match_finite_difference():
     labs = labels(bt, v, 5)
     opts = base_opts()
     teacher = Teacher.Precomputed(t_logits)
-    out = O.distillation_loss(student, weight, labs, teacher, opts)
+    out = dl(student, weight, labs, teacher, opts)
     assert out.grad_teacher_hidden is None and out.grad_teacher_weight is None
     check_grad(student, out.grad_student_hidden, 1e-3, 1e-3, 1e-2,
                lambda s: O.loss_only_f64(s, weight, labs, teacher, opts))
@@ -104,7 +111,7 @@ def test_precomputed_teacher_gradients_match_finite_difference():
                lambda w: O.loss_only_f64(student, w, labs, teacher, opts))
 
 
-def test_pure_student_ce_no_teacher_term():
+def test_pure_student_ce_no_teacher_term(dl):
     # tests/end_to_end.rs:206-228
     bt, h, v = 8, 4, 6
     student = mat(bt, h, 31, 0.3)
@@ -112,13 +119,13 @@ def test_pure_student_ce_no_teacher_term():
     labs = labels(bt, v, None)
     teacher = Teacher.Tied(np.zeros((bt, h), np.float32))
     opts = LossOptions(kd_weight=0.0, teacher_ce_weight=0.0)
-    out = O.distillation_loss(student, weight, labs, teacher, opts)
+    out = dl(student, weight, labs, teacher, opts)
     assert out.teacher_ce == 0.0 and out.kl == 0.0
     check_grad(student, out.grad_student_hidden, 1e-3, 1e-3, 1e-2,
                lambda s: O.loss_only_f64(s, weight, labs, teacher, opts))
 
 
-def test_chunking_is_exact_invariant():
+def test_chunking_is_exact_invariant(dl):
     # tests/end_to_end.rs:230-278
     bt, h, v = 16, 5, 9
     student = mat(bt, h, 41, 0.3)
@@ -127,7 +134,7 @@ def test_chunking_is_exact_invariant():
     labs = labels(bt, v, 3)
 
     def mk(cs):
-        return O.distillation_loss(student, weight, labs, teacher,
+        return dl(student, weight, labs, teacher,
                                    base_opts(chunk_size=cs, teacher_ce_weight=1.0))
     full = mk(ChunkSize.Fixed(bt))
     for other in (mk(ChunkSize.Fixed(1)), mk(ChunkSize.Fixed(3)), mk(ChunkSize.Auto)):
@@ -136,7 +143,7 @@ def test_chunking_is_exact_invariant():
         assert np.max(np.abs(full.grad_student_hidden - other.grad_student_hidden)) < 1e-5
 
 
-def test_loss_components_and_total_are_consistent():
+def test_loss_components_and_total_are_consistent(dl):
     # tests/end_to_end.rs:280-311
     bt, h, v = 10, 4, 8
     student = mat(bt, h, 51, 0.3)
@@ -146,7 +153,7 @@ def test_loss_components_and_total_are_consistent():
     w_s, w_t, kd = 1.0, 0.8, 0.5
     opts = LossOptions(student_ce_weight=w_s, teacher_ce_weight=w_t, kd_weight=kd,
                        temperature=2.0)
-    out = O.distillation_loss(student, weight, labs, teacher, opts)
+    out = dl(student, weight, labs, teacher, opts)
     f32 = np.float32
     recon = f32(w_s) * f32(out.student_ce) + f32(w_t) * f32(out.teacher_ce) + \
         f32(kd) * f32(out.kl)
@@ -154,7 +161,7 @@ def test_loss_components_and_total_are_consistent():
     assert abs(np.float32(O.loss_only_f64(student, weight, labs, teacher, opts)) - out.loss) < 1e-3
 
 
-def test_sum_reduction_is_mean_times_token_count():
+def test_sum_reduction_is_mean_times_token_count(dl):
     # tests/end_to_end.rs:313-358
     bt, h, v = 8, 4, 6
     student = mat(bt, h, 61, 0.3)
@@ -162,24 +169,24 @@ def test_sum_reduction_is_mean_times_token_count():
     teacher = Teacher.Tied(mat(bt, h, 63, 0.3))
     labs = labels(bt, v, 4)
     n_valid = float(np.sum(labs != -100))
-    mean = O.distillation_loss(student, weight, labs, teacher,
+    mean = dl(student, weight, labs, teacher,
                                base_opts(reduction=Reduction.Mean, teacher_ce_weight=1.0))
-    summ = O.distillation_loss(student, weight, labs, teacher,
+    summ = dl(student, weight, labs, teacher,
                                base_opts(reduction=Reduction.Sum, teacher_ce_weight=1.0))
     assert abs(summ.loss - mean.loss * n_valid) < 1e-3
     assert np.all(np.abs(summ.grad_weight - mean.grad_weight * n_valid) < 1e-3)
 
 
-def test_int8_quant_grad_w_is_close_but_lossy():
+def test_int8_quant_grad_w_is_close_but_lossy(dl):
     # tests/end_to_end.rs:360-417
     bt, h, v = 8, 4, 20
     student = mat(bt, h, 71, 0.3)
     weight = mat(v, h, 72, 0.2)
     teacher = Teacher.Tied(mat(bt, h, 73, 0.3))
     labs = labels(bt, v, None)
-    exact = O.distillation_loss(student, weight, labs, teacher, base_opts(teacher_ce_weight=1.0))
+    exact = dl(student, weight, labs, teacher, base_opts(teacher_ce_weight=1.0))
     cfg = KernelConfig(quantize_grad_weight=True)
-    quant = O.distillation_loss(student, weight, labs, teacher,
+    quant = dl(student, weight, labs, teacher,
                                 base_opts(config=cfg, teacher_ce_weight=1.0))
     assert abs(exact.loss - quant.loss) < 1e-6
     max_abs = float(np.max(np.abs(exact.grad_weight - quant.grad_weight)))
