@@ -5,7 +5,9 @@ The chunked row passes (paired bf16 logits: 1024-column blocks; fp32 logits
 above 2^25 logits per block: 512-column blocks) and the logits GEMM's last,
 partial 256-column tile meet a vocabulary that is a multiple of none of them
 (nor of 8, so the logits pitch is padded), with labels in the last columns
-and ignored rows. Small hidden widths keep the oracle's products cheap (run on
+and ignored rows; and vocabularies past 131072 (152064 to 262147) in every
+teacher mode, where a row has more tile statistics than the per-row merge
+holds at once. Small hidden widths keep the oracle's products cheap (run on
 the host's cores; results bitwise the same as one thread). Tolerances as in
 tests/parity.py.
 """
@@ -62,6 +64,22 @@ CASES = {
     "separate-bf16-large-logits-ce": ("separate", "bf16", 600, 800, 720, 5003,
                                       dict(kd_weight=0.0, teacher_ce_weight=0.5,
                                            label_smoothing=0.1), 0.4),
+    # Vocabularies past 131072 (more than 512 tile statistics per row: the
+    # per-row merge reads them in several passes): the paired bf16 pass at
+    # Qwen2's 152064, fp32 logits through the chunked fp32 pass (above 2^25
+    # logits per block), a Separate teacher's logits and Precomputed fp32
+    # logits read in the bf16 logits GEMM's epilogue, Precomputed logits
+    # through the segmented statistics of the fp32 pass.
+    "tied-bf16-paired-v152064": ("tied", "bf16", 96, 24, 24, 152064,
+                                 dict(kd_weight=0.4, temperature=1.5, label_smoothing=0.1)),
+    "tied-f32-chunked-v262147": ("tied", "f32", 160, 16, 16, 262147,
+                                 dict(kd_weight=0.5, temperature=2.0, label_smoothing=0.1)),
+    "separate-bf16-beside-v200003": ("separate", "bf16", 128, 24, 40, 200003,
+                                     dict(kd_weight=0.5, temperature=2.0, teacher_ce_weight=0.3)),
+    "precomputed-bf16-beside-v152064": ("precomputed", "bf16", 96, 24, 24, 152064,
+                                        dict(kd_weight=0.7, temperature=1.0)),
+    "precomputed-f32-chunked-v200003": ("precomputed", "f32", 176, 16, 16, 200003,
+                                        dict(kd_weight=0.7, temperature=1.0, label_smoothing=0.1)),
 }
 
 
@@ -87,8 +105,14 @@ def test_ragged_large_vocab(torch_dev, name):
 
     if mode == "tied":
         t_ref, t_gpu = Teacher.Tied(th), Teacher.Tied(dev_t(th))
-    else:
+    elif mode == "separate":
         t_ref, t_gpu = Teacher.Separate(th, tw), Teacher.Separate(dev_t(th), dev_t(tw))
+    else:
+        tl = normal((bt, v), 26, 2.0)
+        tl[np.arange(bt), np.maximum(y, 0)] += 8.0      # a peaked teacher
+        t_ref = Teacher.Precomputed(tl)
+        t_gpu = Teacher.Precomputed(torch.from_numpy(tl).to(dev))
+    print(f"case {name}", flush=True)
     opts = LossOptions(**kw)
     got = H.distillation_loss(dev_t(s), dev_t(w), torch.from_numpy(y).to(dev), t_gpu, opts)
     ref = O.distillation_loss(s, w, y, t_ref, opts)
