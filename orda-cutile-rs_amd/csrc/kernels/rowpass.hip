@@ -918,19 +918,59 @@ __global__ __launch_bounds__(kGradThreads) void row_grad_kernel(RowPassArgs a, i
 //                              Σ kd·T·(p_s^T − p_t^T), 0},
 // and row_kl_kernel adds a row's shares. Gradients go in place (GT float)
 // or to the separate gradient rows grad_s/grad_t; the teacher rows may have
-// their own pitch (Precomputed logits read in place). Ordinary loads and
-// stores: with the non-temporal hints of row_grad_kernel this pass measured
-// 10-20 % slower at V = 32000 and 65536 (the bf16 pass is 13 % faster with
-// them). One wave per block, one vector per thread: measured at the fp32
-// workloads (BT x V = 2048 x 32000, 4096 x 32000, 4096 x 65536) against
-// 128 and 256 threads (within 1.5 %) and 2 or 4 vectors per thread (1-5 %
-// slower).
+// their own pitch (Precomputed logits read in place). One wave per block,
+// one 16-byte vector (4 logits) of each row per thread, non-temporal loads
+// and stores: measured at the fp32 workloads (BT x V = 2048 x 32000,
+// 4096 x 32000, 4096 x 65536, two alternating passes) 0.174 / 0.338 /
+// 0.520 ms per pass, against 0.189 / 0.400 / 0.585 ms with two vectors per
+// row and thread and ordinary accesses, 0.212 / 0.418 / 0.613 ms with two
+// vectors and non-temporal accesses, 0.174 / 0.364 / 0.553 ms with one
+// vector and ordinary accesses. (The paired bf16 pass moves one 16-byte
+// vector per row and thread too, non-temporally.)
 constexpr int kF32Threads = 64;
-constexpr int kF32Vec = 1;                                 // 8-element vectors per thread
-constexpr int kF32Chunk = kF32Threads * 8 * kF32Vec;       // columns per workgroup
+constexpr int kF32Vec = 1;                                 // NV-element vectors per thread
+constexpr int kF32NV = 4;
+constexpr bool kF32Nt = true;
+constexpr int kF32Chunk = kF32Threads * kF32NV * kF32Vec;  // columns per workgroup
+// N gradient values to p (aligned to their size), as fp32 or packed bf16.
+template <bool NT, int N>
+__device__ __forceinline__ void store_vec(float* p, const float (&g)[N]) {
+#pragma unroll
+  for (int h = 0; h < N / 4; ++h) {
+    const u32x4 w = u32x4{__float_as_uint(g[4 * h]), __float_as_uint(g[4 * h + 1]),
+                          __float_as_uint(g[4 * h + 2]), __float_as_uint(g[4 * h + 3])};
+    if (NT) __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p) + h);
+    else reinterpret_cast<u32x4*>(p)[h] = w;
+  }
+}
+template <bool NT, int N>
+__device__ __forceinline__ void store_vec(__bf16* p, const float (&g)[N]) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  uint32_t w[N / 2];
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i)
+    w[i] = __builtin_bit_cast(uint32_t, bf16x2{static_cast<__bf16>(g[2 * i]),
+                                               static_cast<__bf16>(g[2 * i + 1])});
+  if constexpr (N == 8) {
+    const u32x4 v = u32x4{w[0], w[1], w[2], w[3]};
+    if (NT) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+    else *reinterpret_cast<u32x4*>(p) = v;
+  } else {
+    static_assert(N == 4, "4 or 8 values");
+    const u32x2 v = u32x2{w[0], w[1]};
+    if (NT) __builtin_nontemporal_store(v, reinterpret_cast<u32x2*>(p));
+    else *reinterpret_cast<u32x2*>(p) = v;
+  }
+}
+template <bool NT>
+__device__ __forceinline__ u32x4 load_vec(const float* p) {
+  if (NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return *reinterpret_cast<const u32x4*>(p);
+}
 template <typename GT, bool KL, bool TG>
 __global__ __launch_bounds__(kF32Threads) void row_grad_f32_kernel(RowPassArgs a, int64_t chunks) {
-  constexpr int NV = 8;
+  constexpr int NV = kF32NV;
+  constexpr int NH = NV / 4;   // 16-byte loads per row and thread
   __shared__ float sred[3][kF32Threads / 64];
   const int64_t r = blockIdx.x / chunks;
   const int64_t ci = blockIdx.x - r * chunks;
@@ -945,13 +985,15 @@ __global__ __launch_bounds__(kF32Threads) void row_grad_f32_kernel(RowPassArgs a
   GT* gtrow = TG ? static_cast<GT*>(a.grad_s ? a.grad_t : a.teacher) + r * a.ld : nullptr;
   auto col = [&](int q) { return c0 + (static_cast<int64_t>(q) * kF32Threads + tid) * NV; };
   if (y == a.ignore_index || y < 0 || y >= v) {   // zero gradient rows, no KL
-    const float z[NV] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float z[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) z[i] = 0.f;
 #pragma unroll
     for (int q = 0; q < kF32Vec; ++q) {
       const int64_t j = col(q);
       if (j < v) {
-        store8(gsrow + j, z);
-        if (TG) store8(gtrow + j, z);
+        store_vec<kF32Nt>(gsrow + j, z);
+        if (TG) store_vec<kF32Nt>(gtrow + j, z);
       }
     }
     if (KL && tid == 0) a.kl_part[r * chunks + ci] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -982,16 +1024,15 @@ __global__ __launch_bounds__(kF32Threads) void row_grad_f32_kernel(RowPassArgs a
     xs_y = srow[y];
     if (KL || TG) xt_y = trow[y];
   }
-  u32x4 rs[kF32Vec][2], rt[kF32Vec][2];
+  u32x4 rs[kF32Vec][NH], rt[kF32Vec][NH];
 #pragma unroll
   for (int q = 0; q < kF32Vec; ++q) {
     const int64_t j = col(q);
     if (j < v) {
-      rs[q][0] = reinterpret_cast<const u32x4*>(srow + j)[0];
-      rs[q][1] = reinterpret_cast<const u32x4*>(srow + j)[1];
-      if (KL || TG) {
-        rt[q][0] = reinterpret_cast<const u32x4*>(trow + j)[0];
-        rt[q][1] = reinterpret_cast<const u32x4*>(trow + j)[1];
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        rs[q][h] = load_vec<kF32Nt>(srow + j + 4 * h);
+        if (KL || TG) rt[q][h] = load_vec<kF32Nt>(trow + j + 4 * h);
       }
     }
   }
@@ -1016,8 +1057,8 @@ __global__ __launch_bounds__(kF32Threads) void row_grad_f32_kernel(RowPassArgs a
       g[i] = valid ? gi : 0.f;
       gt[i] = valid ? ti : 0.f;
     }
-    store8(gsrow + j, g);
-    if (TG) store8(gtrow + j, gt);
+    store_vec<kF32Nt>(gsrow + j, g);
+    if (TG) store_vec<kF32Nt>(gtrow + j, gt);
   }
   if (owner) {   // the label term, after this thread's own store of that column
     float gy = 0.f, ty = 0.f, c = 0.f, d = 0.f;
