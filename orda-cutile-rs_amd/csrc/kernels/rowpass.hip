@@ -1431,10 +1431,13 @@ hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
     }
     return hipGetLastError();
   }
-  // The chunked fp32 pass costs two more launches (~12 us) and streams ~8 %
-  // faster: the row-per-workgroup kernel serves small chunks (measured 16.5
-  // against 27 us at 256 rows x V = 8192).
-  const bool big = a.n_rows * a.v >= (int64_t{1} << 25);
+  // The chunked fp32 pass costs two more launches (~12 us) and streams
+  // faster: the row-per-workgroup kernel serves blocks of fewer than 20·2^20
+  // logits (Tied, fp32, one block of rows x V; fused against chunked:
+  // 256 x 8192 14.6 / 23.5 us, 512 x 16384 29.6 / 36.7 us, 1024 x 16000
+  // 48.4 / 58.4 us, 512 x 32000 54.0 / 55.9 us, 768 x 32000 90.2 / 79.1 us,
+  // 1024 x 32000 118.2 / 98.2 us).
+  const bool big = a.n_rows * a.v >= (int64_t{20} << 20);
   if (big && a.ltype == DType::F32 && a.cross == nullptr && a.row_consts != nullptr &&
       (a.kl_part != nullptr || !kl) && (!(kl || tg || a.teacher_ce) || has_t)) {
     // fp32 logits: per-row constants, the chunked elementwise gradient with

@@ -57,7 +57,7 @@ PATHS = {
     "separate-bf16-teacher-ce": ("separate", "bf16", 256, 128, 5000, 128, 0.05, 0.1, 0.3),
     "f32-fused-tied": ("tied", None, 256, 128, 5000, 128, 0.05, 0.5, None),
     "f32-fused-separate": ("separate", None, 256, 128, 5000, 128, 0.05, 0.5, None),
-    # 512 x 65600 >= 2^25 logits per group: the chunked fp32 kernels
+    # 512 x 65600 >= 20·2^20 logits per group: the chunked fp32 kernels
     "f32-chunked-tied": ("tied", None, 512, 32, 65600, 512, 0.1, 0.5, None),
 }
 

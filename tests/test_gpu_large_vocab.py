@@ -2,7 +2,7 @@
 against the oracle.
 
 The chunked row passes (paired bf16 logits: 1024-column blocks; fp32 logits
-above 2^25 logits per block: 512-column blocks) and the logits GEMM's last,
+from 20·2^20 logits per block: 256-column blocks) and the logits GEMM's last,
 partial 256-column tile meet a vocabulary that is a multiple of none of them
 (nor of 8, so the logits pitch is padded), with labels in the last columns
 and ignored rows; and vocabularies past 131072 (152064 to 262147) in every
@@ -66,7 +66,7 @@ CASES = {
                                            label_smoothing=0.1), 0.4),
     # Vocabularies past 131072 (more than 512 tile statistics per row: the
     # per-row merge reads them in several passes): the paired bf16 pass at
-    # Qwen2's 152064, fp32 logits through the chunked fp32 pass (above 2^25
+    # Qwen2's 152064, fp32 logits through the chunked fp32 pass (above 20·2^20
     # logits per block), a Separate teacher's logits and Precomputed fp32
     # logits read in the bf16 logits GEMM's epilogue, Precomputed logits
     # through the segmented statistics of the fp32 pass.
