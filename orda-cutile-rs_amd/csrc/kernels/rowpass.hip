@@ -83,6 +83,7 @@ __device__ __forceinline__ Stat shfl_xor_stat(Stat s, int o) {
 }
 
 // Block-wide merge of per-thread partial stats; every thread gets the result.
+template <int TPB = kThreads>
 __device__ Stat block_merge(Stat s, float it2, Stat* scratch) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) s = merge(s, shfl_xor_stat(s, o), it2);
@@ -92,10 +93,11 @@ __device__ Stat block_merge(Stat s, float it2, Stat* scratch) {
   __syncthreads();
   Stat r = scratch[0];
 #pragma unroll
-  for (int w = 1; w < kThreads / 64; ++w) r = merge(r, scratch[w], it2);
+  for (int w = 1; w < TPB / 64; ++w) r = merge(r, scratch[w], it2);
   return r;
 }
 
+template <int TPB = kThreads>
 __device__ float block_sum(float v, float* scratch) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
@@ -105,17 +107,18 @@ __device__ float block_sum(float v, float* scratch) {
   __syncthreads();
   float r = 0.f;
 #pragma unroll
-  for (int w = 0; w < kThreads / 64; ++w) r += scratch[w];
+  for (int w = 0; w < TPB / 64; ++w) r += scratch[w];
   return r;
 }
 
+template <int TPB = kThreads>
 __device__ Stat load_row_stats(const float4* st, int64_t tiles, float it2, Stat* scratch) {
   Stat s{-INFINITY, 0.f, 0.f, 0.f};
-  for (int64_t t = threadIdx.x; t < tiles; t += kThreads) {
+  for (int64_t t = threadIdx.x; t < tiles; t += TPB) {
     const float4 v = st[t];
     s = merge(s, Stat{v.x, v.y, v.z, v.w}, it2);
   }
-  return block_merge(s, it2, scratch);
+  return block_merge<TPB>(s, it2, scratch);
 }
 
 // Vector of logits in storage type LT <-> fp32.
@@ -195,10 +198,10 @@ __device__ __forceinline__ double row_nll(const Stat& s, float xy, double alpha,
   return lse - static_cast<double>(xy);
 }
 
-template <typename LT, bool SPLIT>
-__global__ __launch_bounds__(kThreads) void row_pass_kernel(RowPassArgs a) {
-  __shared__ Stat sstat[kThreads / 64];
-  __shared__ float ssum[kThreads / 64];
+template <typename LT, bool SPLIT, int TPB>
+__global__ __launch_bounds__(TPB) void row_pass_kernel(RowPassArgs a) {
+  __shared__ Stat sstat[TPB / 64];
+  __shared__ float ssum[TPB / 64];
   const int64_t r = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t y = a.labels[r];
@@ -210,9 +213,9 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(RowPassArgs a) {
   const float inv_t = SPLIT ? a.inv_t : 1.0f / T;
   const float it2 = inv_t * kLog2e;
 
-  const Stat ss = load_row_stats(a.stats_s + r * a.stats_ld, a.stats_tiles, it2, sstat);
+  const Stat ss = load_row_stats<TPB>(a.stats_s + r * a.stats_ld, a.stats_tiles, it2, sstat);
   Stat st{-INFINITY, 0.f, 0.f, 0.f};
-  if (has_t) st = load_row_stats(a.stats_t + r * a.stats_ld, a.stats_tiles_t, it2, sstat);
+  if (has_t) st = load_row_stats<TPB>(a.stats_t + r * a.stats_ld, a.stats_tiles_t, it2, sstat);
 
   const double alpha = static_cast<double>(a.label_smoothing);
   // Per-row constants: p = exp2(x*log2e - off).
@@ -247,8 +250,13 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(RowPassArgs a) {
   // elements otherwise (nothing past column V is read).
   const bool vec = (reinterpret_cast<uintptr_t>(srow) & 15) == 0 &&
                    (!has_t || (reinterpret_cast<uintptr_t>(trow) & 15) == 0);
-  for (int64_t j0 = static_cast<int64_t>(tid) * NV; j0 < vpad; j0 += kThreads * NV) {
-    float xs[NV], xt[NV], gs[NV], gt[NV];
+  // SPLIT outputs (dense fp32 rows) leave as non-temporal 16-byte stores
+  // where this row's outputs are 16-byte aligned.
+  const bool ovec = SPLIT && (reinterpret_cast<uintptr_t>(gce_s) & 15) == 0 &&
+                    (!do_kl || (reinterpret_cast<uintptr_t>(gkl) & 15) == 0) &&
+                    (!do_tgrad || (reinterpret_cast<uintptr_t>(gce_t) & 15) == 0);
+  for (int64_t j0 = static_cast<int64_t>(tid) * NV; j0 < vpad; j0 += TPB * NV) {
+    float xs[NV], xt[NV], gs[NV], gt[NV], gk[NV];
     const bool whole = vec && j0 + NV <= a.v;
     if (whole) {
       VT::unpack(*reinterpret_cast<const typename VT::raw*>(srow + j0), xs);
@@ -288,17 +296,38 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(RowPassArgs a) {
         }
       }
       if (SPLIT) {
-        if (valid) {
-          gce_s[j] = g;
-          if (do_kl) gkl[j] = gkv;
-          if (do_tgrad) gce_t[j] = gtv;
-        }
+        gs[i] = g;
+        gk[i] = gkv;
+        gt[i] = gtv;
       } else {
         gs[i] = ignored ? 0.f : g + gkv;
         gt[i] = gtv;
       }
     }
-    if (!SPLIT) {
+    if (SPLIT) {
+      if (whole && ovec) {
+        typedef float f4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int h = 0; h < NV / 4; ++h) {
+          __builtin_nontemporal_store(f4{gs[4 * h], gs[4 * h + 1], gs[4 * h + 2], gs[4 * h + 3]},
+                                      reinterpret_cast<f4*>(gce_s + j0) + h);
+          if (do_kl)
+            __builtin_nontemporal_store(f4{gk[4 * h], gk[4 * h + 1], gk[4 * h + 2], gk[4 * h + 3]},
+                                        reinterpret_cast<f4*>(gkl + j0) + h);
+          if (do_tgrad)
+            __builtin_nontemporal_store(f4{gt[4 * h], gt[4 * h + 1], gt[4 * h + 2], gt[4 * h + 3]},
+                                        reinterpret_cast<f4*>(gce_t + j0) + h);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          if (j0 + i >= a.v) break;
+          gce_s[j0 + i] = gs[i];
+          if (do_kl) gkl[j0 + i] = gk[i];
+          if (do_tgrad) gce_t[j0 + i] = gt[i];
+        }
+      }
+    } else {
       if (whole) {
         *reinterpret_cast<typename VT::raw*>(srow + j0) = VT::pack(gs);
         if (do_tgrad) *reinterpret_cast<typename VT::raw*>(trow + j0) = VT::pack(gt);
@@ -313,13 +342,13 @@ __global__ __launch_bounds__(kThreads) void row_pass_kernel(RowPassArgs a) {
     }
   }
   if (SPLIT && !do_kl && a.grad_kl) {
-    for (int64_t j = tid; j < a.v; j += kThreads) gkl[j] = 0.f;
+    for (int64_t j = tid; j < a.v; j += TPB) gkl[j] = 0.f;
   }
 
   if (do_kl) {
-    cross = block_sum(cross, ssum);
-    sum_pt = block_sum(sum_pt, ssum);
-    sum_d = block_sum(sum_d, ssum);
+    cross = block_sum<TPB>(cross, ssum);
+    sum_pt = block_sum<TPB>(sum_pt, ssum);
+    sum_d = block_sum<TPB>(sum_d, ssum);
   }
   if (tid == 0) {
     const float xy_s = ignored ? 0.f : a.xy_s[r];
@@ -396,7 +425,7 @@ struct HalfRel {
 
 // The row pass of distillation_loss, specialised on the logits type LT, the
 // gradient type GT and whether the KL term (KL) and the teacher CE gradient
-// (TG) are present. Same results as row_pass_kernel<LT, false>, with the
+// (TG) are present. Same results as the unsplit row_pass_kernel, with the
 // per-element work cut down for the bandwidth-bound case:
 //  * the CE and KL weights are folded into the exponents,
 //      w_s·p_s = 2^(x_s·log2e − lse_s·log2e + log2|w_s|), likewise kd·T·p_s^T,
@@ -1128,6 +1157,7 @@ __global__ __launch_bounds__(kThreads) void row_kl_kernel(RowPassArgs a, int64_t
 }
 
 // ------------------------------------------------------------------ row stats
+template <int TPB = kThreads>
 __device__ float block_max(float v, float* scratch) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
@@ -1137,7 +1167,7 @@ __device__ float block_max(float v, float* scratch) {
   __syncthreads();
   float r = scratch[0];
 #pragma unroll
-  for (int w = 1; w < kThreads / 64; ++w) r = fmaxf(r, scratch[w]);
+  for (int w = 1; w < TPB / 64; ++w) r = fmaxf(r, scratch[w]);
   return r;
 }
 
@@ -1187,6 +1217,56 @@ __global__ __launch_bounds__(kThreads) void row_stats_kernel(RowStatsArgs a) {
     for (int64_t j = a.v + threadIdx.x; j < a.ldd; j += kThreads) dst[j] = static_cast<DT>(0.f);
   if (threadIdx.x == 0) {
     a.stats[r * a.stats_ld] = make_float4(s.m, s.d1, s.dT, s.sx);
+    if (a.labels) {
+      const int64_t y = a.labels[a.label_rows > 0 ? r % a.label_rows : r];
+      if (y != a.ignore_index && y >= 0 && y < a.v) a.xy[r] = static_cast<float>(src[y]);
+    }
+  }
+}
+
+// The chunk-launcher slot's statistics of whole rows (no converted copy):
+// two passes over the row, max then the exponential sums, by 1024 threads,
+// with 16-byte loads where every row is 16-byte aligned. (With 256 threads
+// and single-element loads the slot ran at 1.0-2.0 TB/s at 512-1024 rows.)
+constexpr int kWideThreads = 1024;
+template <typename ST, bool VEC>
+__global__ __launch_bounds__(kWideThreads) void row_stats_wide_kernel(RowStatsArgs a) {
+  __shared__ float sred[kWideThreads / 64];
+  const int64_t r = blockIdx.x;
+  const ST* src = static_cast<const ST*>(a.src) + r * a.lds;
+  const float it2 = a.inv_t * kLog2e;
+  using VT = Vec<ST>;
+  constexpr int NV = VT::N;
+  const int64_t nfull = VEC ? a.v / NV : 0;
+  auto each = [&](auto&& f) {
+    if constexpr (VEC) {
+      for (int64_t q = threadIdx.x; q < nfull; q += kWideThreads) {
+        float x[NV];
+        VT::unpack(*reinterpret_cast<const typename VT::raw*>(src + q * NV), x);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) f(x[i]);
+      }
+    }
+    for (int64_t j = nfull * NV + threadIdx.x; j < a.v; j += kWideThreads)
+      f(static_cast<float>(src[j]));
+  };
+  float m = -INFINITY, sx = 0.f;
+  each([&](float x) {
+    m = fmaxf(m, x);
+    sx += x;
+  });
+  m = block_max<kWideThreads>(m, sred);
+  const float o1 = -m * kLog2e, oT = -m * it2;
+  float d1 = 0.f, dT = 0.f;
+  each([&](float x) {
+    d1 += __builtin_amdgcn_exp2f(fmaf(x, kLog2e, o1));
+    dT += __builtin_amdgcn_exp2f(fmaf(x, it2, oT));
+  });
+  sx = block_sum<kWideThreads>(sx, sred);
+  d1 = block_sum<kWideThreads>(d1, sred);
+  dT = block_sum<kWideThreads>(dT, sred);
+  if (threadIdx.x == 0) {
+    a.stats[r * a.stats_ld] = make_float4(m, d1, dT, sx);
     if (a.labels) {
       const int64_t y = a.labels[a.label_rows > 0 ? r % a.label_rows : r];
       if (y != a.ignore_index && y >= 0 && y < a.v) a.xy[r] = static_cast<float>(src[y]);
@@ -1353,10 +1433,14 @@ hipError_t launch_row_pass(const RowPassArgs& a, hipStream_t s) {
     return hipErrorInvalidValue;
   dim3 grid(static_cast<unsigned>(a.n_rows));
   if (a.split) {   // any pitch and alignment
+    // 512 threads a row: at 512 x 131072 and 1024 x 32000 fp32 logits
+    // 0.470 and 0.220 ms per slot call, against 0.50 and 0.220 ms with 256
+    // threads and 0.468 and 0.242 ms with 1024 (bf16 within 3 % of each other).
+    constexpr int kSplitThreads = 512;
     if (a.ltype == DType::BF16)
-      hipLaunchKernelGGL((row_pass_kernel<__bf16, true>), grid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((row_pass_kernel<__bf16, true, kSplitThreads>), grid, dim3(kSplitThreads), 0, s, a);
     else
-      hipLaunchKernelGGL((row_pass_kernel<float, true>), grid, dim3(kThreads), 0, s, a);
+      hipLaunchKernelGGL((row_pass_kernel<float, true, kSplitThreads>), grid, dim3(kSplitThreads), 0, s, a);
     return hipGetLastError();
   }
   if (a.ld % 8) return hipErrorInvalidValue;
@@ -1517,6 +1601,15 @@ hipError_t launch_row_stats(const RowStatsArgs& a, hipStream_t s) {
     else if (sf) hipLaunchKernelGGL((row_stats_seg_kernel<float, __bf16, false>), g, dim3(kThreads), 0, s, a, nseg);
     else if (df) hipLaunchKernelGGL((row_stats_seg_kernel<__bf16, float, false>), g, dim3(kThreads), 0, s, a, nseg);
     else hipLaunchKernelGGL((row_stats_seg_kernel<__bf16, __bf16, false>), g, dim3(kThreads), 0, s, a, nseg);
+    return hipGetLastError();
+  }
+  if (!a.online && a.dst == nullptr) {
+    const int es = sf ? 4 : 2;
+    const bool vec = reinterpret_cast<uintptr_t>(a.src) % 16 == 0 && (a.lds * es) % 16 == 0;
+    if (sf && vec) hipLaunchKernelGGL((row_stats_wide_kernel<float, true>), grid, dim3(kWideThreads), 0, s, a);
+    else if (sf) hipLaunchKernelGGL((row_stats_wide_kernel<float, false>), grid, dim3(kWideThreads), 0, s, a);
+    else if (vec) hipLaunchKernelGGL((row_stats_wide_kernel<__bf16, true>), grid, dim3(kWideThreads), 0, s, a);
+    else hipLaunchKernelGGL((row_stats_wide_kernel<__bf16, false>), grid, dim3(kWideThreads), 0, s, a);
     return hipGetLastError();
   }
 #define ORDA_ROWSTATS(ONLINE)                                                                        \
