@@ -87,10 +87,12 @@ typedef struct {
  *                   logits GEMM does not read (fp32 inputs, or logits that
  *                   are unaligned or at a pitch that is not a multiple of 4
  *                   (fp32) or 8 (bf16); with bf16 inputs and a KL term,
- *                   aligned logits are read in the GEMM's epilogue) in one online
- *                   pass instead of a max pass and a sum pass. (The
- *                   chunk-launcher slot takes no KernelConfig; it always
- *                   uses the two passes.)
+ *                   aligned logits are read in the GEMM's epilogue) by the
+ *                   online-softmax merge: per 8192-column segment, each
+ *                   thread's sums relative to its own maximum, rescaled to
+ *                   the larger maximum as they merge, instead of a
+ *                   segment-wide maximum first. (The chunk-launcher slot
+ *                   takes no KernelConfig; it always uses the max first.)
  *   fp32_grad_weight_accumulation, max_fused_size: accepted and validated;
  *                   grad_W always accumulates in fp32 (the reference's
  *                   output is f32) and the tile widths are fixed. */

@@ -818,7 +818,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
       const int64_t nseg = row_stats_segments(v);
       r.stats_tiles = seg_s ? nseg : nst;
       r.stats_tiles_t = t_epi ? nst
-                        : P.mode == ORDA_TEACHER_PRECOMPUTED ? (P.online ? 1 : nseg)
+                        : P.mode == ORDA_TEACHER_PRECOMPUTED ? nseg
                         : seg_t ? nseg : nst;
       r.xy_s = xy;
       r.xy_t = xy + btg;

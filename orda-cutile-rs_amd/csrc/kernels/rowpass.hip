@@ -1284,9 +1284,10 @@ __global__ __launch_bounds__(kWideThreads) void row_stats_wide_kernel(RowStatsAr
 // and the sum pass read HBM once.
 constexpr int kSegCols = 8192;
 constexpr int kSegPer = kSegCols / kThreads;   // 32 columns per thread
-template <typename ST, typename DT, bool VEC>
+template <typename ST, typename DT, bool VEC, bool ONLINE>
 __global__ __launch_bounds__(kThreads) void row_stats_seg_kernel(RowStatsArgs a, int64_t nseg) {
   __shared__ float sred[kThreads / 64];
+  __shared__ Stat sstat[kThreads / 64];
   const int64_t r = blockIdx.x / nseg;
   const int64_t sg = blockIdx.x - r * nseg;
   const int64_t c0 = sg * kSegCols;
@@ -1364,6 +1365,27 @@ __global__ __launch_bounds__(kThreads) void row_stats_seg_kernel(RowStatsArgs a,
       }
     }
   }
+  if (dst && sg == nseg - 1)
+    for (int64_t j = a.v + threadIdx.x; j < a.ldd; j += kThreads) dst[j] = static_cast<DT>(0.f);
+  if constexpr (ONLINE) {
+    // KernelConfig::online_softmax: no block-wide maximum before the sums.
+    // Each thread forms {max, sums} of its own columns relative to its own
+    // maximum, and the block merges the threads' states, rescaling each
+    // state's sums to the larger maximum (the online softmax merge).
+    float d1 = 0.f, dT = 0.f;
+    if (m != -INFINITY) {
+      const float o1 = -m * kLog2e, oT = -m * it2;
+#pragma unroll
+      for (int k = 0; k < kSegPer; ++k) {
+        // e^(-inf) = 0 for the columns past V
+        d1 += __builtin_amdgcn_exp2f(fmaf(x[k], kLog2e, o1));
+        dT += __builtin_amdgcn_exp2f(fmaf(x[k], it2, oT));
+      }
+    }
+    const Stat st = block_merge(Stat{m, d1, dT, sx}, it2, sstat);
+    if (threadIdx.x == 0) a.stats[r * a.stats_ld + sg] = make_float4(st.m, st.d1, st.dT, st.sx);
+    return;
+  }
   m = block_max(m, sred);
   const float o1 = -m * kLog2e, oT = -m * it2;
   float d1 = 0.f, dT = 0.f;
@@ -1376,8 +1398,6 @@ __global__ __launch_bounds__(kThreads) void row_stats_seg_kernel(RowStatsArgs a,
   sx = block_sum(sx, sred);
   d1 = block_sum(d1, sred);
   dT = block_sum(dT, sred);
-  if (dst && sg == nseg - 1)
-    for (int64_t j = a.v + threadIdx.x; j < a.ldd; j += kThreads) dst[j] = static_cast<DT>(0.f);
   if (threadIdx.x == 0) a.stats[r * a.stats_ld + sg] = make_float4(m, d1, dT, sx);
 }
 
@@ -1588,7 +1608,7 @@ hipError_t launch_row_stats(const RowStatsArgs& a, hipStream_t s) {
   dim3 grid(static_cast<unsigned>(a.n_rows));
   const bool sf = a.src_type == DType::F32;
   const bool df = a.dst_type == DType::F32;
-  if (a.segmented && !a.online) {
+  if (a.segmented) {
     const int64_t nseg = row_stats_segments(a.v);
     if (a.stats_ld < nseg) return hipErrorInvalidValue;
     const int64_t blocks = a.n_rows * nseg;
@@ -1601,11 +1621,18 @@ hipError_t launch_row_stats(const RowStatsArgs& a, hipStream_t s) {
                      (a.dst == nullptr ||
                       (df && a.ldd % 4 == 0 && reinterpret_cast<uintptr_t>(a.dst) % 16 == 0));
     if (a.src_splits > 1 && !vec) return hipErrorInvalidValue;
-    if (vec) hipLaunchKernelGGL((row_stats_seg_kernel<float, float, true>), g, dim3(kThreads), 0, s, a, nseg);
-    else if (sf && df) hipLaunchKernelGGL((row_stats_seg_kernel<float, float, false>), g, dim3(kThreads), 0, s, a, nseg);
-    else if (sf) hipLaunchKernelGGL((row_stats_seg_kernel<float, __bf16, false>), g, dim3(kThreads), 0, s, a, nseg);
-    else if (df) hipLaunchKernelGGL((row_stats_seg_kernel<__bf16, float, false>), g, dim3(kThreads), 0, s, a, nseg);
-    else hipLaunchKernelGGL((row_stats_seg_kernel<__bf16, __bf16, false>), g, dim3(kThreads), 0, s, a, nseg);
+#define ORDA_ROWSTATS_SEG(ON)                                                                            \
+  if (vec) hipLaunchKernelGGL((row_stats_seg_kernel<float, float, true, ON>), g, dim3(kThreads), 0, s, a, nseg); \
+  else if (sf && df) hipLaunchKernelGGL((row_stats_seg_kernel<float, float, false, ON>), g, dim3(kThreads), 0, s, a, nseg); \
+  else if (sf) hipLaunchKernelGGL((row_stats_seg_kernel<float, __bf16, false, ON>), g, dim3(kThreads), 0, s, a, nseg); \
+  else if (df) hipLaunchKernelGGL((row_stats_seg_kernel<__bf16, float, false, ON>), g, dim3(kThreads), 0, s, a, nseg); \
+  else hipLaunchKernelGGL((row_stats_seg_kernel<__bf16, __bf16, false, ON>), g, dim3(kThreads), 0, s, a, nseg);
+    if (a.online) {
+      ORDA_ROWSTATS_SEG(true)
+    } else {
+      ORDA_ROWSTATS_SEG(false)
+    }
+#undef ORDA_ROWSTATS_SEG
     return hipGetLastError();
   }
   if (!a.online && a.dst == nullptr) {

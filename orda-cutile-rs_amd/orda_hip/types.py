@@ -68,11 +68,13 @@ class KernelConfig:
     * ``profile == Profile.Debug`` (the precise preset): bf16 inputs run the
       fp32 pipeline; ``profile`` is set by ``from_profile`` (the reference
       keeps only the fields a preset sets, so this field is added);
-    * ``online_softmax``: one-pass row statistics of Precomputed teacher
-      logits that the logits GEMM does not read in its epilogue (fp32
-      inputs, or logits that are unaligned or at a pitch that is not a
-      multiple of 4 (fp32) or 8 (bf16); the chunk-launcher slot takes no
-      config and always uses two passes);
+    * ``online_softmax``: row statistics of Precomputed teacher logits that
+      the logits GEMM does not read in its epilogue (fp32 inputs, or logits
+      that are unaligned or at a pitch that is not a multiple of 4 (fp32) or
+      8 (bf16)) by the online-softmax merge of per-thread partial
+      statistics instead of a segment-wide maximum first (the
+      chunk-launcher slot takes no config and always takes the maximum
+      first);
     * ``fp32_grad_weight_accumulation``, ``max_fused_size``: accepted and
       validated; grad_W always accumulates in fp32.
     """
