@@ -212,14 +212,71 @@ __global__ void widen_targets_kernel(const int32_t* in32, int64_t n, int64_t* ou
   }
 }
 
+// Rows of src (any pitch and alignment) into dst rows of pitch ldd, a
+// multiple of 8 elements, zero past `cols`: one workgroup per (row, 2048
+// columns), eight columns a thread, stored as one (bf16) or two (fp32)
+// 16-byte vectors. (One element per thread with a 64-bit division by the
+// pitch each ran at a quarter of this rate.)
+constexpr int kConvCols = 2048;
 template <typename S, typename D>
-__global__ void convert_rows_kernel(const S* src, int64_t lds, D* dst, int64_t ldd, int64_t rows,
-                                    int64_t cols) {
-  const int64_t total = rows * ldd;
-  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t rr = i / ldd, cc = i % ldd;
-    dst[i] = cc < cols ? static_cast<D>(static_cast<float>(src[rr * lds + cc])) : static_cast<D>(0.f);
+__global__ __launch_bounds__(256) void convert_rows_kernel(const S* src, int64_t lds, D* dst,
+                                                           int64_t ldd, int64_t cols, int64_t cpr) {
+  const int64_t r = blockIdx.x / cpr;
+  const int64_t c0 = (blockIdx.x - r * cpr) * kConvCols + threadIdx.x * 8;
+  if (c0 >= ldd) return;
+  const S* s = src + r * lds + c0;
+  float x[8];
+  // the widest loads the source row's alignment allows (a row at an odd
+  // pitch may start on any boundary)
+  const uintptr_t sa = reinterpret_cast<uintptr_t>(s);
+  if (c0 + 8 <= cols && sa % 16 == 0) {
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int h = 0; h < static_cast<int>(sizeof(S)) * 8 / 16; ++h) {
+      const u4 w = reinterpret_cast<const u4*>(s)[h];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (sizeof(S) == 4) {
+          x[4 * h + i] = __uint_as_float(w[i]);
+        } else {
+          x[2 * i] = __uint_as_float(w[i] << 16);
+          x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+      }
+    }
+  } else if (c0 + 8 <= cols && sa % 8 == 0) {
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int h = 0; h < static_cast<int>(sizeof(S)) * 8 / 8; ++h) {
+      const u2 w = reinterpret_cast<const u2*>(s)[h];
+      if constexpr (sizeof(S) == 4) {
+        x[2 * h] = __uint_as_float(w[0]);
+        x[2 * h + 1] = __uint_as_float(w[1]);
+      } else {
+        x[4 * h] = __uint_as_float(w[0] << 16);
+        x[4 * h + 1] = __uint_as_float(w[0] & 0xffff0000u);
+        x[4 * h + 2] = __uint_as_float(w[1] << 16);
+        x[4 * h + 3] = __uint_as_float(w[1] & 0xffff0000u);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = c0 + i < cols ? static_cast<float>(s[i]) : 0.f;
+  }
+  D* d = dst + r * ldd + c0;
+  if constexpr (sizeof(D) == 4) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    reinterpret_cast<f4*>(d)[0] = f4{x[0], x[1], x[2], x[3]};
+    reinterpret_cast<f4*>(d)[1] = f4{x[4], x[5], x[6], x[7]};
+  } else {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    u4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = __builtin_bit_cast(uint32_t, bf16x2{static_cast<__bf16>(x[2 * i]),
+                                                 static_cast<__bf16>(x[2 * i + 1])});
+    *reinterpret_cast<u4*>(d) = w;
   }
 }
 
@@ -274,19 +331,23 @@ hipError_t launch_widen_targets(const int32_t* in32, int64_t n, int64_t* out64, 
 hipError_t launch_convert_rows(DType st, const void* src, int64_t lds, DType dt, void* dst,
                                int64_t ldd, int64_t rows, int64_t cols, hipStream_t s) {
   if (rows <= 0 || ldd <= 0) return hipSuccess;
-  const dim3 g(grid_for(rows * ldd)), b(256);
+  // dst rows start on 16-byte boundaries and hold whole 8-element vectors
+  if (ldd % 8 != 0 || reinterpret_cast<uintptr_t>(dst) % 16 != 0) return hipErrorInvalidValue;
+  const int64_t cpr = (ldd + kConvCols - 1) / kConvCols;
+  if (rows * cpr > 0x7fffffff) return hipErrorInvalidValue;
+  const dim3 g(static_cast<unsigned>(rows * cpr)), b(256);
   if (st == DType::F32 && dt == DType::F32)
     hipLaunchKernelGGL((convert_rows_kernel<float, float>), g, b, 0, s,
-                       static_cast<const float*>(src), lds, static_cast<float*>(dst), ldd, rows, cols);
+                       static_cast<const float*>(src), lds, static_cast<float*>(dst), ldd, cols, cpr);
   else if (st == DType::F32)
     hipLaunchKernelGGL((convert_rows_kernel<float, __bf16>), g, b, 0, s,
-                       static_cast<const float*>(src), lds, static_cast<__bf16*>(dst), ldd, rows, cols);
+                       static_cast<const float*>(src), lds, static_cast<__bf16*>(dst), ldd, cols, cpr);
   else if (dt == DType::F32)
     hipLaunchKernelGGL((convert_rows_kernel<__bf16, float>), g, b, 0, s,
-                       static_cast<const __bf16*>(src), lds, static_cast<float*>(dst), ldd, rows, cols);
+                       static_cast<const __bf16*>(src), lds, static_cast<float*>(dst), ldd, cols, cpr);
   else
     hipLaunchKernelGGL((convert_rows_kernel<__bf16, __bf16>), g, b, 0, s,
-                       static_cast<const __bf16*>(src), lds, static_cast<__bf16*>(dst), ldd, rows, cols);
+                       static_cast<const __bf16*>(src), lds, static_cast<__bf16*>(dst), ldd, cols, cpr);
   return hipGetLastError();
 }
 
