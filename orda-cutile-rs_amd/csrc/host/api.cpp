@@ -505,11 +505,11 @@ int64_t staged_bytes_per_row(const LossPlan& P, const Inputs& in) {
   // the teacher's fp32 logits, and its bf16 gradient rows with teacher CE
   if (sep_epi) b += logits_pitch(P.v) * (P.w_t > 0.f ? 6 : 4);
   b += 2 * nst * 16 + 2 * 4;   // statistics, label logits
-  if (paired) b += nst * 8 + 16;   // KL partials, row constants
+  b += 16;                         // row constants
+  if (paired) b += nst * 8;        // KL partials
   if (lt == orda::DType::BF16) b += 4 * nst * 4;   // half-tile maxima of both rows
-  // fp32 logits: row constants and the gradient blocks' KL sums
-  if (!paired && lt == orda::DType::F32)
-    b += 16 + (P.kd > 0.f ? orda::row_pass_kl_blocks(P.v) * 16 : 0);
+  // fp32 logits with a KL term: the gradient blocks' KL sums
+  if (!paired && lt == orda::DType::F32 && P.kd > 0.f) b += orda::row_pass_kl_blocks(P.v) * 16;
   // hcat: the hidden rows transposed for grad_W ([h_s; h_t] with a Tied
   // teacher and teacher CE; else the student's, then the Separate teacher's).
   b += (P.mode == ORDA_TEACHER_TIED && P.w_t > 0.f ? 2 * P.h
@@ -580,11 +580,10 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   // by side (LogitStatsArgs::hmax).
   const int64_t hld = 4 * nst;
   float* hmax = lt == DType::BF16 ? static_cast<float*>(ws(c, "hmax", cap * hld * 4)) : nullptr;
-  // Row constants of the chunked row passes (paired bf16 logits, or fp32
-  // logits), and for fp32 logits with a KL term the per-block KL sums.
+  // Row constants of the chunked row passes, and for fp32 logits with a KL
+  // term the per-block KL sums.
   const bool f32_rows = !paired && lt == DType::F32;
-  float4* rconst =
-      paired || t_epi || f32_rows ? static_cast<float4*>(ws(c, "rconst", cap * 16)) : nullptr;
+  float4* rconst = static_cast<float4*>(ws(c, "rconst", cap * 16));
   float4* klpart = f32_rows && P.kd > 0.f
                        ? static_cast<float4*>(ws(c, "klpart", cap * row_pass_kl_blocks(v) * 16))
                        : nullptr;

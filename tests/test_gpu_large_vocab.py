@@ -80,6 +80,16 @@ CASES = {
                                         dict(kd_weight=0.7, temperature=1.0)),
     "precomputed-f32-chunked-v200003": ("precomputed", "f32", 176, 16, 16, 200003,
                                         dict(kd_weight=0.7, temperature=1.0, label_smoothing=0.1)),
+    # bf16 logits without a KL term (stored bf16 relative to their half-tile
+    # maxima, not paired), from 20·2^20 logits per block through the chunked
+    # bf16 pass: student CE alone, with a Separate teacher's CE (its gradient
+    # rows in place beside the student's), with a Precomputed teacher's CE.
+    "tied-bf16-student-ce-only": ("tied", "bf16", 320, 16, 16, 70001,
+                                  dict(kd_weight=0.0, teacher_ce_weight=0.0, label_smoothing=0.1)),
+    "separate-bf16-ce-only": ("separate", "bf16", 300, 16, 24, 70001,
+                              dict(kd_weight=0.0, teacher_ce_weight=0.6, label_smoothing=0.1)),
+    "precomputed-bf16-ce-only": ("precomputed", "bf16", 300, 16, 16, 70001,
+                                 dict(kd_weight=0.0, teacher_ce_weight=0.5)),
 }
 
 
