@@ -115,11 +115,20 @@ int64_t round64(int64_t x) { return (x + 63) / 64 * 64; }
 // row starts on a 128-byte line (the backward GEMMs read these rows in
 // 128-byte K-slabs: at V = 50257 a pitch of round8(V) put every slab across two
 // lines, grad_hidden 0.524 of peak against 0.60, the row pass 0.65 against
-// 0.75), plus 64 when that is a multiple of 1024, so that rows (and the many
-// row streams the row pass and the GEMMs walk in step) do not sit a power of
-// two apart.
-int64_t logits_pitch(int64_t v) {
-  const int64_t p = round64(v);
+// 0.75). fp32 rows: plus 64 when that is a multiple of 1024, so that rows (and
+// the many row streams the row pass and the GEMMs walk in step) do not sit a
+// power of two apart. bf16 rows: further up to 64 past a multiple of 1024,
+// which measured the bf16 row pass (BT = 8192, paired rows, TB/s, two passes)
+// at V = 151936 5.9 against 5.0, at 50257 6.0 against 5.7, at 100000 and 128256
+// 1-2 % faster, at 32000 and 200064 1-3 % slower, elsewhere equal; the
+// backward GEMMs equal. (fp32 rows at V = 32000: the row pass 1.5 % slower,
+// so fp32 keeps the first rule.)
+int64_t logits_pitch(int64_t v, orda::DType lt) {
+  int64_t p = round64(v);
+  if (lt == orda::DType::BF16) {
+    while (p % 1024 != 64) p += 64;
+    return p;
+  }
   return p % 1024 == 0 ? p + 64 : p;
 }
 
@@ -500,10 +509,11 @@ int64_t staged_bytes_per_row(const LossPlan& P, const Inputs& in) {
   const orda::DType lt = logits_dtype(P, paired);
   const int64_t blocks = P.need_teacher && !teacher_logits_direct(P, in) && !sep_epi ? 2 : 1;
   const int64_t nst = orda::gemm_stat_tiles(P.v);
-  int64_t b = blocks * logits_pitch(P.v) *
+  const int64_t ldl = logits_pitch(P.v, lt);
+  int64_t b = blocks * ldl *
               (orda::dtype_size(lt) + (lt == P.dt ? 0 : orda::dtype_size(P.dt)));
   // the teacher's fp32 logits, and its bf16 gradient rows with teacher CE
-  if (sep_epi) b += logits_pitch(P.v) * (P.w_t > 0.f ? 6 : 4);
+  if (sep_epi) b += ldl * (P.w_t > 0.f ? 6 : 4);
   b += 2 * nst * 16 + 2 * 4;   // statistics, label logits
   b += 16;                         // row constants
   if (paired) b += nst * 8;        // KL partials
@@ -539,7 +549,6 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   const int64_t bt = P.bt, v = P.v, h = P.h;
   const DType dt = P.dt;
   const int es = dtype_size(dt);
-  const int64_t ldl = logits_pitch(v);
   const int64_t nst = gemm_stat_tiles(v);
   const int64_t cap = std::min(bt, G * cs);
   const bool tl_direct = teacher_logits_direct(P, in);
@@ -557,6 +566,7 @@ void run_loss(orda_ctx* c, const LossPlan& P, const Inputs& in, orda::ChunkPlan 
   // Precomputed ones in place, or a Separate teacher's from its own GEMM
   const bool t_epi = teacher_beside_gemm(P, in) || sep_epi;
   const DType lt = logits_dtype(P, paired || t_epi);
+  const int64_t ldl = logits_pitch(v, lt);
   void* L = ws(c, "logits", blocks * cap * ldl * dtype_size(lt));
   void* TL = sep_epi ? ws(c, "tlogits", cap * ldl * 4) : nullptr;
   void* TG = sep_epi && P.w_t > 0.f ? ws(c, "tgrad", cap * ldl * es) : nullptr;
