@@ -30,6 +30,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <chrono>
 #include <map>
 #include <memory>
 
@@ -64,6 +65,8 @@ struct orda_ctx {
   std::vector<hipEvent_t> pool;
   double total_ms[ORDA_KERNEL_KINDS] = {};
   int64_t launches[ORDA_KERNEL_KINDS] = {};
+  // Recorded at the end of a call and polled by wait_stream.
+  hipEvent_t done = nullptr;
 };
 
 namespace {
@@ -82,6 +85,26 @@ void hip_check(hipError_t e, const char* what) {
   (void)hipGetLastError();
   if (e == hipErrorOutOfMemory) fail(ORDA_ERR_OOM, "%s: device out of memory", what);
   fail(ORDA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// The end-of-call wait for the context's stream. It polls an event for up
+// to kSpinMicros, then blocks in hipStreamSynchronize: a short call's wait
+// ends sooner after its last operation when polled (Tied BT=256 H=512
+// V=8192 fp32: 0.216 against 0.223 ms per call), and a long call does not
+// hold a host core for its whole duration.
+constexpr int64_t kSpinMicros = 1000;
+
+void wait_stream(orda_ctx* c) {
+  hip_check(hipEventRecord(c->done, c->stream), "hipEventRecord");
+  const auto t0 = std::chrono::steady_clock::now();
+  for (;;) {
+    const hipError_t q = hipEventQuery(c->done);
+    if (q == hipSuccess) return;
+    if (q != hipErrorNotReady) hip_check(q, "hipEventQuery");
+    if (std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(kSpinMicros)) break;
+    __builtin_ia32_pause();
+  }
+  hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
 }
 
 void copy_err(const Error& e, char* err, size_t len) {
@@ -1238,7 +1261,7 @@ void loss_impl(orda_ctx* c, const orda_tensor* sh, const orda_tensor* w, const i
   // The one wait of the call: loss scalars and label status together.
   char* hblk = static_cast<char*>(pinned(c, 64));
   hip_check(hipMemcpyAsync(hblk, scal_blk, 64, hipMemcpyDeviceToHost, c->stream), "read loss");
-  hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  wait_stream(c);
   collect_timing(c);
   float hs[4];
   LabelStatus ls;
@@ -1428,7 +1451,7 @@ void kl_ce_slot(orda_ctx* c, const orda_tensor* logits_chunk, const int32_t* tar
   download(c, kr);
   download(c, cl);
   if (capturing) return;
-  hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  wait_stream(c);
   collect_timing(c);
 }
 
@@ -1499,6 +1522,7 @@ int32_t orda_ctx_create(int32_t device, orda_ctx** out, char* err, size_t err_le
     // reads the inputs, and the null stream waits for it in turn.
     hip_check(hipStreamCreateWithFlags(&c->own, hipStreamDefault), "hipStreamCreate");
     c->stream = c->own;
+    hip_check(hipEventCreateWithFlags(&c->done, hipEventDisableTiming), "hipEventCreate");
     // The no-allocation entry point's scratch address on this device.
     hip_check(orda::noalloc_scratch_init(device), "no-allocation scratch");
     *out = c.release();
@@ -1519,6 +1543,7 @@ void orda_ctx_destroy(orda_ctx* c) {
   }
   for (hipEvent_t e : c->pool) (void)hipEventDestroy(e);
   if (c->pinned) (void)hipHostFree(c->pinned);
+  if (c->done) (void)hipEventDestroy(c->done);
   ws_trim(c);
   if (c->own) (void)hipStreamDestroy(c->own);
   delete c;
@@ -1684,7 +1709,7 @@ int32_t orda_quant_rows_int8(orda_ctx* ctx, const orda_tensor* m, const int64_t*
     if (s && scales->location != ORDA_DEVICE && rows > 0)
       hip_check(hipMemcpyAsync(scales->data, s, rows * 4, hipMemcpyDeviceToHost, c->stream),
                 "download scales");
-    hip_check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    wait_stream(c);
     collect_timing(c);
     return ORDA_OK;
   } catch (const Error& e) {
