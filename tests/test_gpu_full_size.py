@@ -176,3 +176,47 @@ def test_bf16_inputs_beside_fp32_teacher_logits_full_shape(name):
         if r is not None:
             rel[k] = check_grad_device(k, g, r, "bf16")
     print("relative errors:", {k: f"{e:.2e}" for k, e in rel.items()})
+
+
+WIDE = [("tied", "bf16", 8192, 8192), ("tied", "bf16", 16384, 16384),
+        ("separate", "bf16", 8192, 16384), ("tied", "f32", 8192, 8192)]
+
+
+@pytest.mark.parametrize("case", WIDE, ids=[f"{m}-{d}-h{h}-ht{ht}" for m, d, h, ht in WIDE])
+def test_wide_hidden(case):
+    """Model widths of the largest decoders (H = 8192 and 16384; a Separate
+    teacher twice the student's width) at BT = 1024 and a ragged V = 50257,
+    kd 0.5, T 2, label smoothing 0.1, teacher CE, every 13th label ignored:
+    the logits GEMM's K, grad_hidden's N and grad_W's N at their widest,
+    against loss_chunked on the same (bf16-rounded) values on the same GPU;
+    loss terms to 1e-4, gradients to the input dtype's gate."""
+    import torch
+    from torch_reference import loss_chunked
+    assert torch.cuda.is_available(), "GPU tests need a visible GPU"
+    assert H.is_available(), "liborda_hip.so does not see a gfx950 device"
+    torch.backends.cuda.matmul.allow_tf32 = False
+    mode, dt, h, ht = case
+    bt, v = 1024, 50257
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(h + ht)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    s = torch.randn(bt, h, generator=g, device=dev).to(tdt)
+    w = (torch.randn(v, h, generator=g, device=dev) * (0.5 / h ** 0.5)).to(tdt)
+    th = torch.randn(bt, ht, generator=g, device=dev).to(tdt)
+    tw = (torch.randn(v, ht, generator=g, device=dev) * (0.5 / ht ** 0.5)).to(tdt) \
+        if mode == "separate" else None
+    y = torch.randint(0, v, (bt,), generator=g, device=dev)
+    y[::13] = -100
+    opts = LossOptions(kd_weight=0.5, temperature=2.0, label_smoothing=0.1, teacher_ce_weight=1.0)
+    teacher = Teacher.Tied(th) if mode == "tied" else Teacher.Separate(th, tw)
+    print(f"case {mode}-{dt}-h{h}-ht{ht}", flush=True)
+    got = H.distillation_loss(s, w, y, teacher, opts)
+    ref = loss_chunked(s, w, y, mode, th, tw, None, kd=0.5, T=2.0, alpha=0.1, w_t=1.0)
+    for k in ("loss", "student_ce", "teacher_ce", "kl"):
+        check_scalar(k, getattr(got, k), ref[k])
+    for k in ("grad_student_hidden", "grad_weight", "grad_teacher_hidden", "grad_teacher_weight"):
+        gk, rk = getattr(got, k), ref[k]
+        assert (gk is None) == (rk is None), f"{k}: presence differs"
+        if rk is not None:
+            check_grad_device(k, gk, rk, dt)
