@@ -544,7 +544,9 @@ __device__ __forceinline__ TileCoord map_tile(const GemmArgs& g, int64_t t) {
   // read the same strips at the same time, so the MALL serves the repeats
   // and each strip is fetched from HBM once per band (the grouped raster
   // walks an XCD's M-tiles over two passes of N and fetches them twice).
-  // Tiles past the last whole band take the grouped raster.
+  // The same blocks with b = all N-tiles (xn = 1) walk a large bf16 logits
+  // GEMM in M bands (set_band_blocks). Tiles past the last whole band take
+  // the grouped raster.
   if (g.sh_a > 0) {
     const int64_t a = g.sh_a, b = g.sh_b, xn = g.sh_xn, bm = a * (8 / xn), per = a * b;
     const int64_t full = Mv / bm * bm * Nt;   // 8 * per tiles per band
@@ -1796,6 +1798,36 @@ void set_share_blocks(GemmArgs& g) {
   g.sh_xn = static_cast<int>(best_xn);
 }
 
+// M bands for a bf16 logits GEMM whose live rows overflow the MALL. The
+// grouped raster gives each XCD its own group_m M-tiles and walks all N with
+// every XCD on the same N-tiles, so 8 groups of A's rows (M x K) are live at
+// once; past ~192 MB (at K = 8192, 64 M-tiles: 256 MB, the MALL's size) A's
+// strips come from HBM again on every round. Then, while a band of 32
+// M-tiles fits in 128 MB, the rows are walked in such bands (map_tile's
+// block path with b = all N-tiles, xn = 1): each XCD takes 4 of the band's
+// M-tiles and all N, 4 M x 8 N tiles a round (the same 12 strips per stage
+// as the grouped raster), and B (the weight rows) is read once per band.
+// Measured at BT = 8192, V = 128256, H = 8192 (two alternating passes on
+// each of two machines): the logits GEMM at 0.545-0.557 of peak against
+// 0.49-0.52, the call 73.6-74.7 against 75.0-77.9 ms.
+// Not applied where it did not gain: H = 16384 (a 256 MB band, or 128 MB in
+// 2 x 16 blocks with 18 strips a stage: 0.50 against 0.51), H = 5120 (A
+// 168 MB: 0.51 against 0.52), BT = 16384 at H = 4096 (the grouped raster
+// already walks N twice with 128 MB live: equal).
+void set_band_blocks(GemmArgs& g) {
+  constexpr int64_t kBandLive = int64_t{192} << 20, kBandMax = int64_t{128} << 20;
+  if (g.sh_a > 0 || g.epi != GemmEpilogue::Logits || g.in_type != DType::BF16) return;
+  const int64_t Mv = ((g.M + kTile - 1) / kTile) * g.nprob;
+  const int64_t Nt = (g.N + kTile - 1) / kTile;
+  const int64_t strip = int64_t{kTile} * g.K * 2;
+  const int64_t gm = g.group_m > 0 ? g.group_m : 1;
+  const int64_t live = (Mv < 8 * gm ? Mv : 8 * gm) * strip;
+  if (live <= kBandLive || 32 * strip > kBandMax || Mv < 32) return;
+  g.sh_a = 4;
+  g.sh_b = static_cast<int>(Nt);
+  g.sh_xn = 1;
+}
+
 SplitPlan plan_split(const GemmArgs& g) {
   SplitPlan sp{1, g.K, 0, 0, 0};
   if (g.epi == GemmEpilogue::Logits || g.M <= 0 || g.N <= 0 || g.K <= 0) return sp;
@@ -2281,6 +2313,7 @@ hipError_t launch_gemm_impl(const GemmArgs& g, hipStream_t stream, bool whole) {
   const int64_t tiles = ((g.M + kTile - 1) / kTile) * ((g.N + kTile - 1) / kTile) * g.nprob;
   GemmArgs gr = g;
   set_share_blocks(gr);
+  set_band_blocks(gr);
   const SplitPlan sp = plan_split(g);
   if (sp.splits > 1 && g.split_ws != nullptr && g.split_ws_bytes >= sp.bytes) {
     // Partials of every split with the Store epilogue (alpha 1), in C's

@@ -178,25 +178,29 @@ def test_bf16_inputs_beside_fp32_teacher_logits_full_shape(name):
     print("relative errors:", {k: f"{e:.2e}" for k, e in rel.items()})
 
 
-WIDE = [("tied", "bf16", 8192, 8192), ("tied", "bf16", 16384, 16384),
-        ("separate", "bf16", 8192, 16384), ("tied", "f32", 8192, 8192)]
+WIDE = [("tied", "bf16", 1024, 8192, 8192, 50257), ("tied", "bf16", 1024, 16384, 16384, 50257),
+        ("separate", "bf16", 1024, 8192, 16384, 50257), ("tied", "f32", 1024, 8192, 8192, 50257),
+        ("tied", "bf16", 6400, 8192, 8192, 16000)]
 
 
-@pytest.mark.parametrize("case", WIDE, ids=[f"{m}-{d}-h{h}-ht{ht}" for m, d, h, ht in WIDE])
+@pytest.mark.parametrize("case", WIDE, ids=[f"{m}-{d}-bt{bt}-h{h}-ht{ht}-v{v}"
+                                            for m, d, bt, h, ht, v in WIDE])
 def test_wide_hidden(case):
     """Model widths of the largest decoders (H = 8192 and 16384; a Separate
-    teacher twice the student's width) at BT = 1024 and a ragged V = 50257,
-    kd 0.5, T 2, label smoothing 0.1, teacher CE, every 13th label ignored:
-    the logits GEMM's K, grad_hidden's N and grad_W's N at their widest,
-    against loss_chunked on the same (bf16-rounded) values on the same GPU;
-    loss terms to 1e-4, gradients to the input dtype's gate."""
+    teacher twice the student's width) at a ragged V, kd 0.5, T 2, label
+    smoothing 0.1, teacher CE, every 13th label ignored: the logits GEMM's K,
+    grad_hidden's N and grad_W's N at their widest, against loss_chunked on
+    the same (bf16-rounded) values on the same GPU; loss terms to 1e-4,
+    gradients to the input dtype's gate. The last shape puts 50 M-tiles of
+    8192-wide bf16 student and teacher rows (200 MB) into the logits GEMM,
+    which then walks them in a band of 32 M-tiles and the 18 M-tiles past it
+    in the grouped raster."""
     import torch
     from torch_reference import loss_chunked
     assert torch.cuda.is_available(), "GPU tests need a visible GPU"
     assert H.is_available(), "liborda_hip.so does not see a gfx950 device"
     torch.backends.cuda.matmul.allow_tf32 = False
-    mode, dt, h, ht = case
-    bt, v = 1024, 50257
+    mode, dt, bt, h, ht, v = case
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(h + ht)
@@ -210,7 +214,7 @@ def test_wide_hidden(case):
     y[::13] = -100
     opts = LossOptions(kd_weight=0.5, temperature=2.0, label_smoothing=0.1, teacher_ce_weight=1.0)
     teacher = Teacher.Tied(th) if mode == "tied" else Teacher.Separate(th, tw)
-    print(f"case {mode}-{dt}-h{h}-ht{ht}", flush=True)
+    print(f"case {mode}-{dt}-bt{bt}-h{h}-ht{ht}-v{v}", flush=True)
     got = H.distillation_loss(s, w, y, teacher, opts)
     ref = loss_chunked(s, w, y, mode, th, tw, None, kd=0.5, T=2.0, alpha=0.1, w_t=1.0)
     for k in ("loss", "student_ce", "teacher_ce", "kl"):
