@@ -52,6 +52,12 @@ WORKLOADS = {
                                            0.1, 1.0, False),
     "precomputed-4096x4096x65536-bf16": ("precomputed", 4096, 4096, 4096, 65536, "bf16", 0.7,
                                          1.0, 0.0, None, False),
+    # wider decoders (H = 8192 and 16384, V = 128256) with the benchmark's
+    # options, bf16 inputs, no INT8 step
+    "tied-8192x8192x128256-bf16": ("tied", 8192, 8192, 8192, 128256, "bf16", 0.4, 1.5, 0.1, None,
+                                   False),
+    "tied-8192x16384x128256-bf16": ("tied", 8192, 16384, 16384, 128256, "bf16", 0.4, 1.5, 0.1,
+                                    None, False),
 }
 DEFAULT = "tied-8192x4096x131072-bf16-int8"
 
